@@ -1,0 +1,166 @@
+/*
+ * pmoe: MI355X-native (gfx950) kernels for pluggy's Qwen3-MoE sparse FFN block.
+ *
+ * C ABI. Conventions shared by every entry point:
+ *  - Pointers are device pointers (HBM) unless stated; tensors are dense
+ *    row-major. Sizes are element counts.
+ *  - dtype codes: PMOE_F32 (fp32) or PMOE_BF16 (bf16 stored as uint16).
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    asynchronously; no entry point synchronises the host or allocates
+ *    memory. Scratch memory comes from the caller through `workspace`, sized by
+ *    the matching *_workspace_size query.
+ *  - Return 0 on success, a negative PMOE_ERR_* code for a rejected argument,
+ *    or a positive hipError_t from the runtime. pmoe_last_error_string()
+ *    describes the most recent failure of the calling thread.
+ *  - Inputs are never modified (except `logits` of pmoe_router_forward, which
+ *    is an output). Outputs are overwritten, never accumulated into.
+ *  - Requirements: H and I are multiples of 8; 1 <= K <= E <= 1024; K <= 64.
+ *
+ * Citations name the reference function each entry point replaces
+ * (sonnetx/pluggy, paths relative to the repository root).
+ */
+#ifndef PMOE_H
+#define PMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PMOE_API __attribute__((visibility("default")))
+
+enum { PMOE_F32 = 0, PMOE_BF16 = 1 };
+enum {
+  PMOE_OK = 0,
+  PMOE_ERR_INVALID = -1,     /* bad shape, dtype or null pointer */
+  PMOE_ERR_UNSUPPORTED = -2, /* a valid request outside what is built */
+  PMOE_ERR_WORKSPACE = -3    /* workspace smaller than the size query */
+};
+
+PMOE_API const char* pmoe_version(void);
+PMOE_API const char* pmoe_last_error_string(void);
+
+/* ---------------------------------------------------------------- router ---
+ * Replaces Qwen3MoeTopKRouter.forward (pluggy/models/qwen3_moe/qwen3_moe.py:168-178):
+ *   logits = x . W^T (+ logit_bias)  [fp32 arithmetic]
+ *   p = softmax(logits) (fp32); top-k of logits (ties -> lower expert id)
+ *   w = p[top] (/ sum p[top] when norm_topk_prob), written as tw_dtype and fp32.
+ * Also emits the additive aux statistics of load_balancing_loss / router_z_loss
+ * (qwen3_moe.py:285-316) and the per-expert counts of _update_expert_counts
+ * (qwen3_moe.py:417-426): expert_counts[e] (int32), prob_sum[e] = sum_t p[t,e],
+ * lse_sq_sum = sum_t logsumexp(logits[t])^2. Any of the three may be NULL.
+ * x: (T,H) x_dtype; weight: (E,H) w_dtype; logit_bias: (E,) fp32 or NULL;
+ * logits: (T,E) fp32; top_weights: (T,K) tw_dtype; top_indices: (T,K) int64;
+ * top_weights_f32: (T,K) fp32 (kept for the backward). */
+PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t E);
+PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
+                                 const float* logit_bias, int64_t T, int64_t H, int64_t E, int64_t K,
+                                 int norm_topk_prob, float* logits, void* top_weights, int tw_dtype,
+                                 int64_t* top_indices, float* top_weights_f32, int32_t* expert_counts,
+                                 float* prob_sum, float* lse_sq_sum, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/* Autograd of pmoe_router_forward (torch derivatives of qwen3_moe.py:172-177):
+ *   dl = d(top_weights) through renorm/softmax/top-k (+ grad_logits)
+ *   grad_x = dl . W  (x_dtype, overwritten),  grad_weight = dl^T . x (w_dtype).
+ * grad_top_weights (T,K) gw_dtype and grad_logits (T,E) fp32 may be NULL
+ * (zero); grad_x / grad_weight may be NULL (not needed). */
+PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E);
+PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
+                                  const float* logits, const int64_t* top_indices, const float* top_weights_f32,
+                                  const void* grad_top_weights, int gw_dtype, const float* grad_logits, int64_t T,
+                                  int64_t H, int64_t E, int64_t K, int norm_topk_prob, void* grad_x,
+                                  void* grad_weight, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------- permutation ---
+ * Replaces the flatten / argsort(stable) / bincount / cumsum of
+ * _expert_ffn_grouped (pluggy/kernels/moe.py:89-108): a stable counting sort of
+ * the P = T*K pairs q = t*K + k by expert top_indices[q].
+ * counts (E,) int32; offs (E,) int32 inclusive end offsets (moe.py:108);
+ * sorted_pair (P,) int32 (token = sorted_pair / K); inv_pos (P,) int32 with
+ * inv_pos[sorted_pair[p]] = p. Ids outside [0,E) are clamped into range. */
+PMOE_API size_t pmoe_permute_workspace_size(int64_t T, int64_t K, int64_t E);
+PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int64_t E, int32_t* counts,
+                          int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Row gather hidden[sorted_token] (moe.py:104): x_perm[p] = hidden[sorted_pair[p] / K]. */
+PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* sorted_pair, int64_t T, int64_t K,
+                           int64_t H, void* x_perm, void* stream);
+
+/* Grouped gate_up GEMM + SwiGLU (moe.py:113-118, swiglu.py:14-16):
+ * gate_up_out[p] = x_perm[p] . gate_up_proj[e(p)]^T  (P, 2I), rounded to dtype;
+ * mid[p] = silu(gate) * up  (P, I). gate_up_proj: (E, 2I, H). */
+PMOE_API int pmoe_gate_up_swiglu(const void* x_perm, const void* gate_up_proj, const int32_t* offs, int dtype,
+                                 int64_t P, int64_t E, int64_t H, int64_t I, void* gate_up_out, void* mid,
+                                 void* stream);
+
+/* Grouped down GEMM (moe.py:119): y[p] = mid[p] . down_proj[e(p)]^T  (P, H);
+ * down_proj: (E, H, I). y is the unweighted expert output. */
+PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_t* offs, int dtype, int64_t P,
+                            int64_t E, int64_t H, int64_t I, void* y, void* stream);
+
+/* Weighted combine (moe.py:120-123, in gather form, fp32 accumulation, k ascending):
+ * out[t] = sum_k top_weights[t,k] * y[inv_pos[t*K+k]]. */
+PMOE_API int pmoe_combine(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
+                          int64_t T, int64_t K, int64_t H, void* out, void* stream);
+
+/* Backward of pmoe_combine: grad_y[p] = w * grad_out[t]; grad_top_weights[t,k] =
+ * <grad_out[t], y[inv_pos[t*K+k]]>. */
+PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const void* top_weights, int w_dtype,
+                                   const int32_t* inv_pos, int dtype, int64_t T, int64_t K, int64_t H,
+                                   void* grad_y, void* grad_top_weights, void* stream);
+
+/* Backward of pmoe_down_proj and the SwiGLU: grad_gate_up_out = SwiGLU'(gate_up_out) *
+ * (grad_y . down_proj[e]) and grad_down_proj[e] = grad_y_e^T . mid_e (zeros for
+ * an empty expert). Either output may be NULL. */
+PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
+                                     const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
+                                     int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
+                                     void* stream);
+
+/* Backward of the gate_up GEMM: grad_x_perm = grad_gate_up_out . gate_up_proj[e];
+ * grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e. Either output may be NULL. */
+PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
+                                   const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
+                                   void* grad_x_perm, void* grad_gate_up_proj, void* stream);
+
+/* Backward of pmoe_dispatch: grad_hidden[t] = sum_k grad_x_perm[inv_pos[t*K+k]] (fp32 sum). */
+PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, int dtype, int64_t T,
+                                    int64_t K, int64_t H, void* grad_hidden, void* stream);
+
+/* ------------------------------------------------------ whole expert FFN ---
+ * Replaces moe_expert_ffn / _expert_ffn_grouped (pluggy/kernels/moe.py:68-168):
+ * permute, dispatch, gate_up+SwiGLU, down, combine. The saved tensors
+ * (counts, offs, sorted_pair, inv_pos, x_perm, gate_up_out, mid, y) are
+ * caller-owned outputs that pmoe_expert_ffn_backward consumes.
+ * hidden (T,H), top_indices (T,K) int64, top_weights (T,K) w_dtype,
+ * gate_up_proj (E,2I,H), down_proj (E,H,I), out (T,H); all but the
+ * weights/indices in `dtype`. */
+PMOE_API size_t pmoe_expert_ffn_forward_workspace_size(int64_t T, int64_t K, int64_t E);
+PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indices, const void* top_weights,
+                                     int w_dtype, const void* gate_up_proj, const void* down_proj, int dtype,
+                                     int64_t T, int64_t K, int64_t E, int64_t H, int64_t I, void* out,
+                                     int32_t* counts, int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos,
+                                     void* x_perm, void* gate_up_out, void* mid, void* y, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+/* Autograd of pmoe_expert_ffn_forward. Any of grad_hidden, grad_top_weights,
+ * grad_gate_up_proj, grad_down_proj may be NULL. Workspace holds grad_y,
+ * grad_gate_up_out and grad_x_perm. */
+PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype);
+PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weights, int w_dtype,
+                                      const void* gate_up_proj, const void* down_proj, int dtype, int64_t T,
+                                      int64_t K, int64_t E, int64_t H, int64_t I, const int32_t* offs,
+                                      const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
+                                      const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
+                                      void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PMOE_H */

@@ -1,0 +1,26 @@
+"""pluggy_amd: MI355X-native (gfx950) Qwen3-MoE sparse FFN block for pluggy.
+
+Drop-in replacements for the reference block (pluggy/models/qwen3_moe/qwen3_moe.py:152-239)
+and operator (pluggy/kernels/moe.py:127-168), backed by hand-written HIP kernels
+in ``libpmoe.so`` (C ABI in ``include/pmoe.h``).
+"""
+
+from .moe import RouterStats, moe_expert_ffn, router_topk
+from .qwen3_moe import (
+    Qwen3MoeExperts,
+    Qwen3MoeSparseMLP,
+    Qwen3MoeTopKRouter,
+    load_balancing_loss_from_stats,
+    router_z_loss_from_stats,
+)
+
+__all__ = [
+    "Qwen3MoeExperts",
+    "Qwen3MoeSparseMLP",
+    "Qwen3MoeTopKRouter",
+    "RouterStats",
+    "load_balancing_loss_from_stats",
+    "moe_expert_ffn",
+    "router_topk",
+    "router_z_loss_from_stats",
+]

@@ -1,0 +1,474 @@
+// C ABI of pmoe (declared in include/pmoe.h): argument checks, dtype dispatch,
+// workspace carving and the multi-kernel sequences of each entry point.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "../../include/pmoe.h"
+#include "kernels.h"
+
+using namespace pmoe;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return PMOE_OK;
+  return fail((int)e, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define PMOE_TRY(expr, where)                        \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return hip_status(e_, where); \
+  } while (0)
+
+#define PMOE_REQUIRE(cond, ...)                               \
+  do {                                                        \
+    if (!(cond)) return fail(PMOE_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+// Bump allocator over the caller's workspace.
+struct Carver {
+  char* base;
+  size_t used = 0;
+  explicit Carver(void* p) : base(static_cast<char*>(p)) {}
+  template <typename T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base + used);
+    used += align_up(count * sizeof(T));
+    return p;
+  }
+};
+
+bool dtype_ok(int d) { return d == PMOE_F32 || d == PMOE_BF16; }
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kRouterRowsPerBlock = 16;
+constexpr int kRouterSplitChunk = 512;
+constexpr int64_t kMaxIndex = 0x7fffffffLL;
+
+int64_t router_blocks(int64_t T) { return (T + kRouterRowsPerBlock - 1) / kRouterRowsPerBlock; }
+int64_t router_splits(int64_t T) { return std::max<int64_t>(1, (T + kRouterSplitChunk - 1) / kRouterSplitChunk); }
+int64_t ldl_of(int64_t E) { return (E + 7) / 8 * 8; }
+
+int check_moe_dims(int64_t T, int64_t K, int64_t E, int64_t H, int64_t I) {
+  PMOE_REQUIRE(T >= 0 && H > 0 && E > 0 && K > 0, "sizes must be positive (T=%lld H=%lld E=%lld K=%lld)",
+               (long long)T, (long long)H, (long long)E, (long long)K);
+  PMOE_REQUIRE(K <= E, "top_k=%lld exceeds num_experts=%lld", (long long)K, (long long)E);
+  PMOE_REQUIRE(E <= 1024, "num_experts=%lld > 1024 is not supported", (long long)E);
+  PMOE_REQUIRE(K <= 64, "top_k=%lld > 64 is not supported", (long long)K);
+  PMOE_REQUIRE(H % 8 == 0, "hidden size %lld must be a multiple of 8", (long long)H);
+  PMOE_REQUIRE(I >= 0 && I % 8 == 0, "moe intermediate size %lld must be a multiple of 8", (long long)I);
+  PMOE_REQUIRE(T * K <= kMaxIndex && T * K * std::max<int64_t>(H, 2 * I) <= (int64_t)1 << 40,
+               "problem too large (T*K=%lld)", (long long)(T * K));
+  return PMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+PMOE_API const char* pmoe_version(void) { return "pmoe 0.1.0 gfx950"; }
+PMOE_API const char* pmoe_last_error_string(void) { return g_err; }
+
+// ------------------------------------------------------------------ router
+
+PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t E) {
+  const int64_t nb = router_blocks(T);
+  return align_up(nb * E * sizeof(float)) + align_up(nb * E * sizeof(int)) + align_up(nb * sizeof(float));
+}
+
+PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
+                                 const float* logit_bias, int64_t T, int64_t H, int64_t E, int64_t K,
+                                 int norm_topk_prob, float* logits, void* top_weights, int tw_dtype,
+                                 int64_t* top_indices, float* top_weights_f32, int32_t* expert_counts,
+                                 float* prob_sum, float* lse_sq_sum, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(tw_dtype), "unknown dtype code");
+  PMOE_REQUIRE(T == 0 || (x && weight && logits && top_weights && top_indices && top_weights_f32),
+               "router_forward: null tensor");
+  const size_t need = pmoe_router_forward_workspace_size(T, E);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(PMOE_ERR_WORKSPACE, "router_forward: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const int t = (int)T, h = (int)H, e = (int)E, k = (int)K;
+  if (T > 0) {
+    hipError_t st;
+    if (x_dtype == PMOE_BF16 && w_dtype == PMOE_F32)
+      st = router_logits_gemm<bf16_t, float>((const bf16_t*)x, (const float*)weight, t, h, e, logits, s);
+    else if (x_dtype == PMOE_BF16)
+      st = router_logits_gemm<bf16_t, bf16_t>((const bf16_t*)x, (const bf16_t*)weight, t, h, e, logits, s);
+    else if (w_dtype == PMOE_F32)
+      st = router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s);
+    else
+      st = router_logits_gemm<float, bf16_t>((const float*)x, (const bf16_t*)weight, t, h, e, logits, s);
+    PMOE_TRY(st, "router logits GEMM");
+  }
+  Carver cv(workspace);
+  const int64_t nb = router_blocks(T);
+  float* blk_psum = cv.take<float>(nb * E);
+  int* blk_cnt = cv.take<int>(nb * E);
+  float* blk_lse2 = cv.take<float>(nb);
+  if (T > 0) {
+    hipError_t st =
+        tw_dtype == PMOE_BF16
+            ? router_topk<bf16_t>(logits, logit_bias, t, e, k, norm_topk_prob, (bf16_t*)top_weights, top_indices,
+                                  top_weights_f32, blk_psum, blk_lse2, blk_cnt, kRouterRowsPerBlock, s)
+            : router_topk<float>(logits, logit_bias, t, e, k, norm_topk_prob, (float*)top_weights, top_indices,
+                                 top_weights_f32, blk_psum, blk_lse2, blk_cnt, kRouterRowsPerBlock, s);
+    PMOE_TRY(st, "router top-k");
+  }
+  if (expert_counts || prob_sum || lse_sq_sum)
+    PMOE_TRY(router_stats_reduce(blk_psum, blk_lse2, blk_cnt, (int)nb, e, prob_sum, lse_sq_sum, expert_counts, s),
+             "router statistics");
+  return PMOE_OK;
+}
+
+PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E) {
+  return align_up(T * ldl_of(E) * sizeof(float)) + align_up(router_splits(T) * E * H * sizeof(float));
+}
+
+PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
+                                  const float* logits, const int64_t* top_indices, const float* top_weights_f32,
+                                  const void* grad_top_weights, int gw_dtype, const float* grad_logits, int64_t T,
+                                  int64_t H, int64_t E, int64_t K, int norm_topk_prob, void* grad_x,
+                                  void* grad_weight, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(gw_dtype), "unknown dtype code");
+  PMOE_REQUIRE(T == 0 || (x && weight && logits && top_indices && top_weights_f32),
+               "router_backward: null tensor");
+  const size_t need = pmoe_router_backward_workspace_size(T, H, E);
+  if (workspace_bytes < need || !workspace)
+    return fail(PMOE_ERR_WORKSPACE, "router_backward: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const int t = (int)T, h = (int)H, e = (int)E, k = (int)K;
+  const int ldl = (int)ldl_of(E);
+  Carver cv(workspace);
+  float* dl = cv.take<float>((size_t)T * ldl);
+  float* partial = cv.take<float>((size_t)router_splits(T) * E * H);
+  if (T > 0) {
+    hipError_t st = gw_dtype == PMOE_BF16
+                        ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32,
+                                                 (const bf16_t*)grad_top_weights, grad_logits, t, e, k,
+                                                 norm_topk_prob, dl, ldl, s)
+                        : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
+                                                grad_logits, t, e, k, norm_topk_prob, dl, ldl, s);
+    PMOE_TRY(st, "router dlogits");
+  }
+  if (grad_x && T > 0) {
+    hipError_t st;
+    if (x_dtype == PMOE_BF16 && w_dtype == PMOE_F32)
+      st = router_dx_gemm<bf16_t, float>(dl, ldl, (const float*)weight, t, h, e, (bf16_t*)grad_x, s);
+    else if (x_dtype == PMOE_BF16)
+      st = router_dx_gemm<bf16_t, bf16_t>(dl, ldl, (const bf16_t*)weight, t, h, e, (bf16_t*)grad_x, s);
+    else if (w_dtype == PMOE_F32)
+      st = router_dx_gemm<float, float>(dl, ldl, (const float*)weight, t, h, e, (float*)grad_x, s);
+    else
+      st = router_dx_gemm<float, bf16_t>(dl, ldl, (const bf16_t*)weight, t, h, e, (float*)grad_x, s);
+    PMOE_TRY(st, "router dx GEMM");
+  }
+  if (grad_weight) {
+    const int splits = (int)router_splits(T);
+    if (T > 0) {
+      hipError_t st = x_dtype == PMOE_BF16
+                          ? router_dw_gemm<bf16_t>(dl, ldl, (const bf16_t*)x, t, h, e, kRouterSplitChunk, partial, s)
+                          : router_dw_gemm<float>(dl, ldl, (const float*)x, t, h, e, kRouterSplitChunk, partial, s);
+      PMOE_TRY(st, "router dW GEMM");
+    } else {
+      PMOE_TRY(hipMemsetAsync(partial, 0, (size_t)E * H * sizeof(float), s), "router dW zero");
+    }
+    const int used = T > 0 ? splits : 1;
+    hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(partial, used, E * H, (bf16_t*)grad_weight, s)
+                                         : reduce_partials<float>(partial, used, E * H, (float*)grad_weight, s);
+    PMOE_TRY(st, "router dW reduce");
+  }
+  return PMOE_OK;
+}
+
+// ------------------------------------------------------------- permutation
+
+PMOE_API size_t pmoe_permute_workspace_size(int64_t T, int64_t K, int64_t E) {
+  return align_up(std::max<int64_t>(1, permute_chunks(T * K)) * E * sizeof(int32_t));
+}
+
+PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int64_t E, int32_t* counts,
+                          int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, E, 8, 0)) return rc;
+  PMOE_REQUIRE(counts && offs && (T == 0 || (top_indices && sorted_pair && inv_pos)), "permute: null tensor");
+  const size_t need = pmoe_permute_workspace_size(T, K, E);
+  if (workspace_bytes < need || !workspace)
+    return fail(PMOE_ERR_WORKSPACE, "permute: workspace %zu < %zu bytes", workspace_bytes, need);
+  PMOE_TRY(permute_pairs(top_indices, (int)T, (int)K, (int)E, counts, offs, sorted_pair, inv_pos,
+                         static_cast<int32_t*>(workspace), kPermuteChunk, as_stream(stream)),
+           "permute");
+  return PMOE_OK;
+}
+
+PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* sorted_pair, int64_t T, int64_t K,
+                           int64_t H, void* x_perm, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(hidden && sorted_pair && x_perm, "dispatch: null tensor");
+  const int P = (int)(T * K);
+  hipError_t st = dtype == PMOE_BF16
+                      ? dispatch_rows<bf16_t>((const bf16_t*)hidden, sorted_pair, P, (int)K, (int)H, (bf16_t*)x_perm,
+                                              as_stream(stream))
+                      : dispatch_rows<float>((const float*)hidden, sorted_pair, P, (int)K, (int)H, (float*)x_perm,
+                                             as_stream(stream));
+  return hip_status(st, "dispatch");
+}
+
+PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, int dtype, int64_t T,
+                                    int64_t K, int64_t H, void* grad_hidden, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(grad_x_perm && inv_pos && grad_hidden, "dispatch_backward: null tensor");
+  hipError_t st = dtype == PMOE_BF16
+                      ? dispatch_rows_bwd<bf16_t>((const bf16_t*)grad_x_perm, inv_pos, (int)T, (int)K, (int)H,
+                                                  (bf16_t*)grad_hidden, as_stream(stream))
+                      : dispatch_rows_bwd<float>((const float*)grad_x_perm, inv_pos, (int)T, (int)K, (int)H,
+                                                 (float*)grad_hidden, as_stream(stream));
+  return hip_status(st, "dispatch_backward");
+}
+
+// ------------------------------------------------------------ expert GEMMs
+
+PMOE_API int pmoe_gate_up_swiglu(const void* x_perm, const void* gate_up_proj, const int32_t* offs, int dtype,
+                                 int64_t P, int64_t E, int64_t H, int64_t I, void* gate_up_out, void* mid,
+                                 void* stream) {
+  if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_swiglu: bad dtype or I");
+  if (P == 0) return PMOE_OK;
+  PMOE_REQUIRE(x_perm && gate_up_proj && offs && gate_up_out && mid, "gate_up_swiglu: null tensor");
+  hipStream_t s = as_stream(stream);
+  hipError_t st = dtype == PMOE_BF16
+                      ? gate_up_swiglu_fwd<bf16_t>((const bf16_t*)x_perm, (const bf16_t*)gate_up_proj, offs, (int)P,
+                                                   (int)E, (int)H, (int)I, (bf16_t*)gate_up_out, (bf16_t*)mid, s)
+                      : gate_up_swiglu_fwd<float>((const float*)x_perm, (const float*)gate_up_proj, offs, (int)P,
+                                                  (int)E, (int)H, (int)I, (float*)gate_up_out, (float*)mid, s);
+  return hip_status(st, "gate_up_swiglu");
+}
+
+PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_t* offs, int dtype, int64_t P,
+                            int64_t E, int64_t H, int64_t I, void* y, void* stream) {
+  if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj: bad dtype or I");
+  if (P == 0) return PMOE_OK;
+  PMOE_REQUIRE(mid && down_proj && offs && y, "down_proj: null tensor");
+  hipStream_t s = as_stream(stream);
+  hipError_t st = dtype == PMOE_BF16 ? down_fwd<bf16_t>((const bf16_t*)mid, (const bf16_t*)down_proj, offs, (int)P,
+                                                        (int)E, (int)H, (int)I, (bf16_t*)y, s)
+                                     : down_fwd<float>((const float*)mid, (const float*)down_proj, offs, (int)P,
+                                                       (int)E, (int)H, (int)I, (float*)y, s);
+  return hip_status(st, "down_proj");
+}
+
+PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
+                                     const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
+                                     int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
+                                     void* stream) {
+  if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj_backward: bad dtype or I");
+  PMOE_REQUIRE(offs && (P == 0 || grad_y), "down_proj_backward: null tensor");
+  hipStream_t s = as_stream(stream);
+  const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
+  if (grad_gate_up_out && P > 0) {
+    PMOE_REQUIRE(down_proj && gate_up_out, "down_proj_backward: null tensor");
+    hipError_t st =
+        dtype == PMOE_BF16
+            ? down_dgrad_swiglu_bwd<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)down_proj,
+                                            (const bf16_t*)gate_up_out, offs, p, e, h, i, (bf16_t*)grad_gate_up_out, s)
+            : down_dgrad_swiglu_bwd<float>((const float*)grad_y, (const float*)down_proj, (const float*)gate_up_out,
+                                           offs, p, e, h, i, (float*)grad_gate_up_out, s);
+    PMOE_TRY(st, "down dgrad");
+  }
+  if (grad_down_proj) {
+    PMOE_REQUIRE(P == 0 || mid, "down_proj_backward: null mid");
+    hipError_t st = dtype == PMOE_BF16 ? down_wgrad<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h,
+                                                            i, (bf16_t*)grad_down_proj, s)
+                                       : down_wgrad<float>((const float*)grad_y, (const float*)mid, offs, p, e, h, i,
+                                                           (float*)grad_down_proj, s);
+    PMOE_TRY(st, "down wgrad");
+  }
+  return PMOE_OK;
+}
+
+PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
+                                   const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
+                                   void* grad_x_perm, void* grad_gate_up_proj, void* stream) {
+  if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_backward: bad dtype or I");
+  PMOE_REQUIRE(offs && (P == 0 || grad_gate_up_out), "gate_up_backward: null tensor");
+  hipStream_t s = as_stream(stream);
+  const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
+  if (grad_x_perm && P > 0) {
+    PMOE_REQUIRE(gate_up_proj, "gate_up_backward: null weight");
+    hipError_t st = dtype == PMOE_BF16
+                        ? gate_up_dgrad<bf16_t>((const bf16_t*)grad_gate_up_out, (const bf16_t*)gate_up_proj, offs, p,
+                                                e, h, i, (bf16_t*)grad_x_perm, s)
+                        : gate_up_dgrad<float>((const float*)grad_gate_up_out, (const float*)gate_up_proj, offs, p, e,
+                                               h, i, (float*)grad_x_perm, s);
+    PMOE_TRY(st, "gate_up dgrad");
+  }
+  if (grad_gate_up_proj) {
+    PMOE_REQUIRE(P == 0 || x_perm, "gate_up_backward: null x_perm");
+    hipError_t st = dtype == PMOE_BF16
+                        ? gate_up_wgrad<bf16_t>((const bf16_t*)grad_gate_up_out, (const bf16_t*)x_perm, offs, p, e, h,
+                                                i, (bf16_t*)grad_gate_up_proj, s)
+                        : gate_up_wgrad<float>((const float*)grad_gate_up_out, (const float*)x_perm, offs, p, e, h, i,
+                                               (float*)grad_gate_up_proj, s);
+    PMOE_TRY(st, "gate_up wgrad");
+  }
+  return PMOE_OK;
+}
+
+// ---------------------------------------------------------------- combine
+
+PMOE_API int pmoe_combine(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
+                          int64_t T, int64_t K, int64_t H, void* out, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(y && top_weights && inv_pos && out, "combine: null tensor");
+  hipStream_t s = as_stream(stream);
+  const int t = (int)T, k = (int)K, h = (int)H;
+  hipError_t st;
+  if (dtype == PMOE_BF16)
+    st = w_dtype == PMOE_BF16
+             ? combine_rows<bf16_t, bf16_t>((const bf16_t*)y, (const bf16_t*)top_weights, inv_pos, t, k, h,
+                                            (bf16_t*)out, s)
+             : combine_rows<bf16_t, float>((const bf16_t*)y, (const float*)top_weights, inv_pos, t, k, h,
+                                           (bf16_t*)out, s);
+  else
+    st = w_dtype == PMOE_BF16 ? combine_rows<float, bf16_t>((const float*)y, (const bf16_t*)top_weights, inv_pos, t,
+                                                            k, h, (float*)out, s)
+                              : combine_rows<float, float>((const float*)y, (const float*)top_weights, inv_pos, t, k,
+                                                           h, (float*)out, s);
+  return hip_status(st, "combine");
+}
+
+PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const void* top_weights, int w_dtype,
+                                   const int32_t* inv_pos, int dtype, int64_t T, int64_t K, int64_t H,
+                                   void* grad_y, void* grad_top_weights, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(grad_out && y && top_weights && inv_pos && grad_y && grad_top_weights,
+               "combine_backward: null tensor");
+  hipStream_t s = as_stream(stream);
+  const int t = (int)T, k = (int)K, h = (int)H;
+  hipError_t st;
+  if (dtype == PMOE_BF16)
+    st = w_dtype == PMOE_BF16
+             ? combine_rows_bwd<bf16_t, bf16_t>((const bf16_t*)grad_out, (const bf16_t*)y,
+                                                (const bf16_t*)top_weights, inv_pos, t, k, h, (bf16_t*)grad_y,
+                                                (bf16_t*)grad_top_weights, s)
+             : combine_rows_bwd<bf16_t, float>((const bf16_t*)grad_out, (const bf16_t*)y, (const float*)top_weights,
+                                               inv_pos, t, k, h, (bf16_t*)grad_y, (float*)grad_top_weights, s);
+  else
+    st = w_dtype == PMOE_BF16
+             ? combine_rows_bwd<float, bf16_t>((const float*)grad_out, (const float*)y, (const bf16_t*)top_weights,
+                                               inv_pos, t, k, h, (float*)grad_y, (bf16_t*)grad_top_weights, s)
+             : combine_rows_bwd<float, float>((const float*)grad_out, (const float*)y, (const float*)top_weights,
+                                              inv_pos, t, k, h, (float*)grad_y, (float*)grad_top_weights, s);
+  return hip_status(st, "combine_backward");
+}
+
+// ------------------------------------------------------- whole expert FFN
+
+PMOE_API size_t pmoe_expert_ffn_forward_workspace_size(int64_t T, int64_t K, int64_t E) {
+  return pmoe_permute_workspace_size(T, K, E);
+}
+
+PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indices, const void* top_weights,
+                                     int w_dtype, const void* gate_up_proj, const void* down_proj, int dtype,
+                                     int64_t T, int64_t K, int64_t E, int64_t H, int64_t I, void* out,
+                                     int32_t* counts, int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos,
+                                     void* x_perm, void* gate_up_out, void* mid, void* y, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
+  PMOE_REQUIRE(I > 0, "expert_ffn_forward: I must be positive");
+  if (int rc = pmoe_permute(top_indices, T, K, E, counts, offs, sorted_pair, inv_pos, workspace, workspace_bytes,
+                            stream))
+    return rc;
+  if (T == 0) return PMOE_OK;
+  const int64_t P = T * K;
+  if (int rc = pmoe_dispatch(hidden, dtype, sorted_pair, T, K, H, x_perm, stream)) return rc;
+  if (int rc = pmoe_gate_up_swiglu(x_perm, gate_up_proj, offs, dtype, P, E, H, I, gate_up_out, mid, stream))
+    return rc;
+  if (int rc = pmoe_down_proj(mid, down_proj, offs, dtype, P, E, H, I, y, stream)) return rc;
+  return pmoe_combine(y, top_weights, w_dtype, inv_pos, dtype, T, K, H, out, stream);
+}
+
+PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype) {
+  const size_t es = dtype == PMOE_BF16 ? 2 : 4;
+  const int64_t P = T * K;
+  return align_up((size_t)P * H * es) + align_up((size_t)P * 2 * I * es);
+}
+
+PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weights, int w_dtype,
+                                      const void* gate_up_proj, const void* down_proj, int dtype, int64_t T,
+                                      int64_t K, int64_t E, int64_t H, int64_t I, const int32_t* offs,
+                                      const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
+                                      const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
+                                      void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
+  (void)sorted_pair;
+  const size_t need = pmoe_expert_ffn_backward_workspace_size(T, K, H, I, dtype);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(PMOE_ERR_WORKSPACE, "expert_ffn_backward: workspace %zu < %zu bytes", workspace_bytes, need);
+  const int64_t P = T * K;
+  const size_t es = dtype == PMOE_BF16 ? 2 : 4;
+  Carver cv(workspace);
+  char* grad_y = cv.take<char>((size_t)P * H * es);
+  char* grad_gu = cv.take<char>((size_t)P * 2 * I * es);
+  hipStream_t s = as_stream(stream);
+  if (T == 0) {
+    if (grad_gate_up_proj) PMOE_TRY(hipMemsetAsync(grad_gate_up_proj, 0, (size_t)E * 2 * I * H * es, s), "zero");
+    if (grad_down_proj) PMOE_TRY(hipMemsetAsync(grad_down_proj, 0, (size_t)E * H * I * es, s), "zero");
+    return PMOE_OK;
+  }
+  // 1. combine backward: grad_y and grad_top_weights. grad_y is needed for any
+  //    other output; grad_top_weights goes to a scratch slot when not requested.
+  void* gtw = grad_top_weights;
+  if (!gtw) gtw = grad_gu;  // grad_gu is written later; P weights fit in P*2I elements
+  if (int rc = pmoe_combine_backward(grad_out, y, top_weights, w_dtype, inv_pos, dtype, T, K, H, grad_y, gtw, stream))
+    return rc;
+  // 2. down GEMM backward (dgrad fused with SwiGLU backward, then wgrad)
+  void* ggu = (grad_hidden || grad_gate_up_proj) ? grad_gu : nullptr;
+  if (int rc = pmoe_down_proj_backward(grad_y, mid, gate_up_out, down_proj, offs, dtype, P, E, H, I, ggu,
+                                       grad_down_proj, stream))
+    return rc;
+  // 3. gate_up GEMM backward; grad_x_perm reuses grad_y (consumed above, same stream)
+  void* gxp = grad_hidden ? grad_y : nullptr;
+  if (ggu) {
+    if (int rc = pmoe_gate_up_backward(grad_gu, x_perm, gate_up_proj, offs, dtype, P, E, H, I, gxp,
+                                       grad_gate_up_proj, stream))
+      return rc;
+  }
+  // 4. dispatch backward
+  if (grad_hidden) return pmoe_dispatch_backward(grad_y, inv_pos, dtype, T, K, H, grad_hidden, stream);
+  return PMOE_OK;
+}
+
+}  // extern "C"

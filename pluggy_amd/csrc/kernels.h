@@ -1,0 +1,76 @@
+// Internal launchers of the pmoe kernels (C++; the C ABI lives in api.hip).
+// Every launcher enqueues on `s`, allocates nothing and never synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace pmoe {
+
+// ---- grouped expert GEMMs (gemm.hip). T = bf16_t or float (activation dtype).
+// offs: (E,) int32 inclusive end row of each expert in the sorted order.
+template <typename T>
+hipError_t gate_up_swiglu_fwd(const T* x_perm, const T* w_gu, const int32_t* offs, int P, int E, int H, int I,
+                              T* gu_out, T* mid, hipStream_t s);
+template <typename T>
+hipError_t down_fwd(const T* mid, const T* w_dn, const int32_t* offs, int P, int E, int H, int I, T* y,
+                    hipStream_t s);
+template <typename T>
+hipError_t down_dgrad_swiglu_bwd(const T* dy, const T* w_dn, const T* gu_out, const int32_t* offs, int P, int E,
+                                 int H, int I, T* dgu, hipStream_t s);
+template <typename T>
+hipError_t down_wgrad(const T* dy, const T* mid, const int32_t* offs, int P, int E, int H, int I, T* dw_dn,
+                      hipStream_t s);
+template <typename T>
+hipError_t gate_up_dgrad(const T* dgu, const T* w_gu, const int32_t* offs, int P, int E, int H, int I, T* dx_perm,
+                         hipStream_t s);
+template <typename T>
+hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int P, int E, int H, int I, T* dw_gu,
+                         hipStream_t s);
+
+// ---- router GEMMs in fp32 arithmetic (gemm.hip). TX: x dtype, TW: router weight dtype.
+template <typename TX, typename TW>
+hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, float* logits, hipStream_t s);
+// dx = dl . W   (dl: (T, ldl) fp32, columns >= E are ignored)
+template <typename TX, typename TW>
+hipError_t router_dx_gemm(const float* dl, int ldl, const TW* w, int T, int H, int E, TX* dx, hipStream_t s);
+// partial[g] = dl[chunk g]^T . x[chunk g]  -> (splits, E, H) fp32
+template <typename TX>
+hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, int E, int split_chunk,
+                          float* partial, hipStream_t s);
+
+// ---- routing, permutation and row movement (route.hip).
+template <typename TW>
+hipError_t router_topk(float* logits, const float* logit_bias, int T, int E, int K, int norm_topk,
+                       TW* top_w, int64_t* top_idx, float* top_w_f32, float* blk_psum, float* blk_lse2,
+                       int* blk_counts, int rows_per_block, hipStream_t s);
+hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
+                               float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s);
+template <typename TG>
+hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
+                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, int ldl,
+                          hipStream_t s);
+template <typename TO>
+hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s);
+
+hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
+                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s);
+template <typename T>
+hipError_t dispatch_rows(const T* x, const int32_t* sorted_pair, int P, int K, int H, T* x_perm, hipStream_t s);
+template <typename T, typename TW>
+hipError_t combine_rows(const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H, T* out,
+                        hipStream_t s);
+template <typename T, typename TW>
+hipError_t combine_rows_bwd(const T* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H,
+                            T* dy, TW* dw, hipStream_t s);
+template <typename T>
+hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, int T_, int K, int H, T* dx,
+                             hipStream_t s);
+
+// Chunk size (pairs) of the permutation histogram and the workspace it needs.
+constexpr int kPermuteChunk = 2048;
+inline int64_t permute_chunks(int64_t P) { return (P + kPermuteChunk - 1) / kPermuteChunk; }
+
+}  // namespace pmoe

@@ -1,0 +1,544 @@
+// Router top-k, routing statistics, the stable expert permutation, and the
+// HBM-bound row movers (dispatch gather, weighted combine and their backward).
+#include <limits.h>
+
+#include <algorithm>
+
+#include "kernels.h"
+
+namespace pmoe {
+
+namespace {
+
+__device__ __forceinline__ float nan_to_neg_inf(float v) { return v != v ? -INFINITY : v; }
+
+// Ranking key of top-k: larger logit first, equal logits -> lower expert id.
+__device__ __forceinline__ bool better(float v, int e, float bv, int be) {
+  return v > bv || (v == bv && e < be);
+}
+
+// One wave per row. EPL = experts per lane (E <= 64 * EPL).
+template <int EPL, typename TW>
+__global__ __launch_bounds__(256) void router_topk_kernel(float* __restrict__ logits, const float* __restrict__ bias,
+                                                          int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
+                                                          int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
+                                                          float* __restrict__ blk_psum, float* __restrict__ blk_lse2,
+                                                          int* __restrict__ blk_counts, int rows_per_block) {
+  extern __shared__ float sh[];  // [4][E] psum partials, then [E] int counts, then [4] lse2
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* s_psum = sh;
+  int* s_cnt = reinterpret_cast<int*>(sh + 4 * E);
+  float* s_lse2 = sh + 5 * E;
+  for (int e = tid; e < E; e += blockDim.x) s_cnt[e] = 0;
+  __syncthreads();
+
+  float psum[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) psum[j] = 0.0f;
+  float lse2 = 0.0f;
+
+  const int row0 = blockIdx.x * rows_per_block;
+  const int row1 = min(T, row0 + rows_per_block);
+  for (int row = row0 + wave; row < row1; row += 4) {
+    float v[EPL];
+    float* lrow = logits + (int64_t)row * E;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      float x = -INFINITY;
+      if (e < E) {
+        x = lrow[e];
+        if (bias != nullptr) { x += bias[e]; lrow[e] = x; }
+      }
+      v[j] = x;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
+    m = wave_max(m);
+    float ex[EPL];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      ex[j] = (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+      s += ex[j];
+    }
+    s = wave_sum(s);
+    const float inv_s = 1.0f / s;
+    const float lse = m + logf(s);
+    lse2 += lse * lse;  // every lane holds the same value; lane 0's copy is used
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) psum[j] += ex[j] * inv_s;
+
+    // top-k by (logit desc, id asc); NaN ranks as -inf so a valid id is always found
+    float key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) key[j] = nan_to_neg_inf(v[j]);
+    unsigned selmask = 0;
+    float p_sel = 0.0f, psum_sel = 0.0f;
+    int e_sel = 0;
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int be = INT_MAX;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !((selmask >> j) & 1u) && better(key[j], e, bv, be)) { bv = key[j]; be = e; }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, kWave);
+        const int oe = __shfl_xor(be, o, kWave);
+        if (better(ov, oe, bv, be)) { bv = ov; be = oe; }
+      }
+      if ((be & 63) == lane) selmask |= 1u << (be >> 6);
+      const float pk = expf(bv - m) * inv_s;
+      psum_sel += pk;
+      if (lane == k) { p_sel = pk; e_sel = be; }
+    }
+    if (lane < K) {
+      const float w = norm_topk ? p_sel / psum_sel : p_sel;
+      const int64_t o = (int64_t)row * K + lane;
+      top_idx[o] = e_sel;
+      top_w_f32[o] = w;
+      store_scalar<TW>(top_w + o, w);
+      atomicAdd(&s_cnt[e_sel], 1);
+    }
+  }
+  // fixed-order block reduction of the statistics (deterministic)
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) s_psum[wave * E + e] = psum[j];
+  }
+  if (lane == 0) s_lse2[wave] = lse2;
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {
+    blk_psum[(int64_t)blockIdx.x * E + e] = ((s_psum[e] + s_psum[E + e]) + s_psum[2 * E + e]) + s_psum[3 * E + e];
+    blk_counts[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+  }
+  if (tid == 0) blk_lse2[blockIdx.x] = ((s_lse2[0] + s_lse2[1]) + s_lse2[2]) + s_lse2[3];
+}
+
+__global__ void router_stats_reduce_kernel(const float* blk_psum, const float* blk_lse2, const int* blk_counts,
+                                           int nblk, int E, float* prob_sum, float* lse_sq_sum, int32_t* counts) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float ps = 0.0f;
+    int c = 0;
+    for (int b = 0; b < nblk; ++b) {
+      ps += blk_psum[(int64_t)b * E + e];
+      c += blk_counts[(int64_t)b * E + e];
+    }
+    if (prob_sum) prob_sum[e] = ps;
+    if (counts) counts[e] = c;
+  }
+  if (threadIdx.x == 0 && lse_sq_sum) {
+    float l = 0.0f;
+    for (int b = 0; b < nblk; ++b) l += blk_lse2[b];
+    *lse_sq_sum = l;
+  }
+}
+
+// d(loss)/d(logits) for one row per wave. See the closed forms in kernels.h users.
+template <int EPL, typename TG>
+__global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __restrict__ logits,
+                                                             const int64_t* __restrict__ top_idx,
+                                                             const float* __restrict__ top_w_f32,
+                                                             const TG* __restrict__ grad_w,
+                                                             const float* __restrict__ grad_logits, int T, int E,
+                                                             int K, int norm_topk, float* __restrict__ dl, int ldl) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const int64_t* irow = top_idx + (int64_t)row * K;
+  const float* wrow = top_w_f32 + (int64_t)row * K;
+  // inner = sum_k w_k G_k, in slot order
+  float inner = 0.0f;
+  if (grad_w != nullptr)
+    for (int k = 0; k < K; ++k) inner += wrow[k] * load_scalar<TG>(grad_w + (int64_t)row * K + k);
+  float d[EPL];
+  if (norm_topk) {
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) d[j] = 0.0f;
+    if (grad_w != nullptr) {
+      for (int k = 0; k < K; ++k) {
+        const int e = (int)irow[k];
+        if ((e & 63) == lane) {
+          const float g = load_scalar<TG>(grad_w + (int64_t)row * K + k);
+          const float val = wrow[k] * (g - inner);
+#pragma unroll
+          for (int j = 0; j < EPL; ++j)
+            if ((e >> 6) == j) d[j] = val;
+        }
+      }
+    }
+  } else {
+    const float* lrow = logits + (int64_t)row * E;
+    float v[EPL];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < E ? lrow[e] : -INFINITY;
+      m = fmaxf(m, v[j]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      v[j] = (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+      s += v[j];
+    }
+    s = wave_sum(s);
+    const float inv_s = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) d[j] = -v[j] * inv_s * inner;
+    if (grad_w != nullptr) {
+      for (int k = 0; k < K; ++k) {
+        const int e = (int)irow[k];
+        if ((e & 63) == lane) {
+          const float g = load_scalar<TG>(grad_w + (int64_t)row * K + k);
+#pragma unroll
+          for (int j = 0; j < EPL; ++j)
+            if ((e >> 6) == j) d[j] += v[j] * inv_s * g;
+        }
+      }
+    }
+  }
+  float* drow = dl + (int64_t)row * ldl;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      float val = d[j];
+      if (grad_logits != nullptr) val += grad_logits[(int64_t)row * E + e];
+      drow[e] = val;
+    } else if (e < ldl) {
+      drow[e] = 0.0f;
+    }
+  }
+  for (int e = 64 * EPL + lane; e < ldl; e += 64) drow[e] = 0.0f;
+}
+
+template <typename TO>
+__global__ void reduce_partials_kernel(const float* __restrict__ partial, int splits, int64_t n, TO* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int g = 0; g < splits; ++g) acc += partial[(int64_t)g * n + i];
+    store_scalar<TO>(out + i, acc);
+  }
+}
+
+// ---- permutation: stable counting sort of the P = T*K pairs by expert id
+
+__device__ __forceinline__ int clamp_expert(int64_t e, int E) {
+  return e < 0 ? 0 : (e >= E ? E - 1 : (int)e);
+}
+
+__global__ __launch_bounds__(256) void permute_hist_kernel(const int64_t* __restrict__ idx, int P, int E, int chunk,
+                                                           int32_t* __restrict__ chunk_hist) {
+  extern __shared__ int s_hist[];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) s_hist[e] = 0;
+  __syncthreads();
+  const int q0 = blockIdx.x * chunk;
+  const int q1 = min(P, q0 + chunk);
+  for (int q = q0 + threadIdx.x; q < q1; q += blockDim.x) atomicAdd(&s_hist[clamp_expert(idx[q], E)], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) chunk_hist[(int64_t)blockIdx.x * E + e] = s_hist[e];
+}
+
+// One block of 1024 threads: per-expert scan over chunks, then an exclusive
+// scan over experts. chunk_hist becomes the global base of (chunk, expert).
+__global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict__ chunk_hist, int nchunks, int E,
+                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offs) {
+  __shared__ int s_wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int total = 0;
+  if (tid < E) {
+    for (int c = 0; c < nchunks; ++c) {
+      const int v = chunk_hist[(int64_t)c * E + tid];
+      chunk_hist[(int64_t)c * E + tid] = total;
+      total += v;
+    }
+  }
+  const int inc = wave_incl_scan(total, lane);
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  int wbase = 0;
+  for (int w = 0; w < wave; ++w) wbase += s_wsum[w];
+  const int excl = wbase + inc - total;
+  if (tid < E) {
+    counts[tid] = total;
+    offs[tid] = excl + total;
+    for (int c = 0; c < nchunks; ++c) chunk_hist[(int64_t)c * E + tid] += excl;
+  }
+}
+
+__global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
+                                                              int chunk, const int32_t* __restrict__ chunk_base,
+                                                              int32_t* __restrict__ sorted_pair,
+                                                              int32_t* __restrict__ inv_pos) {
+  extern __shared__ int sm[];
+  int* s_base = sm;       // [E]
+  int* s_wcnt = sm + E;   // [4][E]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += 256) {
+    s_base[e] = chunk_base[(int64_t)blockIdx.x * E + e];
+    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
+  }
+  __syncthreads();
+  const int q0 = blockIdx.x * chunk;
+  const int q1 = min(P, q0 + chunk);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int qb = q0; qb < q1; qb += 256) {
+    const int q = qb + tid;
+    const bool valid = q < q1;
+    const int e = valid ? clamp_expert(idx[q], E) : 0;
+    uint64_t mask = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bal = __ballot(valid && bit);
+      mask &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(mask & lt_mask);
+    if (valid && rank == 0) s_wcnt[wave * E + e] = __popcll(mask);
+    __syncthreads();
+    if (valid) {
+      int pos = s_base[e] + rank;
+      for (int w = 0; w < wave; ++w) pos += s_wcnt[w * E + e];
+      sorted_pair[pos] = q;
+      inv_pos[q] = pos;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += 256) {
+      s_base[x] += s_wcnt[x] + s_wcnt[E + x] + s_wcnt[2 * E + x] + s_wcnt[3 * E + x];
+      s_wcnt[x] = s_wcnt[E + x] = s_wcnt[2 * E + x] = s_wcnt[3 * E + x] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// ---- row movers: one wave per destination row, 16-byte lanes
+
+template <typename T> struct RowVec { static constexpr int N = 16 / sizeof(T); };
+
+template <typename T>
+__global__ __launch_bounds__(256) void dispatch_kernel(const T* __restrict__ x, const int32_t* __restrict__ sorted_pair,
+                                                       int P, int K, int H, T* __restrict__ x_perm) {
+  const int lane = threadIdx.x & 63;
+  const int pos = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pos >= P) return;
+  const int t = sorted_pair[pos] / K;
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + (int64_t)t * H);
+  u32x4* dst = reinterpret_cast<u32x4*>(x_perm + (int64_t)pos * H);
+  const int nvec = H / RowVec<T>::N;
+  for (int c = lane; c < nvec; c += 64) dst[c] = src[c];
+}
+
+template <typename T, typename TW>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ y, const TW* __restrict__ w,
+                                                      const int32_t* __restrict__ inv_pos, int T_, int K, int H,
+                                                      T* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T_) return;
+  for (int c = lane * 8; c < H; c += 64 * 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < K; ++k) {
+      const int64_t q = (int64_t)t * K + k;
+      const float wk = load_scalar<TW>(w + q);
+      float v[8];
+      Vec8<T>::load(y + (int64_t)inv_pos[q] * H + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
+    }
+    Vec8<T>::store(out + (int64_t)t * H + c, acc);
+  }
+}
+
+template <typename T, typename TW>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ y,
+                                                          const TW* __restrict__ w,
+                                                          const int32_t* __restrict__ inv_pos, int T_, int K, int H,
+                                                          T* __restrict__ dy, TW* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T_) return;
+  const T* drow = dout + (int64_t)t * H;
+  for (int k = 0; k < K; ++k) {
+    const int64_t q = (int64_t)t * K + k;
+    const float wk = load_scalar<TW>(w + q);
+    const int64_t pos = inv_pos[q];
+    float dot = 0.0f;
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+      float g[8], v[8], o[8];
+      Vec8<T>::load(drow + c, g);
+      Vec8<T>::load(y + pos * H + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dot += g[i] * v[i];
+        o[i] = wk * g[i];
+      }
+      Vec8<T>::store(dy + pos * H + c, o);
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) store_scalar<TW>(dw + q, dot);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dispatch_bwd_kernel(const T* __restrict__ dx_perm,
+                                                           const int32_t* __restrict__ inv_pos, int T_, int K, int H,
+                                                           T* __restrict__ dx) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T_) return;
+  for (int c = lane * 8; c < H; c += 64 * 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < K; ++k) {
+      float v[8];
+      Vec8<T>::load(dx_perm + (int64_t)inv_pos[(int64_t)t * K + k] * H + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += v[i];
+    }
+    Vec8<T>::store(dx + (int64_t)t * H + c, acc);
+  }
+}
+
+unsigned blocks_for(int64_t rows, int per_block) { return (unsigned)((rows + per_block - 1) / per_block); }
+
+}  // namespace
+
+template <typename TW>
+hipError_t router_topk(float* logits, const float* logit_bias, int T, int E, int K, int norm_topk, TW* top_w,
+                       int64_t* top_idx, float* top_w_f32, float* blk_psum, float* blk_lse2, int* blk_counts,
+                       int rows_per_block, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const unsigned grid = blocks_for(T, rows_per_block);
+  const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
+#define PMOE_TOPK_CASE(EPL)                                                                                      \
+  hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, logits, logit_bias, T, E, K, \
+                     norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2, blk_counts, rows_per_block)
+  if (E <= 64) PMOE_TOPK_CASE(1);
+  else if (E <= 128) PMOE_TOPK_CASE(2);
+  else if (E <= 256) PMOE_TOPK_CASE(4);
+  else if (E <= 512) PMOE_TOPK_CASE(8);
+  else if (E <= 1024) PMOE_TOPK_CASE(16);
+  else return hipErrorInvalidValue;
+#undef PMOE_TOPK_CASE
+  return hipGetLastError();
+}
+
+hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
+                               float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s) {
+  hipLaunchKernelGGL(router_stats_reduce_kernel, dim3(1), dim3(1024), 0, s, blk_psum, blk_lse2, blk_counts, nblk, E,
+                     prob_sum, lse_sq_sum, counts);
+  return hipGetLastError();
+}
+
+template <typename TG>
+hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
+                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, int ldl,
+                          hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const unsigned grid = blocks_for(T, 4);
+#define PMOE_DL_CASE(EPL)                                                                                        \
+  hipLaunchKernelGGL((router_dlogits_kernel<EPL, TG>), dim3(grid), dim3(256), 0, s, logits, top_idx, top_w_f32, \
+                     grad_w, grad_logits, T, E, K, norm_topk, dl, ldl)
+  if (E <= 64) PMOE_DL_CASE(1);
+  else if (E <= 128) PMOE_DL_CASE(2);
+  else if (E <= 256) PMOE_DL_CASE(4);
+  else if (E <= 512) PMOE_DL_CASE(8);
+  else if (E <= 1024) PMOE_DL_CASE(16);
+  else return hipErrorInvalidValue;
+#undef PMOE_DL_CASE
+  return hipGetLastError();
+}
+
+template <typename TO>
+hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL((reduce_partials_kernel<TO>), dim3(grid), dim3(256), 0, s, partial, splits, n, out);
+  return hipGetLastError();
+}
+
+hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
+                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s) {
+  const int P = T * K;
+  const int nchunks = (P + chunk - 1) / chunk;
+  if (E > 1024 || E < 1) return hipErrorInvalidValue;
+  if (nchunks > 0) {
+    hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
+                       chunk_hist);
+  }
+  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_hist, nchunks, E, counts, offs);
+  if (nchunks > 0) {
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E,
+                       nbits, chunk, chunk_hist, sorted_pair, inv_pos);
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch_rows(const T* x, const int32_t* sorted_pair, int P, int K, int H, T* x_perm, hipStream_t s) {
+  if (P == 0) return hipSuccess;
+  hipLaunchKernelGGL((dispatch_kernel<T>), dim3(blocks_for(P, 4)), dim3(256), 0, s, x, sorted_pair, P, K, H, x_perm);
+  return hipGetLastError();
+}
+
+template <typename T, typename TW>
+hipError_t combine_rows(const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H, T* out,
+                        hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  hipLaunchKernelGGL((combine_kernel<T, TW>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, y, w, inv_pos, T_, K, H, out);
+  return hipGetLastError();
+}
+
+template <typename T, typename TW>
+hipError_t combine_rows_bwd(const T* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H,
+                            T* dy, TW* dw, hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  hipLaunchKernelGGL((combine_bwd_kernel<T, TW>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, dout, y, w, inv_pos, T_,
+                     K, H, dy, dw);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, int T_, int K, int H, T* dx,
+                             hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  hipLaunchKernelGGL((dispatch_bwd_kernel<T>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, dx_perm, inv_pos, T_, K, H,
+                     dx);
+  return hipGetLastError();
+}
+
+template hipError_t router_topk<bf16_t>(float*, const float*, int, int, int, int, bf16_t*, int64_t*, float*, float*,
+                                        float*, int*, int, hipStream_t);
+template hipError_t router_topk<float>(float*, const float*, int, int, int, int, float*, int64_t*, float*, float*,
+                                       float*, int*, int, hipStream_t);
+template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
+                                           int, int, int, int, float*, int, hipStream_t);
+template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
+                                          int, int, int, float*, int, hipStream_t);
+template hipError_t reduce_partials<float>(const float*, int, int64_t, float*, hipStream_t);
+template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*, hipStream_t);
+
+#define PMOE_INST_ROWS(T)                                                                                      \
+  template hipError_t dispatch_rows<T>(const T*, const int32_t*, int, int, int, T*, hipStream_t);              \
+  template hipError_t dispatch_rows_bwd<T>(const T*, const int32_t*, int, int, int, T*, hipStream_t);          \
+  template hipError_t combine_rows<T, bf16_t>(const T*, const bf16_t*, const int32_t*, int, int, int, T*,      \
+                                              hipStream_t);                                                    \
+  template hipError_t combine_rows<T, float>(const T*, const float*, const int32_t*, int, int, int, T*,        \
+                                             hipStream_t);                                                     \
+  template hipError_t combine_rows_bwd<T, bf16_t>(const T*, const T*, const bf16_t*, const int32_t*, int, int, \
+                                                  int, T*, bf16_t*, hipStream_t);                              \
+  template hipError_t combine_rows_bwd<T, float>(const T*, const T*, const float*, const int32_t*, int, int,   \
+                                                 int, T*, float*, hipStream_t);
+
+PMOE_INST_ROWS(bf16_t)
+PMOE_INST_ROWS(float)
+
+}  // namespace pmoe

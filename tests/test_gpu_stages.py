@@ -1,0 +1,274 @@
+"""GPU parity of each kernel stage against CPU references (fp64 or the oracle).
+
+Integer work (permutation, selection, row gather) must be bit-exact. GEMM
+stages are compared with fp64 per-expert products: rel-L2 <= 1e-2 for bf16
+and <= 1e-5 for fp32 arithmetic; the max-abs error is
+printed next to each figure.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests._gpu_helpers import (DEV, gen, max_abs, ref_grouped, ref_wgrad, rel, routing, say, seg_bounds,
+                                silu64, to_np)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 1e-2, torch.float32: 1e-5}
+
+
+def _ops():
+    from pluggy_amd import ops
+    return ops
+
+
+# ------------------------------------------------------------- permutation
+
+
+@pytest.mark.parametrize("T,K,E,mode", [
+    (1, 1, 1, "uniform"), (7, 2, 8, "uniform"), (2048, 2, 8, "uniform"), (3000, 4, 33, "one"),
+    (100, 8, 8, "uniform"), (8192, 8, 128, "uniform"), (8192, 8, 128, "zipf"), (4099, 6, 1000, "low"),
+])
+def test_permute_bitexact(T, K, E, mode):
+    say(f"permute T={T} K={K} E={E} mode={mode}")
+    idx = routing(T, K, E, seed=T + E, mode=mode)
+    counts, offs, sp, inv = _ops().permute(idx.to(DEV), E)
+    torch.cuda.synchronize()
+    rc, ro, rsp, rinv = O.permute(idx, E)
+    assert np.array_equal(to_np(counts), rc.astype(np.int32))
+    assert np.array_equal(to_np(offs), ro)
+    assert np.array_equal(to_np(sp), rsp)
+    assert np.array_equal(to_np(inv), rinv)
+
+
+def test_permute_deterministic():
+    idx = routing(8192, 8, 128, seed=3, mode="zipf").to(DEV)
+    a = _ops().permute(idx, 128)
+    b = _ops().permute(idx, 128)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+# ----------------------------------------------------------- row movement
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,K,E,H", [(300, 4, 16, 264), (64, 8, 128, 2048)])
+def test_dispatch_combine(dtype, T, K, E, H):
+    say(f"dispatch/combine T={T} K={K} E={E} H={H} {dtype}")
+    ops = _ops()
+    g = gen(1)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    idx = routing(T, K, E, seed=2)
+    w = torch.rand(T, K, generator=g).to(dtype)
+    counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
+    xp = ops.dispatch(x.to(DEV), sp, K)
+    ref_xp = x[torch.from_numpy(O.permute(idx, E)[2].astype(np.int64)) // K]
+    assert torch.equal(xp.cpu(), ref_xp), "dispatch must be a bit-exact gather"
+    # combine: out[t] = sum_k w[t,k] * y[inv[t,k]]
+    y = torch.randn(T * K, H, generator=g).to(dtype)
+    out = ops.combine(y.to(DEV), w.to(DEV), inv)
+    inv_c = inv.cpu().long().view(T, K)
+    ref = (w.double().unsqueeze(-1) * y.double()[inv_c]).sum(1)
+    say(f"  combine rel={rel(out, ref):.2e} maxabs={max_abs(out, ref):.2e}")
+    assert rel(out, ref) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    # combine backward
+    go = torch.randn(T, H, generator=g).to(dtype)
+    gy, gw = ops.combine_backward(go.to(DEV), y.to(DEV), w.to(DEV), inv)
+    ref_gy = torch.zeros(T * K, H, dtype=torch.float64)
+    ref_gy[inv_c.reshape(-1)] = (w.double().unsqueeze(-1) * go.double().unsqueeze(1)).reshape(T * K, H)
+    ref_gw = (go.double().unsqueeze(1) * y.double()[inv_c]).sum(-1)
+    assert rel(gy, ref_gy) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    assert rel(gw, ref_gw) < (4e-3 if dtype == torch.bfloat16 else 1e-5)
+    # dispatch backward: grad_x[t] = sum_k gxp[inv[t,k]]
+    gxp = torch.randn(T * K, H, generator=g).to(dtype)
+    gx = ops.dispatch_backward(gxp.to(DEV), inv, T, K)
+    ref_gx = gxp.double()[inv_c].sum(1)
+    assert rel(gx, ref_gx) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+
+
+# -------------------------------------------------------------- GEMMs
+
+
+GEMM_CASES = [
+    # T, K, E, H, I, routing mode
+    (512, 4, 16, 256, 192, "uniform"),
+    (300, 2, 8, 264, 40, "uniform"),      # ragged H and I (masking along k and n)
+    (1024, 8, 64, 512, 128, "zipf"),       # skewed: empty experts, heavy experts
+    (37, 3, 5, 128, 64, "one"),            # tiny: every group below one tile
+]
+
+
+def _gemm_inputs(T, K, E, H, I, mode, dtype, seed=0):
+    ops = _ops()
+    g = gen(seed)
+    idx = routing(T, K, E, seed=seed + 11, mode=mode)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype)
+    counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
+    xp = ops.dispatch(x.to(DEV), sp, K)
+    return idx, x, wgu, wdn, offs, sp, inv, xp
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_gate_up_swiglu(dtype, case):
+    T, K, E, H, I, mode = case
+    say(f"gate_up_swiglu {case} {dtype}")
+    ops = _ops()
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, dtype)
+    gu, mid = ops.gate_up_swiglu(xp, wgu.to(DEV), offs)
+    o = offs.cpu()
+    ref = ref_grouped(xp, wgu, o, trans_w=True)
+    r = rel(gu, ref)
+    say(f"  gate_up rel={r:.2e} maxabs={max_abs(gu, ref):.2e}")
+    assert r < TOL[dtype]
+    gq = gu.cpu().double()
+    ref_mid = silu64(gq[:, :I]) * gq[:, I:]
+    r = rel(mid, ref_mid)
+    say(f"  mid rel={r:.2e}")
+    assert r < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_down_proj(dtype, case):
+    T, K, E, H, I, mode = case
+    say(f"down_proj {case} {dtype}")
+    ops = _ops()
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, dtype)
+    mid = torch.randn(T * K, I, generator=gen(5)).to(dtype)
+    y = ops.down_proj(mid.to(DEV), wdn.to(DEV), offs)
+    ref = ref_grouped(mid, wdn, offs.cpu(), trans_w=True)
+    r = rel(y, ref)
+    say(f"  y rel={r:.2e} maxabs={max_abs(y, ref):.2e}")
+    assert r < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_down_proj_backward(dtype, case):
+    T, K, E, H, I, mode = case
+    say(f"down_proj_backward {case} {dtype}")
+    ops = _ops()
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, dtype)
+    g = gen(7)
+    P = T * K
+    gy = torch.randn(P, H, generator=g).to(dtype)
+    gu = torch.randn(P, 2 * I, generator=g).to(dtype)
+    mid = torch.randn(P, I, generator=g).to(dtype)
+    ggu, gdn = ops.down_proj_backward(gy.to(DEV), mid.to(DEV), gu.to(DEV), wdn.to(DEV), offs)
+    o = offs.cpu()
+    dmid = ref_grouped(gy, wdn, o, trans_w=False)          # (P, I) = gy_e @ W_dn[e]
+    gate, up = gu.double()[:, :I], gu.double()[:, I:]
+    s = torch.sigmoid(gate)
+    ref_ggu = torch.cat([dmid * up * s * (1 + gate * (1 - s)), dmid * gate * s], dim=1)
+    r = rel(ggu, ref_ggu)
+    say(f"  dgate_up rel={r:.2e} maxabs={max_abs(ggu, ref_ggu):.2e}")
+    assert r < TOL[dtype]
+    ref_gdn = ref_wgrad(gy, mid, o)                        # (E, H, I)
+    r = rel(gdn, ref_gdn)
+    say(f"  d down_proj rel={r:.2e}")
+    assert r < TOL[dtype]
+    empty = [e for e, (lo, hi) in enumerate(seg_bounds(o)) if hi == lo]
+    for e in empty:
+        assert torch.count_nonzero(gdn[e]).item() == 0, "an empty expert has a zero weight gradient"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_gate_up_backward(dtype, case):
+    T, K, E, H, I, mode = case
+    say(f"gate_up_backward {case} {dtype}")
+    ops = _ops()
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, dtype)
+    P = T * K
+    ggu = torch.randn(P, 2 * I, generator=gen(9)).to(dtype)
+    gxp, gwgu = ops.gate_up_backward(ggu.to(DEV), xp, wgu.to(DEV), offs)
+    o = offs.cpu()
+    ref_gxp = ref_grouped(ggu, wgu, o, trans_w=False)      # (P, H) = ggu_e @ W_gu[e]
+    r = rel(gxp, ref_gxp)
+    say(f"  d x_perm rel={r:.2e} maxabs={max_abs(gxp, ref_gxp):.2e}")
+    assert r < TOL[dtype]
+    ref_gw = ref_wgrad(ggu, xp, o)                         # (E, 2I, H)
+    r = rel(gwgu, ref_gw)
+    say(f"  d gate_up_proj rel={r:.2e}")
+    assert r < TOL[dtype]
+
+
+# ----------------------------------------------------------------- router
+
+
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,E,K,norm", [(2048, 512, 8, 2, True), (1000, 2048, 128, 8, True),
+                                          (300, 256, 60, 4, False), (64, 2048, 128, 8, True)])
+def test_router_forward(x_dtype, T, H, E, K, norm):
+    say(f"router T={T} H={H} E={E} K={K} norm={norm} {x_dtype}")
+    ops = _ops()
+    g = gen(T + E)
+    x = torch.randn(T, H, generator=g).to(x_dtype)
+    W = torch.randn(E, H, generator=g) * 0.02
+    logits, tw, ti, tw32, counts, psum, lse2 = ops.router_forward(x.to(DEV), W.to(DEV), K, norm)
+    ref_logits = (x.double() @ W.double().t())
+    r = rel(logits, ref_logits)
+    say(f"  logits rel={r:.2e} maxabs={max_abs(logits, ref_logits):.2e}")
+    assert r < 1e-5
+    # routing is bit-exact given identical fp32 logits
+    lg = logits.cpu()
+    sel = O.select_topk(lg, K)
+    assert np.array_equal(to_np(ti), sel)
+    # weights: closed form on the GPU's own logits (fp64)
+    ls = lg.double().gather(1, torch.from_numpy(sel))
+    p = torch.softmax(lg.double(), -1).gather(1, torch.from_numpy(sel))
+    ref_w = torch.softmax(ls, -1) if norm else p
+    assert rel(tw32, ref_w) < 1e-5
+    assert tw.dtype == x_dtype and rel(tw, ref_w) < (4e-3 if x_dtype == torch.bfloat16 else 1e-5)
+    # statistics
+    rc, rps, rl2 = O.router_stats(lg, torch.from_numpy(sel), E)
+    assert np.array_equal(to_np(counts), rc.astype(np.int32))
+    assert rel(psum, rps) < 1e-5
+    assert abs(lse2.item() - rl2.item()) <= 1e-5 * abs(rl2.item()) + 1e-6
+
+
+def test_router_ties_and_bias():
+    """Zero router weight: every logit ties, so the top-k is experts 0..K-1 with weight 1/K."""
+    ops = _ops()
+    T, H, E, K = 333, 256, 128, 8
+    x = torch.randn(T, H, generator=gen(0)).bfloat16().to(DEV)
+    W = torch.zeros(E, H, device=DEV)
+    logits, tw, ti, tw32, counts, psum, lse2 = ops.router_forward(x, W, K, True)
+    assert torch.equal(ti.cpu(), torch.arange(K).expand(T, K))
+    assert torch.allclose(tw32.cpu(), torch.full((T, K), 1.0 / K))
+    assert torch.allclose(lse2.cpu(), torch.tensor([T * np.log(E) ** 2], dtype=torch.float32), rtol=1e-5)
+    # an additive bias that ranks experts in reverse order
+    bias = torch.arange(E, dtype=torch.float32, device=DEV)
+    logits, tw, ti, *_ = ops.router_forward(x, W, K, True, bias)
+    assert torch.equal(ti.cpu(), torch.arange(E - 1, E - 1 - K, -1).expand(T, K))
+    assert torch.equal(logits.cpu(), bias.cpu().expand(T, E))
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_router_backward(norm, x_dtype):
+    say(f"router backward norm={norm} {x_dtype}")
+    ops = _ops()
+    T, H, E, K = 700, 512, 64, 6
+    g = gen(4)
+    x = torch.randn(T, H, generator=g).to(x_dtype)
+    W = torch.randn(E, H, generator=g) * 0.05
+    logits, tw, ti, tw32, *_ = ops.router_forward(x.to(DEV), W.to(DEV), K, norm)
+    gw = torch.randn(T, K, generator=g).to(x_dtype)
+    gl = torch.randn(T, E, generator=g) * 0.1
+    gx, gW = ops.router_backward(x.to(DEV), W.to(DEV), logits, ti, tw32, gw.to(DEV), gl.to(DEV), norm)
+    dl = O.router_backward_closed_form(logits.cpu(), ti.cpu(), gw.double(), norm, grad_logits=gl)
+    ref_gx = dl @ W.double()
+    ref_gW = dl.t() @ x.double()
+    rx, rW = rel(gx, ref_gx), rel(gW, ref_gW)
+    say(f"  dx rel={rx:.2e} dW rel={rW:.2e}")
+    assert rx < (1e-2 if x_dtype == torch.bfloat16 else 1e-5)
+    assert rW < 1e-5
