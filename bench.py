@@ -1,0 +1,204 @@
+#!/usr/bin/env python
+"""Benchmark of the MoE feed-forward block on one MI355X.
+
+Workload: the Qwen3-30B-A3B-shape MoE layer,
+forward + backward, T = 8192 tokens (batch 4 x seq 2048), hidden 2048,
+128 experts, top-8, moe_intermediate 768, SwiGLU, bf16 activations and
+weights with an fp32 router. One step = router + experts forward and the full
+backward (upstream grad N(0,1)), inputs resident in HBM.
+
+Prints one JSON line: tokens/s (whole job), expert-GEMM TFLOP/s and its
+fraction of the bf16 dense MFMA peak, per-stage HIP-event timings, the
+roofline of the dominant kernel, HBM GB/s of the row-movement kernels, and a
+CPU baseline (the restated reference CPU path) timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "MoE layer fwd+bwd tokens/s & TFLOP/s (% bf16 MFMA peak), Qwen3-30B-A3B shape"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, help="workload id (BASELINE.json configs, 1-based)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=None,
+                    help="tokens of the CPU-baseline sample (default: the full workload)")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, tokens: int | None):
+    """The reference CPU path (router + per-expert loop, autograd backward), restated in oracle/."""
+    import torch
+
+    from oracle import moe_oracle as O
+    from pluggy_amd.workloads import make_inputs
+
+    T = cfg.tokens if tokens is None else tokens
+    inp = make_inputs(cfg, tokens=T)
+    H = cfg.hidden
+
+    def step():
+        x = inp["x"].reshape(1, T, H).detach().requires_grad_(cfg.backward)
+        params = [inp["router_weight"], inp["gate_up_proj"], inp["down_proj"]]
+        wr, gu, dn = (p.detach().requires_grad_(cfg.backward) for p in params)
+        y, _ = O.sparse_mlp_forward(x, wr, gu, dn, cfg.top_k, cfg.norm_topk_prob)
+        if cfg.backward:
+            y.reshape(T, H).backward(inp["grad_out"])
+
+    t0 = time.perf_counter()
+    step()
+    dt = time.perf_counter() - t0
+    return {
+        "value": T / dt,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one {'fwd+bwd' if cfg.backward else 'fwd'} step of the restated reference CPU path "
+                   f"(fp32 router + per-expert loop, moe.py:38-65, torch autograd) at T={T} of the "
+                   f"{cfg.name} layer, {cfg.dtype}, no warm-up; {dt:.2f} s"),
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "torch": torch.__version__,
+    }
+
+
+GEMM_STAGES = ("gate_up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "gate_up_dgrad", "gate_up_wgrad")
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import pluggy_amd
+    from pluggy_amd.moe import stage_timer
+    from pluggy_amd.workloads import CONFIGS, combine_bytes, dispatch_bytes, make_inputs
+
+    cfg = CONFIGS[args.config]
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    P = cfg.pairs
+    inp = make_inputs(cfg, device=dev)
+    mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
+    with torch.no_grad():
+        mlp.router.weight.copy_(inp["router_weight"])
+    mlp.experts.gate_up_proj.data = inp["gate_up_proj"]
+    mlp.experts.down_proj.data = inp["down_proj"]
+    if "logit_bias" in inp:
+        mlp.router.logit_bias = inp["logit_bias"]
+    B = cfg.batch
+    x = inp["x"].reshape(B, T // B, H)
+    gout = inp.get("grad_out")
+    gout = gout.reshape(B, T // B, H) if gout is not None else None
+
+    def step():
+        for p in mlp.parameters():
+            p.grad = None
+        xg = x.detach().requires_grad_(cfg.backward)
+        out = mlp(xg)
+        if cfg.backward:
+            out.backward(gout)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with stage_timer() as timer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(args.steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    stages = timer.summary()
+
+    gemm_flops = cfg.gemm_flops()
+    tflops = gemm_flops / (ms * 1e-3) / 1e12
+    # dominant kernel: the grouped-GEMM stage with the largest total time
+    flops_of = {"gate_up": 2.0 * P * H * 2 * I, "down": 2.0 * P * I * H}
+    gemm = {n: s for n, s in stages.items() if n in GEMM_STAGES}
+    dom = max(gemm, key=lambda n: gemm[n]["total_ms"])
+    dom_flops = flops_of[dom.split("_")[0] if dom.startswith("down") else "gate_up"]
+    dom_tflops = dom_flops / (gemm[dom]["mean_ms"] * 1e-3) / 1e12
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    hbm = {}
+    for name, nbytes in (("dispatch", dispatch_bytes(cfg)), ("combine", combine_bytes(cfg)),
+                         ("dispatch_bwd", P * H * es + P * 4 + T * H * es),
+                         ("combine_bwd", T * H * es + 2 * P * H * es + P * (4 + 2 * es))):
+        if name in stages:
+            gbs = nbytes / (stages[name]["mean_ms"] * 1e-3) / 1e9
+            hbm[name] = {"bytes": nbytes, "mean_ms": round(stages[name]["mean_ms"], 4), "GB/s": round(gbs, 1),
+                         "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "f32",
+        "data": "synthetic (seeded N(0,1) inputs and upstream grad, N(0,0.02) weights)",
+        "config": {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if cfg.backward else 'fwd'}", "tokens": T,
+                   "batch": B, "seq_len": T // B, "hidden": H, "experts": E, "top_k": K, "moe_intermediate": I,
+                   "router": "fp32", "parallelism": "single GPU"},
+        "tflops": round(tflops, 2),
+        "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "gemm_gflop_per_step": round(gemm_flops / 1e9, 1),
+        "wall_s": round(wall, 3),
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "flop_per_launch": dom_flops, "mean_ms": round(gemm[dom]["mean_ms"], 4)},
+        "hbm": hbm,
+        "stages_ms": {n: round(s["mean_ms"], 4) for n, s in sorted(stages.items(), key=lambda kv: -kv[1]["total_ms"])},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -11,18 +11,21 @@ Mirrors the reference operator surface:
   (pluggy/models/qwen3_moe/qwen3_moe.py:168-178) with fp32 logits and the
   "ties -> lower expert id" selection rule.
 
-Both are ``torch.autograd.Function``s whose forward and backward each call one
-C-ABI entry point of ``libpmoe.so``.
+Both are ``torch.autograd.Function``s. Each stage (router, permutation, row
+gather, each grouped GEMM, combine, and their backward) is one C-ABI call on
+the current stream; ``stage_timer()`` brackets the stages with HIP events.
 """
 
 from __future__ import annotations
 
+import contextlib
+from collections import defaultdict
 from dataclasses import dataclass
 
 import torch
 
-from . import _lib
-from ._lib import call, dtype_code, ptr, require_gpu, size, stream_of, workspace
+from . import ops
+from ._lib import require_gpu
 
 
 @dataclass
@@ -35,24 +38,63 @@ class RouterStats:
     tokens: int
 
 
+# ------------------------------------------------------------ stage timing
+
+
+class StageTimer:
+    """HIP-event timing of each named stage on the stream it runs on."""
+
+    def __init__(self):
+        self.records: dict[str, list] = defaultdict(list)
+
+    @contextlib.contextmanager
+    def mark(self, name: str):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        try:
+            yield
+        finally:
+            end.record()
+            self.records[name].append((start, end))
+
+    def summary(self) -> dict[str, dict[str, float]]:
+        """name -> {"calls", "total_ms", "mean_ms"} (synchronises)."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, evs in self.records.items():
+            ms = [s.elapsed_time(e) for s, e in evs]
+            out[name] = {"calls": len(ms), "total_ms": sum(ms), "mean_ms": sum(ms) / len(ms)}
+        return out
+
+
+_timer: StageTimer | None = None
+
+
+@contextlib.contextmanager
+def stage_timer():
+    """Collect per-stage HIP-event timings of every MoE call made inside the block."""
+    global _timer
+    prev, _timer = _timer, StageTimer()
+    try:
+        yield _timer
+    finally:
+        _timer = prev
+
+
+def _stage(name: str):
+    return _timer.mark(name) if _timer is not None else contextlib.nullcontext()
+
+
+# ------------------------------------------------------------------ router
+
+
 class _RouterFunction(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, top_k, norm_topk_prob, logit_bias, out_dtype):
-        T, H = x.shape
-        E = weight.shape[0]
-        dev = x.device
-        logits = torch.empty(T, E, dtype=torch.float32, device=dev)
-        top_w = torch.empty(T, top_k, dtype=out_dtype, device=dev)
-        top_i = torch.empty(T, top_k, dtype=torch.int64, device=dev)
-        top_w32 = torch.empty(T, top_k, dtype=torch.float32, device=dev)
-        counts = torch.empty(E, dtype=torch.int32, device=dev)
-        psum = torch.empty(E, dtype=torch.float32, device=dev)
-        lse2 = torch.empty(1, dtype=torch.float32, device=dev)
-        nbytes = size("pmoe_router_forward_workspace_size", T, E)
-        ws = workspace(nbytes, dev)
-        call("pmoe_router_forward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype),
-             ptr(logit_bias), T, H, E, top_k, int(norm_topk_prob), ptr(logits), ptr(top_w), dtype_code(out_dtype),
-             ptr(top_i), ptr(top_w32), ptr(counts), ptr(psum), ptr(lse2), ptr(ws), ws.numel(), stream_of(x))
+    def forward(ctx, x, weight, top_k, norm_topk_prob, logit_bias):
+        with _stage("router_fwd"):
+            logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
+                x, weight, top_k, norm_topk_prob, logit_bias)
         ctx.save_for_backward(x, weight, logits, top_i, top_w32)
         ctx.norm_topk_prob = bool(norm_topk_prob)
         ctx.mark_non_differentiable(top_i, top_w32, counts, psum, lse2)
@@ -61,24 +103,15 @@ class _RouterFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_logits, g_w, _gi, _gw32, _gc, _gp, _gl):
         x, weight, logits, top_i, top_w32 = ctx.saved_tensors
-        T, H = x.shape
-        E, K = weight.shape[0], top_i.shape[1]
-        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_x or need_w) or (g_logits is None and g_w is None):
-            return None, None, None, None, None, None
-        gx = torch.empty_like(x) if need_x else None
-        gW = torch.empty_like(weight) if need_w else None
+        if not (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]) or (g_logits is None and g_w is None):
+            return None, None, None, None, None
         if g_logits is not None:
             g_logits = g_logits.float().contiguous()
-        gw_code = _lib.PMOE_F32
         if g_w is not None:
             g_w = g_w.contiguous()
-            gw_code = dtype_code(g_w.dtype)
-        ws = workspace(size("pmoe_router_backward_workspace_size", T, H, E), x.device)
-        call("pmoe_router_backward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype),
-             ptr(logits), ptr(top_i), ptr(top_w32), ptr(g_w), gw_code, ptr(g_logits), T, H, E, K,
-             int(ctx.norm_topk_prob), ptr(gx), ptr(gW), ptr(ws), ws.numel(), stream_of(x))
-        return gx, gW, None, None, None, None
+        with _stage("router_bwd"):
+            gx, gW = ops.router_backward(x, weight, logits, top_i, top_w32, g_w, g_logits, ctx.norm_topk_prob)
+        return (gx if ctx.needs_input_grad[0] else None), (gW if ctx.needs_input_grad[1] else None), None, None, None
 
 
 def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
@@ -101,58 +134,63 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     logits, top_w, top_i, _w32, counts, psum, lse2 = _RouterFunction.apply(
-        x, w, int(top_k), bool(norm_topk_prob), logit_bias, x.dtype)
+        x, w, int(top_k), bool(norm_topk_prob), logit_bias)
     if return_stats:
         return logits, top_w, top_i, RouterStats(counts, psum, lse2, x.shape[0])
     return logits, top_w, top_i
 
 
+# -------------------------------------------------------------- expert FFN
+
+
 class _ExpertFFNFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, top_indices, top_weights, gate_up_proj, down_proj):
-        T, H = hidden.shape
+        E = gate_up_proj.shape[0]
         K = top_indices.shape[1]
-        E, two_i, _ = gate_up_proj.shape
-        I = two_i // 2
-        P = T * K
-        dev, dt = hidden.device, hidden.dtype
-        out = torch.empty(T, H, dtype=dt, device=dev)
-        counts = torch.empty(E, dtype=torch.int32, device=dev)
-        offs = torch.empty(E, dtype=torch.int32, device=dev)
-        sorted_pair = torch.empty(P, dtype=torch.int32, device=dev)
-        inv_pos = torch.empty(P, dtype=torch.int32, device=dev)
-        x_perm = torch.empty(P, H, dtype=dt, device=dev)
-        gu = torch.empty(P, 2 * I, dtype=dt, device=dev)
-        mid = torch.empty(P, I, dtype=dt, device=dev)
-        y = torch.empty(P, H, dtype=dt, device=dev)
-        ws = workspace(size("pmoe_expert_ffn_forward_workspace_size", T, K, E), dev)
-        call("pmoe_expert_ffn_forward", ptr(hidden), ptr(top_indices), ptr(top_weights),
-             dtype_code(top_weights.dtype), ptr(gate_up_proj), ptr(down_proj), dtype_code(dt), T, K, E, H, I,
-             ptr(out), ptr(counts), ptr(offs), ptr(sorted_pair), ptr(inv_pos), ptr(x_perm), ptr(gu), ptr(mid),
-             ptr(y), ptr(ws), ws.numel(), stream_of(hidden))
-        ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, sorted_pair, inv_pos, x_perm, gu, mid, y)
-        ctx.dims = (T, K, E, H, I)
+        with _stage("permute"):
+            counts, offs, sorted_pair, inv_pos = ops.permute(top_indices, E)
+        with _stage("dispatch"):
+            x_perm = ops.dispatch(hidden, sorted_pair, K)
+        with _stage("gate_up_fwd"):
+            gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
+        with _stage("down_fwd"):
+            y = ops.down_proj(mid, down_proj, offs)
+        with _stage("combine"):
+            out = ops.combine(y, top_weights, inv_pos)
+        ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
+        ctx.dims = (hidden.shape[0], K, E)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        top_w, gate_up, down, offs, sorted_pair, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
-        T, K, E, H, I = ctx.dims
+        top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
+        T, K, E = ctx.dims
         need = ctx.needs_input_grad
         grad_out = grad_out.contiguous()
         if grad_out.dtype != x_perm.dtype:
             grad_out = grad_out.to(x_perm.dtype)
-        dev = grad_out.device
-        g_hidden = torch.empty(T, H, dtype=x_perm.dtype, device=dev) if need[0] else None
-        g_w = torch.empty_like(top_w) if need[2] else None
-        g_gu = torch.empty_like(gate_up) if need[3] else None
-        g_dn = torch.empty_like(down) if need[4] else None
-        ws = workspace(size("pmoe_expert_ffn_backward_workspace_size", T, K, H, I, dtype_code(x_perm.dtype)), dev)
-        call("pmoe_expert_ffn_backward", ptr(grad_out), ptr(top_w), dtype_code(top_w.dtype), ptr(gate_up),
-             ptr(down), dtype_code(x_perm.dtype), T, K, E, H, I, ptr(offs), ptr(sorted_pair), ptr(inv_pos),
-             ptr(x_perm), ptr(gu), ptr(mid), ptr(y), ptr(g_hidden), ptr(g_w), ptr(g_gu), ptr(g_dn), ptr(ws),
-             ws.numel(), stream_of(grad_out))
-        return g_hidden, None, g_w, g_gu, g_dn
+        with _stage("combine_bwd"):
+            g_y, g_w = ops.combine_backward(grad_out, y, top_w, inv_pos)
+        g_hidden = g_gu_w = g_dn_w = None
+        g_gu = None
+        if need[0] or need[3]:
+            with _stage("down_dgrad"):
+                g_gu = ops.down_proj_dgrad(g_y, gu, down, offs)
+        if need[4]:
+            with _stage("down_wgrad"):
+                g_dn_w = ops.down_proj_wgrad(g_y, mid, offs, E)
+        del g_y
+        if need[0]:
+            with _stage("gate_up_dgrad"):
+                g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
+            with _stage("dispatch_bwd"):
+                g_hidden = ops.dispatch_backward(g_xp, inv_pos, T, K)
+            del g_xp
+        if need[3]:
+            with _stage("gate_up_wgrad"):
+                g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+        return g_hidden, None, (g_w if need[2] else None), g_gu_w, g_dn_w
 
 
 def moe_expert_ffn(
@@ -183,4 +221,3 @@ def moe_expert_ffn(
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
     return _ExpertFFNFunction.apply(hidden.contiguous(), top_indices.to(torch.int64).contiguous(), tw.contiguous(),
                                     gu, dn)
-

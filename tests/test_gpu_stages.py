@@ -272,3 +272,73 @@ def test_router_backward(norm, x_dtype):
     say(f"  dx rel={rx:.2e} dW rel={rW:.2e}")
     assert rx < (1e-2 if x_dtype == torch.bfloat16 else 1e-5)
     assert rW < 1e-5
+
+
+# ------------------------------------------------- fused C entry points
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_expert_ffn_entry_points(dtype):
+    """pmoe_expert_ffn_forward/backward (the whole-operator C ABI) == the per-stage path, bitwise."""
+    from pluggy_amd._lib import call, dtype_code, ptr, size, workspace
+
+    import pluggy_amd
+    T, K, E, H, I = 300, 4, 16, 256, 64
+    say(f"fused entry points T={T} K={K} E={E} H={H} I={I} {dtype}")
+    g = gen(31)
+    x = torch.randn(T, H, generator=g).to(dtype).to(DEV)
+    idx = routing(T, K, E, seed=5, mode="zipf").to(DEV)
+    w = torch.rand(T, K, generator=g).to(dtype).to(DEV)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype).to(DEV)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype).to(DEV)
+    gout = torch.randn(T, H, generator=g).to(dtype).to(DEV)
+    # stage path through autograd
+    xs = x.clone().requires_grad_(True)
+    ws_ = w.clone().requires_grad_(True)
+    a = wgu.clone().requires_grad_(True)
+    b = wdn.clone().requires_grad_(True)
+    out_s = pluggy_amd.moe_expert_ffn(xs, idx, ws_, a, b)
+    out_s.backward(gout)
+    # fused entry points
+    P = T * K
+    dt = dtype_code(dtype)
+    out = torch.empty(T, H, dtype=dtype, device=DEV)
+    counts = torch.empty(E, dtype=torch.int32, device=DEV)
+    offs = torch.empty(E, dtype=torch.int32, device=DEV)
+    sp = torch.empty(P, dtype=torch.int32, device=DEV)
+    inv = torch.empty(P, dtype=torch.int32, device=DEV)
+    xp = torch.empty(P, H, dtype=dtype, device=DEV)
+    gu = torch.empty(P, 2 * I, dtype=dtype, device=DEV)
+    mid = torch.empty(P, I, dtype=dtype, device=DEV)
+    y = torch.empty(P, H, dtype=dtype, device=DEV)
+    wsp = workspace(size("pmoe_expert_ffn_forward_workspace_size", T, K, E), DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    call("pmoe_expert_ffn_forward", ptr(x), ptr(idx), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(out),
+         ptr(counts), ptr(offs), ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(wsp), wsp.numel(), stream)
+    gx = torch.empty_like(x)
+    gw = torch.empty_like(w)
+    ggu = torch.empty_like(wgu)
+    gdn = torch.empty_like(wdn)
+    wsb = workspace(size("pmoe_expert_ffn_backward_workspace_size", T, K, H, I, dt), DEV)
+    call("pmoe_expert_ffn_backward", ptr(gout), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
+         ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(gx), ptr(gw), ptr(ggu), ptr(gdn), ptr(wsb),
+         wsb.numel(), stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_s)
+    assert torch.equal(gx, xs.grad) and torch.equal(gw, ws_.grad)
+    assert torch.equal(ggu, a.grad) and torch.equal(gdn, b.grad)
+
+
+def test_argument_errors_raise():
+    """Rejected arguments come back as RuntimeError with the library's message (no kernel launched)."""
+    ops = _ops()
+    idx = torch.zeros(4, 3, dtype=torch.int64, device=DEV)
+    with pytest.raises(RuntimeError, match="exceeds num_experts"):
+        ops.permute(idx, 2)
+    x = torch.zeros(4, 12, dtype=torch.bfloat16, device=DEV)  # H not a multiple of 8
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        ops.router_forward(x, torch.zeros(4, 12, device=DEV), 2)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        import pluggy_amd
+        pluggy_amd.moe_expert_ffn(torch.zeros(4, 8), torch.zeros(4, 1, dtype=torch.int64), torch.ones(4, 1),
+                                  torch.zeros(2, 16, 8), torch.zeros(2, 8, 8))

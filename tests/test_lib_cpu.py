@@ -1,0 +1,103 @@
+"""The C-ABI library loads on a CPU-only host and exports exactly what include/pmoe.h declares.
+
+No compute is launched here: only workspace-size queries and argument
+rejections, which return before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "pmoe.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"PMOE_API\s+[\w\s\*]+?\b(pmoe_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pluggy_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libpmoe.so is not built (run python -m pluggy_amd.build / __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    for name in ("pmoe_router_forward", "pmoe_router_backward", "pmoe_permute", "pmoe_dispatch",
+                 "pmoe_gate_up_swiglu", "pmoe_down_proj", "pmoe_combine", "pmoe_expert_ffn_forward",
+                 "pmoe_expert_ffn_backward"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_binding_table_matches_header():
+    from pluggy_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_workspace_queries(lib):
+    assert lib.pmoe_version().startswith(b"pmoe")
+    from pluggy_amd import _lib
+
+    # backward workspace holds grad_y (P*H) and grad_gate_up_out (P*2I) in bf16
+    P, H, I = 8192 * 8, 2048, 768
+    assert _lib.size("pmoe_expert_ffn_backward_workspace_size", 8192, 8, H, I, 1) >= P * H * 2 + P * 2 * I * 2
+    assert _lib.size("pmoe_permute_workspace_size", 8192, 8, 128) >= 32 * 128 * 4
+    assert _lib.size("pmoe_router_forward_workspace_size", 0, 128) >= 0
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((None, 10, 9, 8), b"exceeds num_experts"),       # K > E
+    ((None, 10, 2, 2000), b"> 1024"),                  # too many experts
+    ((None, 10, 70, 100), b"top_k=70 > 64"),
+])
+def test_permute_rejects_bad_arguments(lib, args, needle):
+    rc = lib.pmoe_permute(*args, None, None, None, None, None, 0, None)
+    assert rc == -1
+    assert needle in lib.pmoe_last_error_string()
+
+
+def test_gemm_rejects_unaligned_hidden(lib):
+    from pluggy_amd import _lib
+
+    rc = lib.pmoe_down_proj(None, None, None, _lib.PMOE_BF16, 64, 8, 100, 64, None, None)
+    assert rc == -1 and b"multiple of 8" in lib.pmoe_last_error_string()
+
+
+def test_workspace_too_small_is_rejected(lib):
+    rc = lib.pmoe_permute(ctypes.c_void_p(16), 100, 2, 8, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                          ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, None)
+    assert rc == -3 and b"workspace" in lib.pmoe_last_error_string()
+
+
+def test_product_path_has_no_cpu_fallback():
+    import torch
+
+    import pluggy_amd
+
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pluggy_amd.moe_expert_ffn(torch.zeros(4, 8), torch.zeros(4, 1, dtype=torch.int64), torch.ones(4, 1),
+                                  torch.zeros(2, 16, 8), torch.zeros(2, 8, 8))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pluggy_amd.router_topk(torch.zeros(4, 8), torch.zeros(2, 8), 1)
+
+
+def test_product_package_does_not_import_the_oracle():
+    for path in (ROOT / "pluggy_amd").rglob("*.py"):
+        src = path.read_text()
+        assert "import oracle" not in src and "from oracle" not in src, path
