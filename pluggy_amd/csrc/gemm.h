@@ -247,6 +247,8 @@ struct GemmParams {
   int M, N, K;          // see GroupMode; GM_RED: M x N per group, K = total reduction
   int split_chunk;
   int inter;            // SwiGLU: I (columns of gate; up starts at I)
+  uint64_t a_bytes;     // extent of A's storage (from A), and of one group's B (from B + g*strideB)
+  uint64_t b_bytes;
 };
 
 struct TileInfo {
@@ -298,146 +300,14 @@ __device__ __forceinline__ float round_to(float v) {
   else return v;
 }
 
-// ----------------------------------------------------------------- kernel ----
-
-template <class Cfg, typename TA, typename TB, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
-__global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
-  typedef typename Cfg::Tc Tc;
-  typedef Mfma<Tc> MF;
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, LDK = Cfg::LDK, NT = Cfg::NT;
+// Epilogue shared by the GEMM engines: each wave stages its accumulators one
+// 32-row slab at a time through LDS (fp32), then writes rows with 16-byte
+// vector stores, applying the fused SwiGLU forward / backward when asked.
+template <class Cfg, typename Tout, int GM, int EPI>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* smem_f, const TileInfo& ti,
+                                          const GemmParams& p, int wave, int wm, int wn, int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
-  static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
-  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS), "SwiGLU epilogue is the gate_up forward");
-  static_assert(EPI != EPI_SWIGLU || (Cfg::NI % 2 == 0), "SwiGLU pairs gate and up halves of a wave tile");
-
-  __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM_BYTES];
-  __shared__ int s_scan[1025];
-  __shared__ int s_found;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
-
-  // ---- tile mapping
-  const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-  const int bid = blockIdx.x;
-  const int tn = bid % ntiles_n;
-  const int slot = bid / ntiles_n;
-  TileInfo ti;
-  const TA* A = reinterpret_cast<const TA*>(p.A);
-  const TB* B = reinterpret_cast<const TB*>(p.B);
-  if constexpr (GM == GM_ROWS) {
-    int g, r0, re;
-    if (!rows_tile_lookup<BM>(p.offs, p.groups, slot, s_scan, &s_found, g, r0, re)) return;
-    ti.group = g; ti.m0 = r0; ti.m_end = re; ti.k_lo = 0; ti.k_hi = p.K;
-    B += (int64_t)g * p.strideB;
-  } else if constexpr (GM == GM_RED) {
-    const int mt = (p.M + BM - 1) / BM;
-    const int g = slot / mt;
-    if (g >= p.groups) return;
-    ti.group = g; ti.m0 = (slot % mt) * BM; ti.m_end = p.M;
-    if (p.offs != nullptr) {
-      ti.k_lo = g == 0 ? 0 : p.offs[g - 1];
-      ti.k_hi = p.offs[g];
-    } else {
-      ti.k_lo = g * p.split_chunk;
-      ti.k_hi = min(p.K, ti.k_lo + p.split_chunk);
-    }
-  } else {
-    ti.group = 0; ti.m0 = slot * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
-    if (ti.m0 >= p.M) return;
-  }
-  ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
-
-  Tc* lds = reinterpret_cast<Tc*>(smem);
-  Tc* As[2] = {lds, lds + Cfg::STAGE_ELEMS};
-  Tc* Bs[2] = {lds + BM * LDK, lds + Cfg::STAGE_ELEMS + BM * LDK};
-
-  // ---- operand stagers
-  typedef typename std::conditional<A_KC, KContigStager<TA, Tc, BM, BK, LDK, NT>,
-                                    TransStager<TA, Tc, BM, BK, LDK, NT>>::type StA;
-  typedef typename std::conditional<B_KC, KContigStager<TB, Tc, BN, BK, LDK, NT>,
-                                    TransStager<TB, Tc, BN, BK, LDK, NT>>::type StB;
-  StA sa;
-  StB sb;
-  if constexpr (A_KC) {
-    const int m0 = ti.m0, me = ti.m_end;
-    const int64_t lda = p.lda;
-    sa.init([&](int r) -> const TA* { return (m0 + r < me) ? A + (int64_t)(m0 + r) * lda : nullptr; }, tid);
-  } else {
-    sa.init(A, p.lda, ti.m0, ti.m_end);
-  }
-  if constexpr (B_KC) {
-    const int n0 = ti.n0, N = p.N, I = p.inter;
-    const int64_t ldb = p.ldb;
-    if constexpr (EPI == EPI_SWIGLU) {
-      // Block column c -> B row: each wave's WN columns are WN/2 gate rows then
-      // the WN/2 matching up rows (offset I), so one lane holds both halves.
-      sb.init([&](int c) -> const TB* {
-        int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
-        int gcol = n0 + w * h + (cc % h);
-        if (gcol >= I) return nullptr;
-        int row = (cc < h) ? gcol : I + gcol;
-        return B + (int64_t)row * ldb;
-      }, tid);
-    } else {
-      sb.init([&](int c) -> const TB* { return (n0 + c < N) ? B + (int64_t)(n0 + c) * ldb : nullptr; }, tid);
-    }
-  } else {
-    sb.init(B, p.ldb, ti.n0, p.N);
-  }
-
-  f32x16 acc[MI][NI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int klen = ti.k_hi - ti.k_lo;
-  const int nk = klen > 0 ? (klen + BK - 1) / BK : 0;
-
-  if (nk > 0) {
-    sa.load(ti.k_lo, ti.k_hi, tid);
-    sb.load(ti.k_lo, ti.k_hi, tid);
-    sa.store(As[0], tid);
-    sb.store(Bs[0], tid);
-  }
-  __syncthreads();
-
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * MF::KPACK;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      sa.load(ti.k_lo + (kt + 1) * BK, ti.k_hi, tid);
-      sb.load(ti.k_lo + (kt + 1) * BK, ti.k_hi, tid);
-    }
-    const Tc* a_base = As[cur] + (wm * Cfg::WM + frag_row) * LDK + frag_k;
-    const Tc* b_base = Bs[cur] + (wn * Cfg::WN + frag_row) * LDK + frag_k;
-#pragma unroll
-    for (int ks = 0; ks < BK / MF::MK; ++ks) {
-      typename MF::frag_t af[MI], bf[NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = MF::load(a_base + i * 32 * LDK + ks * MF::MK);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bf[j] = MF::load(b_base + j * 32 * LDK + ks * MF::MK);
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = MF::mma(af[i], bf[j], acc[i][j]);
-    }
-    if (kt + 1 < nk) {
-      sa.store(As[cur ^ 1], tid);
-      sb.store(Bs[cur ^ 1], tid);
-    }
-    __syncthreads();
-  }
-
-  // ---- epilogue: stage each 32-row slab of the wave tile through LDS as fp32
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * Cfg::EPI_LD;
+  float* stage = smem_f + wave * 32 * Cfg::EPI_LD;
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
   constexpr int WN = Cfg::WN;
@@ -509,6 +379,257 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
     }
     __syncthreads();
   }
+}
+
+// ----------------------------------------------------------------- kernel ----
+
+template <class Cfg, typename TA, typename TB, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
+__global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
+  typedef typename Cfg::Tc Tc;
+  typedef Mfma<Tc> MF;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, LDK = Cfg::LDK, NT = Cfg::NT;
+  constexpr int MI = Cfg::MI, NI = Cfg::NI;
+  static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
+  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS), "SwiGLU epilogue is the gate_up forward");
+  static_assert(EPI != EPI_SWIGLU || (Cfg::NI % 2 == 0), "SwiGLU pairs gate and up halves of a wave tile");
+
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM_BYTES];
+  __shared__ int s_scan[1025];
+  __shared__ int s_found;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
+
+  // ---- tile mapping
+  const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+  const int bid = blockIdx.x;
+  const int tn = bid % ntiles_n;
+  const int slot = bid / ntiles_n;
+  TileInfo ti;
+  const TA* A = reinterpret_cast<const TA*>(p.A);
+  const TB* B = reinterpret_cast<const TB*>(p.B);
+  if constexpr (GM == GM_ROWS) {
+    int g, r0, re;
+    if (!rows_tile_lookup<BM>(p.offs, p.groups, slot, s_scan, &s_found, g, r0, re)) return;
+    ti.group = g; ti.m0 = r0; ti.m_end = re; ti.k_lo = 0; ti.k_hi = p.K;
+    B += (int64_t)g * p.strideB;
+  } else if constexpr (GM == GM_RED) {
+    const int mt = (p.M + BM - 1) / BM;
+    const int g = slot / mt;
+    if (g >= p.groups) return;
+    ti.group = g; ti.m0 = (slot % mt) * BM; ti.m_end = p.M;
+    if (p.offs != nullptr) {
+      ti.k_lo = g == 0 ? 0 : p.offs[g - 1];
+      ti.k_hi = p.offs[g];
+    } else {
+      ti.k_lo = g * p.split_chunk;
+      ti.k_hi = min(p.K, ti.k_lo + p.split_chunk);
+    }
+  } else {
+    ti.group = 0; ti.m0 = slot * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
+    if (ti.m0 >= p.M) return;
+  }
+  ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+
+  // LDS stage s holds the A tile at [s*STAGE_ELEMS] and the B tile right after it.
+  // Addresses are always formed from the __shared__ base so they stay in the
+  // LDS address space (ds_read/ds_write, not flat accesses).
+  Tc* const lds = reinterpret_cast<Tc*>(smem);
+
+  // ---- operand stagers
+  typedef typename std::conditional<A_KC, KContigStager<TA, Tc, BM, BK, LDK, NT>,
+                                    TransStager<TA, Tc, BM, BK, LDK, NT>>::type StA;
+  typedef typename std::conditional<B_KC, KContigStager<TB, Tc, BN, BK, LDK, NT>,
+                                    TransStager<TB, Tc, BN, BK, LDK, NT>>::type StB;
+  StA sa;
+  StB sb;
+  if constexpr (A_KC) {
+    const int m0 = ti.m0, me = ti.m_end;
+    const int64_t lda = p.lda;
+    sa.init([&](int r) -> const TA* { return (m0 + r < me) ? A + (int64_t)(m0 + r) * lda : nullptr; }, tid);
+  } else {
+    sa.init(A, p.lda, ti.m0, ti.m_end);
+  }
+  if constexpr (B_KC) {
+    const int n0 = ti.n0, N = p.N, I = p.inter;
+    const int64_t ldb = p.ldb;
+    if constexpr (EPI == EPI_SWIGLU) {
+      // Block column c -> B row: each wave's WN columns are WN/2 gate rows then
+      // the WN/2 matching up rows (offset I), so one lane holds both halves.
+      sb.init([&](int c) -> const TB* {
+        int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
+        int gcol = n0 + w * h + (cc % h);
+        if (gcol >= I) return nullptr;
+        int row = (cc < h) ? gcol : I + gcol;
+        return B + (int64_t)row * ldb;
+      }, tid);
+    } else {
+      sb.init([&](int c) -> const TB* { return (n0 + c < N) ? B + (int64_t)(n0 + c) * ldb : nullptr; }, tid);
+    }
+  } else {
+    sb.init(B, p.ldb, ti.n0, p.N);
+  }
+
+  f32x16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int klen = ti.k_hi - ti.k_lo;
+  const int nk = klen > 0 ? (klen + BK - 1) / BK : 0;
+
+  if (nk > 0) {
+    sa.load(ti.k_lo, ti.k_hi, tid);
+    sb.load(ti.k_lo, ti.k_hi, tid);
+    sa.store(lds, tid);
+    sb.store(lds + BM * LDK, tid);
+  }
+  __syncthreads();
+
+  const int frag_row = lane & 31;
+  const int frag_k = (lane >> 5) * MF::KPACK;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      sa.load(ti.k_lo + (kt + 1) * BK, ti.k_hi, tid);
+      sb.load(ti.k_lo + (kt + 1) * BK, ti.k_hi, tid);
+    }
+    const Tc* a_base = lds + cur * Cfg::STAGE_ELEMS + (wm * Cfg::WM + frag_row) * LDK + frag_k;
+    const Tc* b_base = lds + cur * Cfg::STAGE_ELEMS + BM * LDK + (wn * Cfg::WN + frag_row) * LDK + frag_k;
+#pragma unroll
+    for (int ks = 0; ks < BK / MF::MK; ++ks) {
+      typename MF::frag_t af[MI], bf[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = MF::load(a_base + i * 32 * LDK + ks * MF::MK);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bf[j] = MF::load(b_base + j * 32 * LDK + ks * MF::MK);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = MF::mma(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) {
+      sa.store(lds + (cur ^ 1) * Cfg::STAGE_ELEMS, tid);
+      sb.store(lds + (cur ^ 1) * Cfg::STAGE_ELEMS + BM * LDK, tid);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: stage each 32-row slab of the wave tile through LDS as fp32
+  store_tile<Cfg, Tout, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
+}
+
+// ------------------------------------------------------------- launchers ----
+
+inline GemmParams zero_params() {
+  GemmParams p;
+  p.A = nullptr; p.lda = 0;
+  p.B = nullptr; p.ldb = 0; p.strideB = 0;
+  p.C = nullptr; p.ldc = 0; p.strideC = 0;
+  p.C2 = nullptr; p.ldc2 = 0;
+  p.aux = nullptr; p.ldaux = 0;
+  p.offs = nullptr; p.groups = 1;
+  p.M = p.N = p.K = 0; p.split_chunk = 0; p.inter = 0;
+  p.a_bytes = p.b_bytes = 0;
+  return p;
+}
+
+template <class Cfg, typename TA, typename TB, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
+hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
+  const int ntn = (EPI == EPI_SWIGLU) ? (p.inter + Cfg::BN / 2 - 1) / (Cfg::BN / 2) : (p.N + Cfg::BN - 1) / Cfg::BN;
+  int64_t slots;
+  if (GM == GM_ROWS) slots = (p.M + Cfg::BM - 1) / Cfg::BM + p.groups;
+  else if (GM == GM_RED) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);
+  else slots = (p.M + Cfg::BM - 1) / Cfg::BM;
+  const int64_t grid = slots * ntn;
+  if (grid <= 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((grouped_gemm_kernel<Cfg, TA, TB, Tout, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid),
+                     dim3(Cfg::NT), 0, s, p);
+  return hipGetLastError();
+}
+
+// The six grouped GEMMs of the expert FFN (forward, dgrad, wgrad of gate_up and down).
+enum ExpertGemm {
+  EG_GATE_UP_FWD = 0,  // gu, mid <- x_perm . W_gu[e]^T, SwiGLU epilogue
+  EG_DOWN_FWD = 1,     // y <- mid . W_dn[e]^T
+  EG_DOWN_DGRAD = 2,   // dgu <- SwiGLU'(gu) * (dy . W_dn[e])
+  EG_DOWN_WGRAD = 3,   // dW_dn[e] <- dy_e^T . mid_e
+  EG_GATE_UP_DGRAD = 4,  // dx_perm <- dgu . W_gu[e]
+  EG_GATE_UP_WGRAD = 5,  // dW_gu[e] <- dgu_e^T . x_perm_e
+};
+
+// Problem description of one expert GEMM. A, B: operands as listed above;
+// aux: gu for EG_DOWN_DGRAD; C2: mid for EG_GATE_UP_FWD.
+template <typename T>
+GemmParams expert_params(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P,
+                         int E, int H, int I) {
+  GemmParams p = zero_params();
+  const uint64_t es = sizeof(T);
+  p.offs = offs;
+  p.groups = E;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  switch (kind) {
+    case EG_GATE_UP_FWD:
+      p.lda = H; p.ldb = H; p.strideB = (int64_t)2 * I * H;
+      p.ldc = 2 * I; p.C2 = C2; p.ldc2 = I;
+      p.M = P; p.N = 2 * I; p.K = H; p.inter = I;
+      p.a_bytes = (uint64_t)P * H * es; p.b_bytes = (uint64_t)2 * I * H * es;
+      break;
+    case EG_DOWN_FWD:
+      p.lda = I; p.ldb = I; p.strideB = (int64_t)H * I;
+      p.ldc = H;
+      p.M = P; p.N = H; p.K = I;
+      p.a_bytes = (uint64_t)P * I * es; p.b_bytes = (uint64_t)H * I * es;
+      break;
+    case EG_DOWN_DGRAD:  // B[k=h][n=i] = W_dn[e][h][i]
+      p.lda = H; p.ldb = I; p.strideB = (int64_t)H * I;
+      p.ldc = 2 * I; p.aux = aux; p.ldaux = 2 * I;
+      p.M = P; p.N = I; p.K = H; p.inter = I;
+      p.a_bytes = (uint64_t)P * H * es; p.b_bytes = (uint64_t)H * I * es;
+      break;
+    case EG_DOWN_WGRAD:  // A[m=h][k=p] = dy[p][h], B[k=p][n=i] = mid[p][i]
+      p.lda = H; p.ldb = I;
+      p.ldc = I; p.strideC = (int64_t)H * I;
+      p.M = H; p.N = I; p.K = P;
+      p.a_bytes = (uint64_t)P * H * es; p.b_bytes = (uint64_t)P * I * es;
+      break;
+    case EG_GATE_UP_DGRAD:  // B[k=j][n=h] = W_gu[e][j][h]
+      p.lda = 2 * I; p.ldb = H; p.strideB = (int64_t)2 * I * H;
+      p.ldc = H;
+      p.M = P; p.N = H; p.K = 2 * I;
+      p.a_bytes = (uint64_t)P * 2 * I * es; p.b_bytes = (uint64_t)2 * I * H * es;
+      break;
+    case EG_GATE_UP_WGRAD:  // A[m=j][k=p] = dgu[p][j], B[k=p][n=h] = x_perm[p][h]
+      p.lda = 2 * I; p.ldb = H;
+      p.ldc = H; p.strideC = (int64_t)2 * I * H;
+      p.M = 2 * I; p.N = H; p.K = P;
+      p.a_bytes = (uint64_t)P * 2 * I * es; p.b_bytes = (uint64_t)P * H * es;
+      break;
+  }
+  return p;
+}
+
+template <class Cfg, typename T>
+hipError_t expert_gemm(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P,
+                       int E, int H, int I, hipStream_t s) {
+  const GemmParams p = expert_params<T>(kind, A, B, aux, C, C2, offs, P, E, H, I);
+  switch (kind) {
+    case EG_GATE_UP_FWD: return launch_gemm<Cfg, T, T, T, true, true, GM_ROWS, EPI_SWIGLU>(p, s);
+    case EG_DOWN_FWD: return launch_gemm<Cfg, T, T, T, true, true, GM_ROWS, EPI_STORE>(p, s);
+    case EG_DOWN_DGRAD: return launch_gemm<Cfg, T, T, T, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, s);
+    case EG_DOWN_WGRAD: return launch_gemm<Cfg, T, T, T, false, false, GM_RED, EPI_STORE>(p, s);
+    case EG_GATE_UP_DGRAD: return launch_gemm<Cfg, T, T, T, true, false, GM_ROWS, EPI_STORE>(p, s);
+    case EG_GATE_UP_WGRAD: return launch_gemm<Cfg, T, T, T, false, false, GM_RED, EPI_STORE>(p, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace pmoe

@@ -1,13 +1,13 @@
 // Launchers of the grouped expert GEMMs and the router GEMMs.
-#include "gemm.h"
+#include "gemm_dma.h"
 #include "kernels.h"
 
 namespace pmoe {
 
 namespace {
 
-// Tile shapes. bf16: 128x128 block, four 64x64 wave tiles of 2x2 MFMA 32x32x16.
-// fp32: 64x128 block, four 32x64 wave tiles of MFMA 32x32x2.
+// Tile shapes of the register-staged engine: fp32 (MFMA 32x32x2) uses 64x128
+// blocks of four 32x64 wave tiles.
 typedef TileCfg<bf16_t, 128, 128, 64, 64> CfgBf16;
 typedef TileCfg<float, 64, 128, 32, 64> CfgF32;
 
@@ -15,31 +15,23 @@ template <typename T> struct CfgFor;
 template <> struct CfgFor<bf16_t> { typedef CfgBf16 type; };
 template <> struct CfgFor<float> { typedef CfgF32 type; };
 
-template <class Cfg, typename TA, typename TB, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
-hipError_t launch(const GemmParams& p, hipStream_t s) {
-  const int ntn = (EPI == EPI_SWIGLU) ? (p.inter + Cfg::BN / 2 - 1) / (Cfg::BN / 2) : (p.N + Cfg::BN - 1) / Cfg::BN;
-  int64_t slots;
-  if (GM == GM_ROWS) slots = (p.M + Cfg::BM - 1) / Cfg::BM + p.groups;
-  else if (GM == GM_RED) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);
-  else slots = (p.M + Cfg::BM - 1) / Cfg::BM;
-  const int64_t grid = slots * ntn;
-  if (grid <= 0) return hipSuccess;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((grouped_gemm_kernel<Cfg, TA, TB, Tout, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid),
-                     dim3(Cfg::NT), 0, s, p);
-  return hipGetLastError();
-}
+// bf16 expert GEMMs run on the DMA engine. Two tilings, chosen per GEMM from
+// measurements at the Qwen3-30B-A3B shape: 256x256 blocks of eight 128x64 wave
+// tiles (one block per CU), or 128x128 blocks of four 64x64 wave tiles (two
+// blocks per CU); both double-buffer 64-deep k stages in LDS.
+typedef DmaCfg<256, 256, 128, 64, 2> DmaBig;
+typedef DmaCfg<128, 128, 64, 64, 2> DmaSmall;
 
-GemmParams zero_params() {
-  GemmParams p;
-  p.A = nullptr; p.lda = 0;
-  p.B = nullptr; p.ldb = 0; p.strideB = 0;
-  p.C = nullptr; p.ldc = 0; p.strideC = 0;
-  p.C2 = nullptr; p.ldc2 = 0;
-  p.aux = nullptr; p.ldaux = 0;
-  p.offs = nullptr; p.groups = 1;
-  p.M = p.N = p.K = 0; p.split_chunk = 0; p.inter = 0;
-  return p;
+template <typename T>
+hipError_t run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P, int E, int H,
+               int I, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    if (kind == EG_GATE_UP_FWD || kind == EG_DOWN_DGRAD)
+      return expert_gemm_dma<DmaSmall>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+    return expert_gemm_dma<DmaBig>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+  } else {
+    return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+  }
 }
 
 }  // namespace
@@ -47,75 +39,37 @@ GemmParams zero_params() {
 template <typename T>
 hipError_t gate_up_swiglu_fwd(const T* x_perm, const T* w_gu, const int32_t* offs, int P, int E, int H, int I,
                               T* gu_out, T* mid, hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = x_perm; p.lda = H;
-  p.B = w_gu; p.ldb = H; p.strideB = (int64_t)2 * I * H;
-  p.C = gu_out; p.ldc = 2 * I;
-  p.C2 = mid; p.ldc2 = I;
-  p.offs = offs; p.groups = E;
-  p.M = P; p.N = 2 * I; p.K = H; p.inter = I;
-  return launch<typename CfgFor<T>::type, T, T, T, true, true, GM_ROWS, EPI_SWIGLU>(p, s);
+  return run<T>(EG_GATE_UP_FWD, x_perm, w_gu, nullptr, gu_out, mid, offs, P, E, H, I, s);
 }
 
 template <typename T>
 hipError_t down_fwd(const T* mid, const T* w_dn, const int32_t* offs, int P, int E, int H, int I, T* y,
                     hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = mid; p.lda = I;
-  p.B = w_dn; p.ldb = I; p.strideB = (int64_t)H * I;
-  p.C = y; p.ldc = H;
-  p.offs = offs; p.groups = E;
-  p.M = P; p.N = H; p.K = I;
-  return launch<typename CfgFor<T>::type, T, T, T, true, true, GM_ROWS, EPI_STORE>(p, s);
+  return run<T>(EG_DOWN_FWD, mid, w_dn, nullptr, y, nullptr, offs, P, E, H, I, s);
 }
 
 template <typename T>
 hipError_t down_dgrad_swiglu_bwd(const T* dy, const T* w_dn, const T* gu_out, const int32_t* offs, int P, int E,
                                  int H, int I, T* dgu, hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = dy; p.lda = H;
-  p.B = w_dn; p.ldb = I; p.strideB = (int64_t)H * I;  // B[k=h][n=i] = W_dn[e][h][i]
-  p.C = dgu; p.ldc = 2 * I;
-  p.aux = gu_out; p.ldaux = 2 * I;
-  p.offs = offs; p.groups = E;
-  p.M = P; p.N = I; p.K = H; p.inter = I;
-  return launch<typename CfgFor<T>::type, T, T, T, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, s);
+  return run<T>(EG_DOWN_DGRAD, dy, w_dn, gu_out, dgu, nullptr, offs, P, E, H, I, s);
 }
 
 template <typename T>
 hipError_t down_wgrad(const T* dy, const T* mid, const int32_t* offs, int P, int E, int H, int I, T* dw_dn,
                       hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = dy; p.lda = H;   // A[m=h][k=p] = dy[p][h]
-  p.B = mid; p.ldb = I;  // B[k=p][n=i] = mid[p][i]
-  p.C = dw_dn; p.ldc = I; p.strideC = (int64_t)H * I;
-  p.offs = offs; p.groups = E;
-  p.M = H; p.N = I; p.K = P;
-  return launch<typename CfgFor<T>::type, T, T, T, false, false, GM_RED, EPI_STORE>(p, s);
+  return run<T>(EG_DOWN_WGRAD, dy, mid, nullptr, dw_dn, nullptr, offs, P, E, H, I, s);
 }
 
 template <typename T>
 hipError_t gate_up_dgrad(const T* dgu, const T* w_gu, const int32_t* offs, int P, int E, int H, int I, T* dx_perm,
                          hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = dgu; p.lda = 2 * I;
-  p.B = w_gu; p.ldb = H; p.strideB = (int64_t)2 * I * H;  // B[k=j][n=h] = W_gu[e][j][h]
-  p.C = dx_perm; p.ldc = H;
-  p.offs = offs; p.groups = E;
-  p.M = P; p.N = H; p.K = 2 * I;
-  return launch<typename CfgFor<T>::type, T, T, T, true, false, GM_ROWS, EPI_STORE>(p, s);
+  return run<T>(EG_GATE_UP_DGRAD, dgu, w_gu, nullptr, dx_perm, nullptr, offs, P, E, H, I, s);
 }
 
 template <typename T>
 hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int P, int E, int H, int I, T* dw_gu,
                          hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = dgu; p.lda = 2 * I;  // A[m=j][k=p] = dgu[p][j]
-  p.B = x_perm; p.ldb = H;   // B[k=p][n=h] = x_perm[p][h]
-  p.C = dw_gu; p.ldc = H; p.strideC = (int64_t)2 * I * H;
-  p.offs = offs; p.groups = E;
-  p.M = 2 * I; p.N = H; p.K = P;
-  return launch<typename CfgFor<T>::type, T, T, T, false, false, GM_RED, EPI_STORE>(p, s);
+  return run<T>(EG_GATE_UP_WGRAD, dgu, x_perm, nullptr, dw_gu, nullptr, offs, P, E, H, I, s);
 }
 
 template <typename TX, typename TW>
@@ -125,7 +79,7 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
   p.B = w; p.ldb = H;
   p.C = logits; p.ldc = E;
   p.M = T; p.N = E; p.K = H;
-  return launch<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
+  return launch_gemm<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
 }
 
 template <typename TX, typename TW>
@@ -135,7 +89,7 @@ hipError_t router_dx_gemm(const float* dl, int ldl, const TW* w, int T, int H, i
   p.B = w; p.ldb = H;  // B[k=e][n=h] = W[e][h]
   p.C = dx; p.ldc = H;
   p.M = T; p.N = H; p.K = E;
-  return launch<CfgF32, float, TW, TX, true, false, GM_NONE, EPI_STORE>(p, s);
+  return launch_gemm<CfgF32, float, TW, TX, true, false, GM_NONE, EPI_STORE>(p, s);
 }
 
 template <typename TX>
@@ -147,7 +101,7 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
   p.C = partial; p.ldc = H; p.strideC = (int64_t)E * H;
   p.offs = nullptr; p.split_chunk = split_chunk; p.groups = (T + split_chunk - 1) / split_chunk;
   p.M = E; p.N = H; p.K = T;
-  return launch<CfgF32, float, TX, float, false, false, GM_RED, EPI_STORE>(p, s);
+  return launch_gemm<CfgF32, float, TX, float, false, false, GM_RED, EPI_STORE>(p, s);
 }
 
 #define PMOE_INST_EXPERT(T)                                                                                      \
