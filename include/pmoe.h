@@ -44,7 +44,8 @@ PMOE_API const char* pmoe_last_error_string(void);
 
 /* ---------------------------------------------------------------- router ---
  * Replaces Qwen3MoeTopKRouter.forward (pluggy/models/qwen3_moe/qwen3_moe.py:168-178):
- *   logits = x . W^T (+ logit_bias)  [fp32 arithmetic]
+ *   logits = x . W^T (+ logit_bias)  [fp32 arithmetic; for bf16 x the fp32 W is
+ *   split into three bf16 pieces whose products with x are exact]
  *   p = softmax(logits) (fp32); top-k of logits (ties -> lower expert id)
  *   w = p[top] (/ sum p[top] when norm_topk_prob), written as tw_dtype and fp32.
  * Also emits the additive aux statistics of load_balancing_loss / router_z_loss
@@ -54,7 +55,7 @@ PMOE_API const char* pmoe_last_error_string(void);
  * x: (T,H) x_dtype; weight: (E,H) w_dtype; logit_bias: (E,) fp32 or NULL;
  * logits: (T,E) fp32; top_weights: (T,K) tw_dtype; top_indices: (T,K) int64;
  * top_weights_f32: (T,K) fp32 (kept for the backward). */
-PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t E);
+PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E);
 PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
                                  const float* logit_bias, int64_t T, int64_t H, int64_t E, int64_t K,
                                  int norm_topk_prob, float* logits, void* top_weights, int tw_dtype,

@@ -26,7 +26,7 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "pmoe_version": (ctypes.c_char_p, []),
     "pmoe_last_error_string": (ctypes.c_char_p, []),
-    "pmoe_router_forward_workspace_size": (_SZ, [_I64, _I64]),
+    "pmoe_router_forward_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_router_forward": (_INT, [_P, _INT, _P, _INT, _P, _I64, _I64, _I64, _I64, _INT, _P, _P, _INT, _P, _P, _P,
                                    _P, _P, _P, _SZ, _P]),
     "pmoe_router_backward_workspace_size": (_SZ, [_I64, _I64, _I64]),

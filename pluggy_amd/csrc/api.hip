@@ -87,9 +87,10 @@ PMOE_API const char* pmoe_last_error_string(void) { return g_err; }
 
 // ------------------------------------------------------------------ router
 
-PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t E) {
+PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E) {
   const int64_t nb = router_blocks(T);
-  return align_up(nb * E * sizeof(float)) + align_up(nb * E * sizeof(int)) + align_up(nb * sizeof(float));
+  return align_up(nb * E * sizeof(float)) + align_up(nb * E * sizeof(int)) + align_up(nb * sizeof(float)) +
+         align_up(3 * E * H * sizeof(bf16_t)) + align_up(3 * T * E * sizeof(float));
 }
 
 PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
@@ -102,35 +103,51 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(tw_dtype), "unknown dtype code");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_weights && top_indices && top_weights_f32),
                "router_forward: null tensor");
-  const size_t need = pmoe_router_forward_workspace_size(T, E);
+  const size_t need = pmoe_router_forward_workspace_size(T, H, E);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(PMOE_ERR_WORKSPACE, "router_forward: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   const int t = (int)T, h = (int)H, e = (int)E, k = (int)K;
-  if (T > 0) {
-    hipError_t st;
-    if (x_dtype == PMOE_BF16 && w_dtype == PMOE_F32)
-      st = router_logits_gemm<bf16_t, float>((const bf16_t*)x, (const float*)weight, t, h, e, logits, s);
-    else if (x_dtype == PMOE_BF16)
-      st = router_logits_gemm<bf16_t, bf16_t>((const bf16_t*)x, (const bf16_t*)weight, t, h, e, logits, s);
-    else if (w_dtype == PMOE_F32)
-      st = router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s);
-    else
-      st = router_logits_gemm<float, bf16_t>((const float*)x, (const bf16_t*)weight, t, h, e, logits, s);
-    PMOE_TRY(st, "router logits GEMM");
-  }
   Carver cv(workspace);
   const int64_t nb = router_blocks(T);
   float* blk_psum = cv.take<float>(nb * E);
   int* blk_cnt = cv.take<int>(nb * E);
   float* blk_lse2 = cv.take<float>(nb);
+  bf16_t* w3 = cv.take<bf16_t>(3 * E * H);
+  float* parts = cv.take<float>(3 * T * E);
+  // Logits in fp32 arithmetic. bf16 x: x is exact in bf16, so splitting an fp32
+  // weight into three bf16 pieces makes every MFMA product exact; the three
+  // fp32 partials are summed in a fixed order by the top-k kernel.
+  const float* lparts = logits;
+  int nparts = 1;
+  int64_t pstride = 0;
   if (T > 0) {
+    if (x_dtype == PMOE_BF16) {
+      const bf16_t* wb = (const bf16_t*)weight;
+      nparts = 1;
+      if (w_dtype == PMOE_F32) {
+        PMOE_TRY(split_bf16x3((const float*)weight, E * H, w3, s), "router weight split");
+        wb = w3;
+        nparts = 3;
+      }
+      PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, nparts, t, h, e, parts, s), "router logits GEMM");
+      lparts = parts;
+      pstride = T * E;
+    } else {
+      hipError_t st = w_dtype == PMOE_F32
+                          ? router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s)
+                          : router_logits_gemm<float, bf16_t>((const float*)x, (const bf16_t*)weight, t, h, e, logits,
+                                                              s);
+      PMOE_TRY(st, "router logits GEMM");
+    }
     hipError_t st =
         tw_dtype == PMOE_BF16
-            ? router_topk<bf16_t>(logits, logit_bias, t, e, k, norm_topk_prob, (bf16_t*)top_weights, top_indices,
-                                  top_weights_f32, blk_psum, blk_lse2, blk_cnt, kRouterRowsPerBlock, s)
-            : router_topk<float>(logits, logit_bias, t, e, k, norm_topk_prob, (float*)top_weights, top_indices,
-                                 top_weights_f32, blk_psum, blk_lse2, blk_cnt, kRouterRowsPerBlock, s);
+            ? router_topk<bf16_t>(lparts, nparts, pstride, logits, logit_bias, t, e, k, norm_topk_prob,
+                                  (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
+                                  kRouterRowsPerBlock, s)
+            : router_topk<float>(lparts, nparts, pstride, logits, logit_bias, t, e, k, norm_topk_prob,
+                                 (float*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
+                                 kRouterRowsPerBlock, s);
     PMOE_TRY(st, "router top-k");
   }
   if (expert_counts || prob_sum || lse_sq_sum)
@@ -140,7 +157,11 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
 }
 
 PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E) {
-  return align_up(T * ldl_of(E) * sizeof(float)) + align_up(router_splits(T) * E * H * sizeof(float));
+  const int64_t ldl = ldl_of(E);
+  const size_t fp32_path = align_up(T * ldl * sizeof(float)) + align_up(router_splits(T) * E * H * sizeof(float));
+  const size_t bf16_path = align_up(T * 3 * ldl * sizeof(bf16_t)) + align_up(3 * ldl * H * sizeof(bf16_t)) +
+                           align_up(2 * router_splits(T) * E * H * sizeof(float));
+  return std::max(fp32_path, bf16_path);
 }
 
 PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
@@ -158,43 +179,64 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
   hipStream_t s = as_stream(stream);
   const int t = (int)T, h = (int)H, e = (int)E, k = (int)K;
   const int ldl = (int)ldl_of(E);
+  const int splits = (int)router_splits(T);
   Carver cv(workspace);
-  float* dl = cv.take<float>((size_t)T * ldl);
-  float* partial = cv.take<float>((size_t)router_splits(T) * E * H);
-  if (T > 0) {
-    hipError_t st = gw_dtype == PMOE_BF16
-                        ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32,
-                                                 (const bf16_t*)grad_top_weights, grad_logits, t, e, k,
-                                                 norm_topk_prob, dl, ldl, s)
-                        : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
-                                                grad_logits, t, e, k, norm_topk_prob, dl, ldl, s);
-    PMOE_TRY(st, "router dlogits");
+  if (T == 0) {
+    if (grad_weight) {
+      float* zero = cv.take<float>((size_t)E * H);
+      PMOE_TRY(hipMemsetAsync(zero, 0, (size_t)E * H * sizeof(float), s), "router dW zero");
+      hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(zero, 1, E * H, (bf16_t*)grad_weight, s)
+                                           : reduce_partials<float>(zero, 1, E * H, (float*)grad_weight, s);
+      PMOE_TRY(st, "router dW reduce");
+    }
+    return PMOE_OK;
   }
-  if (grad_x && T > 0) {
-    hipError_t st;
-    if (x_dtype == PMOE_BF16 && w_dtype == PMOE_F32)
-      st = router_dx_gemm<bf16_t, float>(dl, ldl, (const float*)weight, t, h, e, (bf16_t*)grad_x, s);
-    else if (x_dtype == PMOE_BF16)
-      st = router_dx_gemm<bf16_t, bf16_t>(dl, ldl, (const bf16_t*)weight, t, h, e, (bf16_t*)grad_x, s);
-    else if (w_dtype == PMOE_F32)
-      st = router_dx_gemm<float, float>(dl, ldl, (const float*)weight, t, h, e, (float*)grad_x, s);
-    else
-      st = router_dx_gemm<float, bf16_t>(dl, ldl, (const bf16_t*)weight, t, h, e, (float*)grad_x, s);
+  if (x_dtype == PMOE_BF16) {
+    // bf16 x: dl is split into bf16 planes hi + lo; dx = [hi|lo|hi].[W_hi;W_hi;W_lo]
+    // and dW = hi^T x + lo^T x, all products exact, fp32 accumulation.
+    bf16_t* dl3 = cv.take<bf16_t>((size_t)T * 3 * ldl);
+    bf16_t* w3t = cv.take<bf16_t>((size_t)3 * ldl * H);
+    float* partial = cv.take<float>((size_t)2 * splits * E * H);
+    hipError_t st = gw_dtype == PMOE_BF16
+                        ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32, (const bf16_t*)grad_top_weights,
+                                                 grad_logits, t, e, k, norm_topk_prob, nullptr, dl3, ldl, s)
+                        : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
+                                                grad_logits, t, e, k, norm_topk_prob, nullptr, dl3, ldl, s);
+    PMOE_TRY(st, "router dlogits");
+    if (grad_x) {
+      st = w_dtype == PMOE_F32 ? split_router_weight_bwd<float>((const float*)weight, e, h, ldl, w3t, s)
+                               : split_router_weight_bwd<bf16_t>((const bf16_t*)weight, e, h, ldl, w3t, s);
+      PMOE_TRY(st, "router weight split");
+      PMOE_TRY(router_dx_bf16(dl3, ldl, w3t, t, h, (bf16_t*)grad_x, s), "router dx GEMM");
+    }
+    if (grad_weight) {
+      PMOE_TRY(router_dw_bf16(dl3, ldl, (const bf16_t*)x, t, h, e, kRouterSplitChunk, partial, s), "router dW GEMM");
+      st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(partial, 2 * splits, E * H, (bf16_t*)grad_weight, s)
+                                : reduce_partials<float>(partial, 2 * splits, E * H, (float*)grad_weight, s);
+      PMOE_TRY(st, "router dW reduce");
+    }
+    return PMOE_OK;
+  }
+  // fp32 x: fp32 MFMA GEMMs on the fp32 dl
+  float* dl = cv.take<float>((size_t)T * ldl);
+  float* partial = cv.take<float>((size_t)splits * E * H);
+  hipError_t st = gw_dtype == PMOE_BF16
+                      ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32, (const bf16_t*)grad_top_weights,
+                                               grad_logits, t, e, k, norm_topk_prob, dl, nullptr, ldl, s)
+                      : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
+                                              grad_logits, t, e, k, norm_topk_prob, dl, nullptr, ldl, s);
+  PMOE_TRY(st, "router dlogits");
+  if (grad_x) {
+    st = w_dtype == PMOE_F32
+             ? router_dx_gemm<float, float>(dl, ldl, (const float*)weight, t, h, e, (float*)grad_x, s)
+             : router_dx_gemm<float, bf16_t>(dl, ldl, (const bf16_t*)weight, t, h, e, (float*)grad_x, s);
     PMOE_TRY(st, "router dx GEMM");
   }
   if (grad_weight) {
-    const int splits = (int)router_splits(T);
-    if (T > 0) {
-      hipError_t st = x_dtype == PMOE_BF16
-                          ? router_dw_gemm<bf16_t>(dl, ldl, (const bf16_t*)x, t, h, e, kRouterSplitChunk, partial, s)
-                          : router_dw_gemm<float>(dl, ldl, (const float*)x, t, h, e, kRouterSplitChunk, partial, s);
-      PMOE_TRY(st, "router dW GEMM");
-    } else {
-      PMOE_TRY(hipMemsetAsync(partial, 0, (size_t)E * H * sizeof(float), s), "router dW zero");
-    }
-    const int used = T > 0 ? splits : 1;
-    hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(partial, used, E * H, (bf16_t*)grad_weight, s)
-                                         : reduce_partials<float>(partial, used, E * H, (float*)grad_weight, s);
+    PMOE_TRY(router_dw_gemm<float>(dl, ldl, (const float*)x, t, h, e, kRouterSplitChunk, partial, s),
+             "router dW GEMM");
+    st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(partial, splits, E * H, (bf16_t*)grad_weight, s)
+                              : reduce_partials<float>(partial, splits, E * H, (float*)grad_weight, s);
     PMOE_TRY(st, "router dW reduce");
   }
   return PMOE_OK;

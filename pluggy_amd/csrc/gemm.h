@@ -21,7 +21,7 @@
 
 namespace pmoe {
 
-enum GroupMode { GM_NONE = 0, GM_ROWS = 1, GM_RED = 2 };
+enum GroupMode { GM_NONE = 0, GM_ROWS = 1, GM_RED = 2, GM_BATCH = 3 };  // GM_BATCH: shared A, B and C per group
 enum EpiKind { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2 };
 
 template <typename Tc> struct Mfma;
@@ -249,6 +249,8 @@ struct GemmParams {
   int inter;            // SwiGLU: I (columns of gate; up starts at I)
   uint64_t a_bytes;     // extent of A's storage (from A), and of one group's B (from B + g*strideB)
   uint64_t b_bytes;
+  int planes;           // GM_RED uniform split: groups = planes * splits, plane g / splits reads A + plane * strideA
+  int64_t strideA;
 };
 
 struct TileInfo {
@@ -309,7 +311,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Cfg::MI][Cfg::NI]
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   float* stage = smem_f + wave * 32 * Cfg::EPI_LD;
   Tout* C = reinterpret_cast<Tout*>(p.C);
-  if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
+  if constexpr (GM == GM_RED || GM == GM_BATCH) C += (int64_t)ti.group * p.strideC;
   constexpr int WN = Cfg::WN;
 
 #pragma unroll
@@ -536,6 +538,7 @@ inline GemmParams zero_params() {
   p.offs = nullptr; p.groups = 1;
   p.M = p.N = p.K = 0; p.split_chunk = 0; p.inter = 0;
   p.a_bytes = p.b_bytes = 0;
+  p.planes = 1; p.strideA = 0;
   return p;
 }
 

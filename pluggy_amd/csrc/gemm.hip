@@ -82,6 +82,47 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
   return launch_gemm<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
 }
 
+// Router logits from bf16 pieces of the router weight on the DMA engine: one
+// batched GEMM (64x128 blocks, four 32x64 wave tiles) per piece, fp32 out.
+hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
+                                     float* parts, hipStream_t s) {
+  GemmParams p = zero_params();
+  p.A = x; p.lda = H;
+  p.B = w3; p.ldb = H; p.strideB = (int64_t)E * H;
+  p.C = parts; p.ldc = E; p.strideC = (int64_t)T * E;
+  p.groups = npieces;
+  p.M = T; p.N = E; p.K = H;
+  p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)E * H * 2;
+  return launch_gemm_dma<DmaCfg<64, 128, 32, 64, 2>, true, true, GM_BATCH, EPI_STORE, float>(p, s);
+}
+
+// Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
+// (T, 3*ldl), w3t = [W_hi; W_hi; W_lo] (3*ldl, H).
+hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s) {
+  GemmParams p = zero_params();
+  p.A = dl3; p.lda = 3 * ldl;
+  p.B = w3t; p.ldb = H;  // B[k][n=h]
+  p.C = dx; p.ldc = H;
+  p.M = T; p.N = H; p.K = 3 * ldl;
+  p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)3 * ldl * H * 2;
+  return launch_gemm_dma<DmaCfg<128, 128, 64, 64, 2>, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
+}
+
+// partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and
+// lo planes of dl3 -> (2 * splits, E, H) fp32.
+hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, int H, int E, int split_chunk,
+                          float* partial, hipStream_t s) {
+  GemmParams p = zero_params();
+  p.A = dl3; p.lda = 3 * ldl;  // A[m=e][k=t] = dl_plane[t][e]
+  p.B = x; p.ldb = H;          // B[k=t][n=h]
+  p.C = partial; p.ldc = H; p.strideC = (int64_t)E * H;
+  const int splits = (T + split_chunk - 1) / split_chunk;
+  p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
+  p.M = E; p.N = H; p.K = T;
+  p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
+  return launch_gemm_dma<DmaCfg<128, 128, 64, 64, 2>, false, false, GM_RED, EPI_STORE, float>(p, s);
+}
+
 template <typename TX, typename TW>
 hipError_t router_dx_gemm(const float* dl, int ldl, const TW* w, int T, int H, int E, TX* dx, hipStream_t s) {
   GemmParams p = zero_params();

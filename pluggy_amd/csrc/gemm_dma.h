@@ -48,7 +48,6 @@ struct DmaCfg {
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % WM == 0 && BN % WN == 0, "tile shape");
   static_assert(A_INSTR * NW * 8 == BM && B_INSTR * NW * 8 == BN, "DMA instructions must divide among waves");
   static_assert(NS >= 2, "at least double buffering");
-  static_assert(BM >= 128 && BN >= 128, "[k][r] swizzle needs 16 chunks per row");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -142,6 +141,7 @@ __device__ __forceinline__ bf16x8 kc_frag(const char* tile, int r, int c) {
 // [k][r] operand: 64 k-rows x R columns per stage.
 template <int R, int NW>
 struct TDma {
+  static_assert(R >= 128, "[k][r] swizzle needs 16 chunks per row");
   static constexpr int CPR = R / 8;       // 16-byte chunks per k-row
   static constexpr int KPI = 64 / CPR;    // k-rows per 1 KB instruction
   static constexpr int INSTR = R / 8 / NW;
@@ -196,7 +196,7 @@ __device__ __forceinline__ int xcd_remap(int b, int grid) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
 }
 
-template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI>
+template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
 __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW, NS = Cfg::NS;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
@@ -232,9 +232,17 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p)
       ti.k_lo = g == 0 ? 0 : p.offs[g - 1];
       ti.k_hi = p.offs[g];
     } else {
-      ti.k_lo = g * p.split_chunk;
+      const int splits = p.groups / p.planes;
+      A += (int64_t)(g / splits) * p.strideA;
+      ti.k_lo = (g % splits) * p.split_chunk;
       ti.k_hi = min(p.K, ti.k_lo + p.split_chunk);
     }
+  } else if constexpr (GM == GM_BATCH) {
+    const int mt = (p.M + BM - 1) / BM;
+    const int g = slot / mt;
+    if (g >= p.groups) return;
+    ti.group = g; ti.m0 = (slot % mt) * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
+    B += (int64_t)g * p.strideB;
   } else {
     ti.group = 0; ti.m0 = slot * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
     if (ti.m0 >= p.M) return;
@@ -313,50 +321,72 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p)
     if (s < nk) issue(s);
 
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
+  // Fragments of k-substep ks (16 deep) of the stage at sa / sb.
+  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      if constexpr (A_KC) af[i] = kc_frag(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      if constexpr (B_KC) bfr[j] = kc_frag(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
+    }
+  };
+  constexpr int KS = Cfg::BK / 16;
+  // LDS reads per substep (a [k][r] fragment takes two transposing reads)
+  constexpr int NREAD = MI * (A_KC ? 1 : 2) + NI * (B_KC ? 1 : 2);
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * Cfg::D>();
     else wait_vmcnt<0>();
     lds_barrier();
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
     const char* sa = smem + (kt % NS) * Cfg::STAGE_BYTES;
     const char* sb = sa + Cfg::A_BYTES;
+    // Software pipeline over the substeps: the fragments of substep ks + 1 are
+    // read while the MFMAs of substep ks run. The first reads go out ahead of
+    // the next stage's DMA issue so their latency overlaps it.
+    bf16x8 af[2][MI], bfr[2][NI];
+    load_frags(sa, sb, 0, af[0], bfr[0]);
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
 #pragma unroll
-    for (int ks = 0; ks < Cfg::BK / 16; ++ks) {
-      bf16x8 af[MI], bfr[NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        if constexpr (A_KC) af[i] = kc_frag(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
-        else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
-      }
-#pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        if constexpr (B_KC) bfr[j] = kc_frag(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
-        else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KS) load_frags(sa, sb, ks + 1, af[cur ^ 1], bfr[cur ^ 1]);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+      if (ks + 1 < KS) {
+        // interleave: one LDS read, one MFMA, ...; remaining MFMAs after
+#pragma unroll
+        for (int q = 0; q < (NREAD < MI * NI ? NREAD : MI * NI); ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+        if constexpr (NREAD < MI * NI) __builtin_amdgcn_sched_group_barrier(0x008, MI * NI - NREAD, 0);
+        else if constexpr (NREAD > MI * NI) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - MI * NI, 0);
+      }
     }
   }
   wait_vmcnt<0>();
   lds_barrier();
-  store_tile<Cfg, bf16_t, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
+  store_tile<Cfg, Tout, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
 }
 
-template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI>
+template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
 hipError_t launch_gemm_dma(const GemmParams& p, hipStream_t s) {
   const int ntn = (EPI == EPI_SWIGLU) ? (p.inter + Cfg::BN / 2 - 1) / (Cfg::BN / 2) : (p.N + Cfg::BN - 1) / Cfg::BN;
   int64_t slots;
   if (GM == GM_ROWS) slots = (p.M + Cfg::BM - 1) / Cfg::BM + p.groups;
-  else if (GM == GM_RED) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);
+  else if (GM == GM_RED || GM == GM_BATCH) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);
   else slots = (p.M + Cfg::BM - 1) / Cfg::BM;
   const int64_t grid = slots * ntn;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((grouped_gemm_dma_kernel<Cfg, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid), dim3(Cfg::NT), 0, s,
-                     p);
+  hipLaunchKernelGGL((grouped_gemm_dma_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid), dim3(Cfg::NT), 0,
+                     s, p);
   return hipGetLastError();
 }
 

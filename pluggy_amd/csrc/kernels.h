@@ -42,16 +42,29 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
                           float* partial, hipStream_t s);
 
 // ---- routing, permutation and row movement (route.hip).
+// logits = sum of nparts fp32 partial products (parts + q*part_stride), then
+// softmax / top-k / renormalisation and the per-block statistics.
 template <typename TW>
-hipError_t router_topk(float* logits, const float* logit_bias, int T, int E, int K, int norm_topk,
-                       TW* top_w, int64_t* top_idx, float* top_w_f32, float* blk_psum, float* blk_lse2,
-                       int* blk_counts, int rows_per_block, hipStream_t s);
+hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, float* logits, const float* logit_bias,
+                       int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
+                       float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s);
+hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s);
+// parts[g] = x . w3[g]^T for g < npieces, x (T,H) bf16, w3 (npieces,E,H) bf16, parts fp32 (npieces,T,E)
+hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
+                                     float* parts, hipStream_t s);
 hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
                                float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s);
+// dl (T, ldl) fp32, or with dl3 != nullptr the bf16 planes [dl_hi | dl_lo | dl_hi] (T, 3*ldl).
 template <typename TG>
 hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
-                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, int ldl,
-                          hipStream_t s);
+                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, bf16_t* dl3,
+                          int ldl, hipStream_t s);
+// w3t = [W_hi; W_hi; W_lo] with rows E..ldl-1 of each plane zero (3*ldl, H)
+template <typename TW>
+hipError_t split_router_weight_bwd(const TW* w, int E, int H, int ldl, bf16_t* w3t, hipStream_t s);
+hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s);
+hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, int H, int E, int split_chunk,
+                          float* partial, hipStream_t s);
 template <typename TO>
 hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s);
 

@@ -18,8 +18,45 @@ __device__ __forceinline__ bool better(float v, int e, float bv, int be) {
 }
 
 // One wave per row. EPL = experts per lane (E <= 64 * EPL).
+// W (E*H fp32) -> three bf16 planes hi, mid, lo with hi + mid + lo == W to
+// within 2^-24 relative (each residual is exact in fp32).
+__global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16_t* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = w[i];
+    const bf16_t hi = f32_to_bf16(v);
+    const float r1 = v - bf16_to_f32(hi);
+    const bf16_t mid = f32_to_bf16(r1);
+    const float r2 = r1 - bf16_to_f32(mid);
+    out[i] = hi;
+    out[n + i] = mid;
+    out[2 * n + i] = f32_to_bf16(r2);
+  }
+}
+
+// Logits of row `row`: the fixed-order sum of the partial products
+// ((p0 + p1) + p2), plus the optional bias. parts may alias logits (nparts 1).
+template <int EPL>
+__device__ __forceinline__ void load_logits(const float* parts, int nparts, int64_t part_stride, float* logits,
+                                            const float* bias, int row, int E, int lane, float (&v)[EPL]) {
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    float x = -INFINITY;
+    if (e < E) {
+      const int64_t o = (int64_t)row * E + e;
+      x = parts[o];
+      for (int q = 1; q < nparts; ++q) x += parts[q * part_stride + o];
+      if (bias != nullptr) x += bias[e];
+      if (nparts > 1 || bias != nullptr || parts != logits) logits[o] = x;
+    }
+    v[j] = x;
+  }
+}
+
 template <int EPL, typename TW>
-__global__ __launch_bounds__(256) void router_topk_kernel(float* __restrict__ logits, const float* __restrict__ bias,
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ parts, int nparts,
+                                                          int64_t part_stride, float* logits,
+                                                          const float* __restrict__ bias,
                                                           int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
                                                           int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
                                                           float* __restrict__ blk_psum, float* __restrict__ blk_lse2,
@@ -41,17 +78,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(float* __restrict__ lo
   const int row1 = min(T, row0 + rows_per_block);
   for (int row = row0 + wave; row < row1; row += 4) {
     float v[EPL];
-    float* lrow = logits + (int64_t)row * E;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const int e = lane + 64 * j;
-      float x = -INFINITY;
-      if (e < E) {
-        x = lrow[e];
-        if (bias != nullptr) { x += bias[e]; lrow[e] = x; }
-      }
-      v[j] = x;
-    }
+    load_logits<EPL>(parts, nparts, part_stride, logits, bias, row, E, lane, v);
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
@@ -120,22 +147,35 @@ __global__ __launch_bounds__(256) void router_topk_kernel(float* __restrict__ lo
   if (tid == 0) blk_lse2[blockIdx.x] = ((s_lse2[0] + s_lse2[1]) + s_lse2[2]) + s_lse2[3];
 }
 
-__global__ void router_stats_reduce_kernel(const float* blk_psum, const float* blk_lse2, const int* blk_counts,
-                                           int nblk, int E, float* prob_sum, float* lse_sq_sum, int32_t* counts) {
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    float ps = 0.0f;
-    int c = 0;
-    for (int b = 0; b < nblk; ++b) {
-      ps += blk_psum[(int64_t)b * E + e];
-      c += blk_counts[(int64_t)b * E + e];
-    }
+// One wave per expert (and one more for the lse^2 total): lane l sums the
+// partials b = l, l + 64, ... in order, then a fixed butterfly combines lanes,
+// so the result is the same on every run.
+__global__ __launch_bounds__(256) void router_stats_reduce_kernel(const float* blk_psum, const float* blk_lse2,
+                                                                  const int* blk_counts, int nblk, int E,
+                                                                  float* prob_sum, float* lse_sq_sum,
+                                                                  int32_t* counts) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e > E) return;
+  if (e == E) {
+    float l = 0.0f;
+    for (int b = lane; b < nblk; b += 64) l += blk_lse2[b];
+    l = wave_sum(l);
+    if (lane == 0 && lse_sq_sum) *lse_sq_sum = l;
+    return;
+  }
+  float ps = 0.0f;
+  int c = 0;
+  for (int b = lane; b < nblk; b += 64) {
+    ps += blk_psum[(int64_t)b * E + e];
+    c += blk_counts[(int64_t)b * E + e];
+  }
+  ps = wave_sum(ps);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, kWave);
+  if (lane == 0) {
     if (prob_sum) prob_sum[e] = ps;
     if (counts) counts[e] = c;
-  }
-  if (threadIdx.x == 0 && lse_sq_sum) {
-    float l = 0.0f;
-    for (int b = 0; b < nblk; ++b) l += blk_lse2[b];
-    *lse_sq_sum = l;
   }
 }
 
@@ -146,7 +186,8 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
                                                              const float* __restrict__ top_w_f32,
                                                              const TG* __restrict__ grad_w,
                                                              const float* __restrict__ grad_logits, int T, int E,
-                                                             int K, int norm_topk, float* __restrict__ dl, int ldl) {
+                                                             int K, int norm_topk, float* __restrict__ dl,
+                                                             bf16_t* __restrict__ dl3, int ldl) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
@@ -205,19 +246,51 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
       }
     }
   }
-  float* drow = dl + (int64_t)row * ldl;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
+    float val = 0.0f;
     if (e < E) {
-      float val = d[j];
+      val = d[j];
       if (grad_logits != nullptr) val += grad_logits[(int64_t)row * E + e];
-      drow[e] = val;
-    } else if (e < ldl) {
-      drow[e] = 0.0f;
+    }
+    if (e < ldl) {
+      if (dl3 == nullptr) {
+        dl[(int64_t)row * ldl + e] = val;
+      } else {
+        // val = hi + lo to 2^-16 relative; hi appears twice so that
+        // [hi | lo | hi] . [W_hi; W_hi; W_lo] = dl . W to that precision.
+        const bf16_t hi = f32_to_bf16(val);
+        const bf16_t lo = f32_to_bf16(val - bf16_to_f32(hi));
+        bf16_t* o = dl3 + (int64_t)row * 3 * ldl;
+        o[e] = hi;
+        o[ldl + e] = lo;
+        o[2 * ldl + e] = hi;
+      }
     }
   }
-  for (int e = 64 * EPL + lane; e < ldl; e += 64) drow[e] = 0.0f;
+  for (int e = 64 * EPL + lane; e < ldl; e += 64) {
+    if (dl3 == nullptr) {
+      dl[(int64_t)row * ldl + e] = 0.0f;
+    } else {
+      bf16_t* o = dl3 + (int64_t)row * 3 * ldl;
+      o[e] = o[ldl + e] = o[2 * ldl + e] = 0;
+    }
+  }
+}
+
+template <typename TW>
+__global__ void split_router_weight_bwd_kernel(const TW* __restrict__ w, int E, int H, int ldl,
+                                               bf16_t* __restrict__ w3t) {
+  const int64_t n = (int64_t)ldl * H;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i / H);
+    const float v = e < E ? load_scalar<TW>(w + i) : 0.0f;
+    const bf16_t hi = f32_to_bf16(v);
+    w3t[i] = hi;
+    w3t[n + i] = hi;
+    w3t[2 * n + i] = f32_to_bf16(v - bf16_to_f32(hi));
+  }
 }
 
 template <typename TO>
@@ -409,16 +482,24 @@ unsigned blocks_for(int64_t rows, int per_block) { return (unsigned)((rows + per
 
 }  // namespace
 
+hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 2048);
+  hipLaunchKernelGGL(split_bf16x3_kernel, dim3(grid), dim3(256), 0, s, w, n, out);
+  return hipGetLastError();
+}
+
 template <typename TW>
-hipError_t router_topk(float* logits, const float* logit_bias, int T, int E, int K, int norm_topk, TW* top_w,
-                       int64_t* top_idx, float* top_w_f32, float* blk_psum, float* blk_lse2, int* blk_counts,
-                       int rows_per_block, hipStream_t s) {
+hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, float* logits, const float* logit_bias,
+                       int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
+                       float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const unsigned grid = blocks_for(T, rows_per_block);
   const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
-#define PMOE_TOPK_CASE(EPL)                                                                                      \
-  hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, logits, logit_bias, T, E, K, \
-                     norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2, blk_counts, rows_per_block)
+#define PMOE_TOPK_CASE(EPL)                                                                                        \
+  hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, parts, nparts, part_stride,   \
+                     logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2,        \
+                     blk_counts, rows_per_block)
   if (E <= 64) PMOE_TOPK_CASE(1);
   else if (E <= 128) PMOE_TOPK_CASE(2);
   else if (E <= 256) PMOE_TOPK_CASE(4);
@@ -431,20 +512,30 @@ hipError_t router_topk(float* logits, const float* logit_bias, int T, int E, int
 
 hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
                                float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s) {
-  hipLaunchKernelGGL(router_stats_reduce_kernel, dim3(1), dim3(1024), 0, s, blk_psum, blk_lse2, blk_counts, nblk, E,
-                     prob_sum, lse_sq_sum, counts);
+  hipLaunchKernelGGL(router_stats_reduce_kernel, dim3((unsigned)((E + 1 + 3) / 4)), dim3(256), 0, s, blk_psum, blk_lse2,
+                     blk_counts, nblk, E, prob_sum, lse_sq_sum, counts);
   return hipGetLastError();
 }
 
+template <typename TW>
+hipError_t split_router_weight_bwd(const TW* w, int E, int H, int ldl, bf16_t* w3t, hipStream_t s) {
+  const int64_t n = (int64_t)ldl * H;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 2048);
+  hipLaunchKernelGGL((split_router_weight_bwd_kernel<TW>), dim3(grid), dim3(256), 0, s, w, E, H, ldl, w3t);
+  return hipGetLastError();
+}
+template hipError_t split_router_weight_bwd<float>(const float*, int, int, int, bf16_t*, hipStream_t);
+template hipError_t split_router_weight_bwd<bf16_t>(const bf16_t*, int, int, int, bf16_t*, hipStream_t);
+
 template <typename TG>
 hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
-                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, int ldl,
-                          hipStream_t s) {
+                          const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, bf16_t* dl3,
+                          int ldl, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const unsigned grid = blocks_for(T, 4);
 #define PMOE_DL_CASE(EPL)                                                                                        \
   hipLaunchKernelGGL((router_dlogits_kernel<EPL, TG>), dim3(grid), dim3(256), 0, s, logits, top_idx, top_w_f32, \
-                     grad_w, grad_logits, T, E, K, norm_topk, dl, ldl)
+                     grad_w, grad_logits, T, E, K, norm_topk, dl, dl3, ldl)
   if (E <= 64) PMOE_DL_CASE(1);
   else if (E <= 128) PMOE_DL_CASE(2);
   else if (E <= 256) PMOE_DL_CASE(4);
@@ -515,14 +606,14 @@ hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, int T_, i
   return hipGetLastError();
 }
 
-template hipError_t router_topk<bf16_t>(float*, const float*, int, int, int, int, bf16_t*, int64_t*, float*, float*,
-                                        float*, int*, int, hipStream_t);
-template hipError_t router_topk<float>(float*, const float*, int, int, int, int, float*, int64_t*, float*, float*,
-                                       float*, int*, int, hipStream_t);
+template hipError_t router_topk<bf16_t>(const float*, int, int64_t, float*, const float*, int, int, int, int, bf16_t*,
+                                        int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<float>(const float*, int, int64_t, float*, const float*, int, int, int, int, float*,
+                                       int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
-                                           int, int, int, int, float*, int, hipStream_t);
+                                           int, int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
-                                          int, int, int, float*, int, hipStream_t);
+                                          int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t reduce_partials<float>(const float*, int, int64_t, float*, hipStream_t);
 template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*, hipStream_t);
 

@@ -98,6 +98,7 @@ class _RouterFunction(torch.autograd.Function):
         ctx.save_for_backward(x, weight, logits, top_i, top_w32)
         ctx.norm_topk_prob = bool(norm_topk_prob)
         ctx.mark_non_differentiable(top_i, top_w32, counts, psum, lse2)
+        ctx.set_materialize_grads(False)  # absent gradients stay None (no zero-filled tensors)
         return logits, top_w, top_i, top_w32, counts, psum, lse2
 
     @staticmethod
@@ -160,10 +161,13 @@ class _ExpertFFNFunction(torch.autograd.Function):
             out = ops.combine(y, top_weights, inv_pos)
         ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
         ctx.dims = (hidden.shape[0], K, E)
+        ctx.set_materialize_grads(False)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
+        if grad_out is None:
+            return None, None, None, None, None
         top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
         T, K, E = ctx.dims
         need = ctx.needs_input_grad

@@ -30,7 +30,7 @@ def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bia
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     psum = torch.empty(E, dtype=torch.float32, device=dev)
     lse2 = torch.empty(1, dtype=torch.float32, device=dev)
-    ws = workspace(size("pmoe_router_forward_workspace_size", T, E), dev)
+    ws = workspace(size("pmoe_router_forward_workspace_size", T, H, E), dev)
     call("pmoe_router_forward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype), ptr(logit_bias),
          T, H, E, top_k, int(norm_topk_prob), ptr(logits), ptr(top_w), dtype_code(x.dtype), ptr(top_i),
          ptr(top_w32), ptr(counts), ptr(psum), ptr(lse2), ptr(ws), ws.numel(), stream_of(x))

@@ -58,7 +58,7 @@ def test_version_and_workspace_queries(lib):
     P, H, I = 8192 * 8, 2048, 768
     assert _lib.size("pmoe_expert_ffn_backward_workspace_size", 8192, 8, H, I, 1) >= P * H * 2 + P * 2 * I * 2
     assert _lib.size("pmoe_permute_workspace_size", 8192, 8, 128) >= 32 * 128 * 4
-    assert _lib.size("pmoe_router_forward_workspace_size", 0, 128) >= 0
+    assert _lib.size("pmoe_router_forward_workspace_size", 0, 2048, 128) >= 3 * 128 * 2048 * 2
 
 
 @pytest.mark.parametrize("args,needle", [
