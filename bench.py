@@ -35,8 +35,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, help="workload id (BASELINE.json configs, 1-based)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=None,
-                    help="tokens of the CPU-baseline sample (default: the full workload)")
+    ap.add_argument("--cpu-tokens", type=int, default=512,
+                    help="tokens of the CPU-baseline sample (0: the full workload)")
+    ap.add_argument("--copy-mib", type=int, default=256,
+                    help="size of the device-to-device copy timed as the measured HBM reference (0: skip)")
     return ap.parse_args()
 
 
@@ -58,7 +60,7 @@ def cpu_baseline(cfg, tokens: int | None):
     from oracle import moe_oracle as O
     from pluggy_amd.workloads import make_inputs
 
-    T = cfg.tokens if tokens is None else tokens
+    T = cfg.tokens if not tokens else min(tokens, cfg.tokens)
     inp = make_inputs(cfg, tokens=T)
     H = cfg.hidden
 
@@ -85,6 +87,50 @@ def cpu_baseline(cfg, tokens: int | None):
         "os_cpu_count": os.cpu_count(),
         "torch": torch.__version__,
     }
+
+
+def copy_bandwidth(mib: int, dev, reps: int = 5):
+    """HIP-event time of a plain device-to-device copy of `mib` MiB (read + write counted).
+
+    Runs after the timed region. Its rocprofv3 FETCH_SIZE / WRITE_SIZE readings
+    calibrate the counters against a known byte count.
+    """
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return {"bytes_per_copy": n, "mean_ms": round(ms, 4), "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 1)}
+
+
+def profiled_traffic(workload: str) -> dict:
+    """HBM bytes per launch of each kernel, from the committed rocprofv3 summary.
+
+    ``profiles/traffic_<workload>.txt`` holds lines ``kernel <name> avg_us <t>
+    hbm_bytes <b>`` computed from FETCH_SIZE / WRITE_SIZE passes (scaled by a
+    copy kernel of known size). Missing file -> {} (traffic reported as null).
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{workload}.txt")
+    out = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                tok = line.split()
+                if len(tok) >= 6 and tok[0] == "kernel" and tok[4] == "hbm_bytes":
+                    out[tok[1]] = int(tok[5])
+    except OSError:
+        return out
+    out["_source"] = os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
+    return out
 
 
 GEMM_STAGES = ("gate_up_fwd", "down_fwd", "down_dgrad", "down_wgrad", "gate_up_dgrad", "gate_up_wgrad")
@@ -149,6 +195,7 @@ def main() -> int:
     ms = start.elapsed_time(end) / args.steps
     stages = timer.summary()
 
+    traffic = profiled_traffic(cfg.name)
     gemm_flops = cfg.gemm_flops()
     tflops = gemm_flops / (ms * 1e-3) / 1e12
     # dominant kernel: the grouped-GEMM stage with the largest total time
@@ -188,12 +235,15 @@ def main() -> int:
         "gemm_gflop_per_step": round(gemm_flops / 1e9, 1),
         "wall_s": round(wall, 3),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic.get(dom), "traffic_source": traffic.get("_source"),
                      "flop_per_launch": dom_flops, "mean_ms": round(gemm[dom]["mean_ms"], 4)},
         "hbm": hbm,
         "stages_ms": {n: round(s["mean_ms"], 4) for n, s in sorted(stages.items(), key=lambda kv: -kv[1]["total_ms"])},
         "cpu_baseline": None,
     }
+    if args.copy_mib > 0:
+        result["copy_reference"] = copy_bandwidth(args.copy_mib, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(result), flush=True)
