@@ -105,6 +105,23 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // SiLU and its derivative in fp32: silu(g) = g * sigmoid(g).
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
 
+// sigmoid from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; each
+// about 1 ulp): 1 / (1 + 2^(-g log2 e)). Saturates to 0 / 1 without NaN for
+// large |g|.
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 (lo in bits 0-15), round to nearest even, with the
+// gfx950 conversion instruction (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace pmoe

@@ -15,20 +15,47 @@ template <typename T> struct CfgFor;
 template <> struct CfgFor<bf16_t> { typedef CfgBf16 type; };
 template <> struct CfgFor<float> { typedef CfgF32 type; };
 
-// bf16 expert GEMMs run on the DMA engine. Two tilings, chosen per GEMM from
-// measurements at the Qwen3-30B-A3B shape: 256x256 blocks of eight 128x64 wave
-// tiles (one block per CU), or 128x128 blocks of four 64x64 wave tiles (two
-// blocks per CU); both double-buffer 64-deep k stages in LDS.
-typedef DmaCfg<256, 256, 128, 64, 2> DmaBig;
-typedef DmaCfg<128, 128, 64, 64, 2> DmaSmall;
+// bf16 expert GEMMs run on the DMA engine: 256x256 blocks of eight 128x64
+// wave tiles (two waves per SIMD, one block per CU) with a four-stage ring of
+// 32-deep k tiles (128 KiB of LDS). Chosen by measurement at the
+// Qwen3-30B-A3B shape over 128x128 .. 256x256 tilings, 2..5 stages and
+// 32/64-deep k tiles: larger tiles fetch fewer bytes per MFMA through each
+// CU's vector-memory path, which bounds the smaller ones.
+typedef DmaCfg<256, 256, 128, 64, 4, 32, 1, 0> DmaExpert;
+#ifndef PMOE_CFG_GATE_UP_FWD
+#define PMOE_CFG_GATE_UP_FWD DmaExpert
+#endif
+#ifndef PMOE_CFG_DOWN_FWD
+#define PMOE_CFG_DOWN_FWD DmaExpert
+#endif
+#ifndef PMOE_CFG_DOWN_DGRAD
+#define PMOE_CFG_DOWN_DGRAD DmaExpert
+#endif
+#ifndef PMOE_CFG_DOWN_WGRAD
+#define PMOE_CFG_DOWN_WGRAD DmaExpert
+#endif
+#ifndef PMOE_CFG_GATE_UP_DGRAD
+#define PMOE_CFG_GATE_UP_DGRAD DmaExpert
+#endif
+#ifndef PMOE_CFG_GATE_UP_WGRAD
+#define PMOE_CFG_GATE_UP_WGRAD DmaExpert
+#endif
 
 template <typename T>
 hipError_t run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P, int E, int H,
                int I, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {
-    if (kind == EG_GATE_UP_FWD || kind == EG_DOWN_DGRAD)
-      return expert_gemm_dma<DmaSmall>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-    return expert_gemm_dma<DmaBig>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+    switch (kind) {
+      case EG_GATE_UP_FWD: return expert_gemm_dma<PMOE_CFG_GATE_UP_FWD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_DOWN_FWD: return expert_gemm_dma<PMOE_CFG_DOWN_FWD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_DOWN_DGRAD: return expert_gemm_dma<PMOE_CFG_DOWN_DGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_DOWN_WGRAD: return expert_gemm_dma<PMOE_CFG_DOWN_WGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_GATE_UP_DGRAD:
+        return expert_gemm_dma<PMOE_CFG_GATE_UP_DGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_GATE_UP_WGRAD:
+        return expert_gemm_dma<PMOE_CFG_GATE_UP_WGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+    }
+    return hipErrorInvalidValue;
   } else {
     return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
   }

@@ -5,10 +5,13 @@
 //  * tiles move HBM -> LDS with buffer_load_dwordx4 ... lds (no staging
 //    registers); lanes whose chunk is out of range get a buffer offset past
 //    the resource bound, which the hardware turns into zeros;
-//  * an NS-stage LDS ring keeps NS-1 k-tiles in flight;
+//  * an NS-stage LDS ring of BK-deep k-tiles: the prologue fills every slot,
+//    and each slot is refilled as soon as the block has finished reading it,
+//    so NS-1 stages are in flight while one is consumed;
 //  * LDS tiles are unpadded and XOR-swizzled at 16-byte granularity:
-//      k-contiguous tile [r][64]:  chunk' = chunk ^ ((r >> 1) & 7)
-//      [k][r] tile, R columns:     chunk' = chunk ^ (2 * (k & 7))
+//      k-contiguous tile [r][BK]:  chunk' = chunk ^ ((r >> 1) & 7)  (BK 64)
+//                                  chunk' = chunk ^ ((r >> 2) & 3)  (BK 32)
+//      [k][r] tile, R columns:     chunk' = chunk ^ (4 * (k & 3))
 //    so fragment reads of 16 consecutive lanes hit distinct banks;
 //  * fragments of k-contiguous tiles are one ds_read_b128; fragments of [k][r]
 //    tiles are two ds_read_b64_tr_b16, which transpose 4x4 blocks of 16-bit
@@ -26,32 +29,43 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 #define PMOE_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-constexpr uint32_t kBufOOB = 0xFFFFFFF0u;  // buffer offset past every resource bound
 
-template <int BM_, int BN_, int WM_, int WN_, int NS_>
+// MINB: blocks per CU the register allocation must allow (launch bounds).
+// SPLIT: the first half of the waves issue every DMA of a stage (each wave
+// then has one DMA-issuing and one MFMA-only partner per SIMD, so a wave
+// stalled on memory-instruction issue never idles the matrix unit).
+template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1, int SPLIT_ = 0>
 struct DmaCfg {
   typedef bf16_t Tc;
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, BK = BK_, MINB = MINB_;
+  static constexpr bool SPLIT = SPLIT_ != 0;
   static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = kWave * NW;
   static constexpr int MI = WM / 32, NI = WN / 32;
-  static constexpr int BK = 64;
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int A_INSTR = BM / 8 / NW, B_INSTR = BN / 8 / NW;  // 1 KB DMA instructions per wave
-  static constexpr int D = A_INSTR + B_INSTR;
+  static constexpr int A_INSTR = A_BYTES / 1024 / NW, B_INSTR = B_BYTES / 1024 / NW;  // 1 KB DMAs per wave
+  static constexpr int D = A_INSTR + B_INSTR;  // DMAs per wave-share of a stage
+  static constexpr int DW = SPLIT ? 2 * D : D;   // DMAs per issuing wave per stage
   static constexpr int EPI_LD = WN + 4;
   static constexpr int EPI_BYTES = NW * 32 * EPI_LD * 4;
   static constexpr int MAIN_BYTES = NS * STAGE_BYTES;
   static constexpr int SMEM_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % WM == 0 && BN % WN == 0, "tile shape");
-  static_assert(A_INSTR * NW * 8 == BM && B_INSTR * NW * 8 == BN, "DMA instructions must divide among waves");
-  static_assert(NS >= 2, "at least double buffering");
+  static_assert(BK == 32 || BK == 64, "k extent of a stage");
+  static_assert(A_INSTR * NW * 1024 == A_BYTES && B_INSTR * NW * 1024 == B_BYTES,
+                "DMA instructions must divide among waves");
+  static_assert(NS >= 2 && (NS - 1) * DW < 64, "ring depth");
+  static_assert(!SPLIT || NW % 2 == 0, "split DMA issue needs an even number of waves");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef i32x4 BufRsrc;  // buffer resource descriptor (V#), kept in SGPRs
+
+// Offsets at or above kOOB lie past every descriptor bound (make_rsrc keeps
+// bounds below 2^31) and read as zero; adding a k offset keeps them there.
+constexpr uint32_t kOOB = 0x80000000u;
 
 // Raw buffer over [base, base + bytes): stride 0, bound = bytes, dword 3 as
 // for untyped raw buffers on gfx9. Offsets at or past the bound read as zero.
@@ -60,7 +74,7 @@ __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint64_t bytes) {
   BufRsrc r;
   r[0] = (int)(uint32_t)a;
   r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = (int)(bytes > (uint64_t)kBufOOB ? kBufOOB : (uint32_t)bytes);
+  r[2] = (int)(bytes >= (uint64_t)kOOB ? kOOB - 16 : (uint32_t)bytes);
   r[3] = 0x00020000;
   return r;
 }
@@ -69,12 +83,12 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p);
 }
 
-// One wave-wide 16-byte-per-lane DMA: lane l's chunk goes to lds_dst + 16*l.
-// Issued from inline asm so that the compiler adds no waits of its own; every
-// consumer waits explicitly with wait_vmcnt<> and a barrier.
-// m0 (the LDS destination) is saved and restored inside the statement, so the
-// compiler's view of m0 is untouched.
-__device__ __forceinline__ void dma16(const BufRsrc& rs, char* lds_dst, uint32_t voff) {
+// One wave-wide 16-byte-per-lane DMA: lane l's chunk goes to LDS byte address
+// lds + 16*l (lds is wave-uniform). Issued from inline asm so that the
+// compiler adds no waits of its own; every consumer waits explicitly with
+// wait_vmcnt<> and a barrier. m0 (the LDS destination) is saved and restored
+// inside the statement, so the compiler's view of m0 is untouched.
+__device__ __forceinline__ void dma16(const BufRsrc& rs, uint32_t lds, uint32_t voff) {
   int saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -83,7 +97,7 @@ __device__ __forceinline__ void dma16(const BufRsrc& rs, char* lds_dst, uint32_t
       "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))), "v"(voff), "s"(rs)
+      : "s"(lds), "v"(voff), "s"(rs)
       : "memory");
 }
 
@@ -104,49 +118,81 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ int swz_t(int k) { return 2 * (k & 7); }
+// Wait until at most n stages of D DMAs each are outstanding (n a runtime
+// value in [0, NS-1]; the count must be an immediate, hence the switch).
+template <int D, int NS>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (NS >= 5) { if (n >= 4) { wait_vmcnt<4 * D>(); return; } }
+  if constexpr (NS >= 4) { if (n >= 3) { wait_vmcnt<3 * D>(); return; } }
+  if constexpr (NS >= 3) { if (n >= 2) { wait_vmcnt<2 * D>(); return; } }
+  if (n >= 1) { wait_vmcnt<D>(); return; }
+  wait_vmcnt<0>();
+}
 
-// k-contiguous operand, R rows x 64 k per stage.
-template <int R, int NW>
+// [k][r] tiles: a ds_read_b64_tr_b16 half-wave reads 4 consecutive k-rows x 32
+// columns (4 chunks per row); shifting the chunk by 4 per k (mod 4) puts those
+// 16 chunks in 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz_t(int k) { return 4 * (k & 3); }
+
+// k-contiguous tiles, rows of BK bf16 (CPR = BK/8 chunks): the chunk is XORed
+// with a function of the row so that 16 consecutive rows at one logical chunk
+// fall in 16 distinct 16-byte bank groups.
+template <int BK>
+__device__ __forceinline__ int swz_kc(int r) {
+  if constexpr (BK == 64) return (r >> 1) & 7;
+  else return (r >> 2) & 3;
+}
+
+// k-contiguous operand, R rows x BK k per stage; instruction i of wave w fills
+// rows [(w + i*NW) * RPI, +RPI) with RPI = 512 / BK.
+template <int R, int NW, int BK>
 struct KcDma {
-  static constexpr int INSTR = R / 8 / NW;
-  uint32_t rowoff[INSTR];  // bytes of (row, this lane's chunk) at k = 0, or kBufOOB
-  int kc[INSTR];           // this lane's k offset within the stage (8 * logical chunk)
+  static constexpr int CPR = BK / 8, RPI = 512 / BK;
+  static constexpr int INSTR = R / RPI / NW;
+  uint32_t rowoff[INSTR];  // bytes of (row, this lane's chunk) at k = 0, or kOOB
+  int kc[INSTR];           // this lane's k offset within the stage
 
-  // row_of(r) -> global storage row of tile row r, or -1 when out of range
+  // row_of(r) -> storage row of tile row r relative to the descriptor base, or -1
   template <class RowFn>
   __device__ __forceinline__ void init(RowFn row_of, int64_t ld, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
-      const int r = 8 * (wave + i * NW) + (lane >> 3);
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int r = RPI * (wave + i * NW) + lane / CPR;
+      const int c = (lane % CPR) ^ swz_kc<BK>(r);
       const int g = row_of(r);
       kc[i] = 8 * c;
-      rowoff[i] = g < 0 ? kBufOOB : (uint32_t)(((int64_t)g * ld + 8 * c) * 2);
+      rowoff[i] = g < 0 ? kOOB : (uint32_t)(((int64_t)g * ld + 8 * c) * 2);
     }
   }
-  __device__ __forceinline__ void issue(const BufRsrc& rs, char* tile, int k0, int k_hi, int wave) const {
-#pragma unroll
-    for (int i = 0; i < INSTR; ++i) {
-      const uint32_t v = (rowoff[i] != kBufOOB && k0 + kc[i] < k_hi) ? rowoff[i] + (uint32_t)(k0 * 2) : kBufOOB;
-      dma16(rs, tile + (wave + i * NW) * 1024, v);
-    }
+  // k0: first k of the stage relative to the descriptor; tail: the stage
+  // reaches past k_hi (only then are lanes checked one by one).
+  // instruction I of the stage at LDS byte address tile
+  template <int I>
+  __device__ __forceinline__ void issue1(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, bool tail,
+                                         int wave) const {
+    uint32_t v = rowoff[I] + (uint32_t)(k0 * 2);
+    if (tail && k0 + kc[I] >= k_hi) v = kOOB;
+    dma16(rs, tile + (wave + I * NW) * 1024, v);
   }
 };
 
+template <int BK>
 __device__ __forceinline__ bf16x8 kc_frag(const char* tile, int r, int c) {
-  return *reinterpret_cast<const bf16x8*>(tile + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+  return *reinterpret_cast<const bf16x8*>(tile + r * (BK * 2) + ((c ^ swz_kc<BK>(r)) << 4));
 }
 
-// [k][r] operand: 64 k-rows x R columns per stage.
-template <int R, int NW>
+// [k][r] operand: BK k-rows x R columns per stage; instruction i of wave w
+// fills k-rows [(w + i*NW) * KPI, +KPI) with KPI = 512 / R. k-rows past the
+// descriptor bound read as zero, so ragged reduction ranges need no checks.
+template <int R, int NW, int BK>
 struct TDma {
   static_assert(R >= 128, "[k][r] swizzle needs 16 chunks per row");
   static constexpr int CPR = R / 8;       // 16-byte chunks per k-row
-  static constexpr int KPI = 64 / CPR;    // k-rows per 1 KB instruction
-  static constexpr int INSTR = R / 8 / NW;
+  static constexpr int KPI = 512 / R;     // k-rows per 1 KB instruction
+  static constexpr int INSTR = BK / KPI / NW;
+  static_assert(INSTR * KPI * NW == BK, "[k][r] DMA instructions must divide among waves");
   int kk[INSTR];
-  uint32_t coloff[INSTR];  // bytes of this lane's column chunk, or kBufOOB
+  uint32_t coloff[INSTR];  // bytes of this lane's column chunk, or kOOB
 
   __device__ __forceinline__ void init(int r0, int r_limit, int wave, int lane) {
 #pragma unroll
@@ -155,17 +201,12 @@ struct TDma {
       const int c = (lane % CPR) ^ swz_t(k);
       const int col = r0 + 8 * c;
       kk[i] = k;
-      coloff[i] = col < r_limit ? (uint32_t)(col * 2) : kBufOOB;
+      coloff[i] = col < r_limit ? (uint32_t)(col * 2) : kOOB;
     }
   }
-  __device__ __forceinline__ void issue(const BufRsrc& rs, char* tile, int k0, int k_hi, int64_t ld,
-                                        int wave) const {
-#pragma unroll
-    for (int i = 0; i < INSTR; ++i) {
-      const int kg = k0 + kk[i];
-      const uint32_t v = (coloff[i] != kBufOOB && kg < k_hi) ? (uint32_t)((int64_t)kg * ld * 2) + coloff[i] : kBufOOB;
-      dma16(rs, tile + (wave + i * NW) * 1024, v);
-    }
+  template <int I>
+  __device__ __forceinline__ void issue1(const BufRsrc& rs, uint32_t tile, int k0, int64_t ld, int wave) const {
+    dma16(rs, tile + (wave + I * NW) * 1024, (uint32_t)((int64_t)(k0 + kk[I]) * ld * 2) + coloff[I]);
   }
 };
 
@@ -188,6 +229,150 @@ __device__ __forceinline__ bf16x8 t_frag(const char* tile, int r_base, int kbase
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// 8 consecutive outputs from fp32: bf16 through the native converter, or fp32.
+template <typename Tout> struct Out8;
+template <> struct Out8<bf16_t> {
+  __device__ static __forceinline__ u32x4 pack(const float* v) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = cvt_pk_bf16(v[2 * i], v[2 * i + 1]);
+    return w;
+  }
+  __device__ static __forceinline__ void store(bf16_t* p, const float* v) { *reinterpret_cast<u32x4*>(p) = pack(v); }
+};
+template <> struct Out8<float> {
+  __device__ static __forceinline__ void store(float* p, const float* v) { Vec8<float>::store(p, v); }
+};
+
+__device__ __forceinline__ void unpack8(const u32x4& w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { v[2 * i] = bf16lo(w[i]); v[2 * i + 1] = bf16hi(w[i]); }
+}
+
+// Epilogue of the DMA engine. Each wave moves its accumulators to HBM one
+// 32-row slab at a time through its own LDS region (no block barriers): lanes
+// write their MFMA columns as fp32, then read back 8 consecutive columns of a
+// row with 16-byte LDS reads, convert with v_cvt_pk_bf16_f32 and store 16-byte
+// vectors. The fused SwiGLU forward / backward run on those 8-wide rows.
+template <class Cfg, typename Tout, int GM, int EPI>
+__device__ __forceinline__ void store_tile_dma(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* smem_f,
+                                               const TileInfo& ti, const GemmParams& p, int wave, int wm, int wn,
+                                               int lane) {
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN, LD = Cfg::EPI_LD;
+  static_assert(LD % 4 == 0, "16-byte aligned staging rows");
+  static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
+  float* stage = smem_f + wave * 32 * LD;
+  Tout* C = reinterpret_cast<Tout*>(p.C);
+  if constexpr (GM == GM_RED || GM == GM_BATCH) C += (int64_t)ti.group * p.strideC;
+  const int half = lane >> 5, col_l = lane & 31;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stage[(8 * q + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * q + r];
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
+    asm volatile("" ::: "memory");
+    const int row_base = ti.m0 + wm * Cfg::WM + i * 32;
+    if constexpr (EPI == EPI_SWIGLU) {
+      constexpr int H2 = WN / 2, CPR = H2 / 8;
+      bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
+      const int col_base = ti.n0 + wn * H2;
+#pragma unroll
+      for (int e = lane; e < 32 * CPR; e += 64) {
+        const int r = e / CPR, c = (e % CPR) * 8;
+        const int row = row_base + r, col = col_base + c;
+        if (row < ti.m_end && col < p.inter) {
+          float g[8], u[8], m[8];
+          Vec8<float>::load(stage + r * LD + c, g);
+          Vec8<float>::load(stage + r * LD + H2 + c, u);
+          const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
+          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
+          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
+          unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
+          unpack8(uw, u);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
+          Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
+        }
+      }
+    } else {
+      constexpr int CPR = WN / 8;
+      const int col_base = ti.n0 + wn * WN;
+#pragma unroll
+      for (int e = lane; e < 32 * CPR; e += 64) {
+        const int r = e / CPR, c = (e % CPR) * 8;
+        const int row = row_base + r, col = col_base + c;
+        if (row < ti.m_end && col < p.N) {
+          float v[8];
+          Vec8<float>::load(stage + r * LD + c, v);
+          if constexpr (EPI == EPI_SWIGLU_BWD) {
+            // v = d(mid); the aux row holds the [gate | up] pre-activations
+            const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
+            float g[8], u[8], dg[8], du[8];
+            Vec8<bf16_t>::load(GU + col, g);
+            Vec8<bf16_t>::load(GU + p.inter + col, u);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float sg = fast_sigmoid(g[t]);
+              const float silu = g[t] * sg;
+              dg[t] = v[t] * u[t] * (sg + silu * (1.0f - sg));
+              du[t] = v[t] * silu;
+            }
+            Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
+            Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
+          } else if (col + 8 <= p.N) {
+            Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
+          } else {
+            for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Compile-time loop: f(integral_constant<int, B>), ..., f(integral_constant<int, E-1>).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>());
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Timestamps of pipeline events for performance analysis builds only
+// (-DPMOE_PROBE=<block>): wave 0 of that block records (event, clock64) pairs.
+#ifdef PMOE_PROBE
+__device__ unsigned long long g_probe[4096];
+#define PMOE_MARK(ev)                                                                        \
+  do {                                                                                       \
+    if (blockIdx.x == PMOE_PROBE && threadIdx.x == 0 && probe_n < 4094) {                    \
+      g_probe[probe_n++] = (ev);                                                             \
+      g_probe[probe_n++] = clock64();                                                        \
+    }                                                                                        \
+  } while (0)
+#else
+#define PMOE_MARK(ev) \
+  do {                \
+  } while (0)
+#endif
+// Per-block start / end wall clock (-DPMOE_BLOCKTIME): g_btime[2b], g_btime[2b+1].
+#ifdef PMOE_BLOCKTIME
+__device__ unsigned long long g_btime[2 * 65536];
+#define PMOE_BTIME(slot)                                                         \
+  do {                                                                           \
+    if (threadIdx.x == 0 && blockIdx.x < 65536)                                  \
+      g_btime[2 * blockIdx.x + (slot)] = __builtin_amdgcn_s_memrealtime();       \
+  } while (0)
+#else
+#define PMOE_BTIME(slot) \
+  do {                   \
+  } while (0)
+#endif
+
 // Blocks are dispatched to the 8 XCDs round-robin; give each XCD a contiguous
 // range of logical tiles so that tiles sharing operands share an L2.
 __device__ __forceinline__ int xcd_remap(int b, int grid) {
@@ -196,33 +381,96 @@ __device__ __forceinline__ int xcd_remap(int b, int grid) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
 }
 
+// GM_ROWS tile scan: s_scan[g] = first m-tile of group g (s_scan[groups] =
+// total m-tiles), computed by wave 0 from the inclusive end offsets; every
+// thread returns the total. s_scan holds >= groups+1 ints.
+template <int BM>
+__device__ __forceinline__ int rows_scan(const int32_t* offs, int groups, int* s_scan) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    int carry = 0;
+    for (int base = 0; base < groups; base += 64) {
+      const int g = base + lane;
+      int tiles = 0;
+      if (g < groups) {
+        const int lo = g == 0 ? 0 : offs[g - 1];
+        tiles = (offs[g] - lo + BM - 1) / BM;
+      }
+      const int inc = wave_incl_scan(tiles, lane) + carry;
+      if (g < groups) s_scan[g + 1] = inc;
+      carry = __shfl(inc, 63, kWave);
+    }
+    if (lane == 0) s_scan[0] = 0;
+  }
+  __syncthreads();
+  return s_scan[groups];
+}
+
+// Group of m-tile `slot` (binary search over the scan; slot < total).
+__device__ __forceinline__ int rows_group(const int* s_scan, int groups, int slot) {
+  int lo = 0, hi = groups - 1;  // the group g with s_scan[g] <= slot < s_scan[g + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_scan[mid] <= slot) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Logical tile of this block when `total` tiles are spread over the 8 XCDs
+// (blocks reach XCD blockIdx % 8): XCD x takes a contiguous share of
+// total/8 (+1) tiles, so neighbouring tiles share its L2 and every XCD gets
+// the same amount of work. -1: no tile for this block.
+__device__ __forceinline__ int xcd_tile(int b, int total) {
+  const int x = b & 7, i = b >> 3;
+  const int per = total >> 3, rem = total & 7;
+  const int cnt = per + (x < rem ? 1 : 0);
+  if (i >= cnt) return -1;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
 template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
-__global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW, NS = Cfg::NS;
+__global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(GemmParams p) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && NI % 2 == 0), "SwiGLU epilogue layout");
 
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::SMEM_BYTES];
   __shared__ int s_scan[1025];
-  __shared__ int s_found;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#ifdef PMOE_PROBE
+  int probe_n = 0;
+#endif
+  PMOE_MARK(0);
+  PMOE_BTIME(0);
   const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
 
   // ---- tile mapping (logical tile id, n fastest)
   const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int tn = bid % ntiles_n;
-  const int slot = bid / ntiles_n;
   TileInfo ti;
   const bf16_t* A = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B = reinterpret_cast<const bf16_t*>(p.B);
+  int tn, slot;
   if constexpr (GM == GM_ROWS) {
-    int g, r0, re;
-    if (!rows_tile_lookup<BM>(p.offs, p.groups, slot, s_scan, &s_found, g, r0, re)) return;
-    ti.group = g; ti.m0 = r0; ti.m_end = re; ti.k_lo = 0; ti.k_hi = p.K;
+    // the grid covers the worst case; only the real tiles are spread over XCDs
+    const int mtiles = rows_scan<BM>(p.offs, p.groups, s_scan);
+    const int bid = xcd_tile(blockIdx.x, mtiles * ntiles_n);
+    if (bid < 0) return;
+    tn = bid % ntiles_n;
+    slot = bid / ntiles_n;
+    const int g = rows_group(s_scan, p.groups, slot);
+    const int lo = g == 0 ? 0 : p.offs[g - 1];
+    ti.group = g; ti.m0 = lo + (slot - s_scan[g]) * BM; ti.m_end = p.offs[g]; ti.k_lo = 0; ti.k_hi = p.K;
     B += (int64_t)g * p.strideB;
+  } else {
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    tn = bid % ntiles_n;
+    slot = bid / ntiles_n;
+  }
+  if constexpr (GM == GM_ROWS) {
   } else if constexpr (GM == GM_RED) {
     const int mt = (p.M + BM - 1) / BM;
     const int g = slot / mt;
@@ -249,8 +497,10 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p)
   }
   ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
 
-  // ---- operand DMA descriptors, based at the tile's first row (k-contiguous
-  // A) or first k (the [k][r] operands of GM_RED) so every offset stays small.
+  // ---- operand DMA descriptors. k-contiguous A is based at the tile's first
+  // row and bounded by the group's last row; the [k][r] operands of GM_RED are
+  // based at the group's first k and bounded by its last, so rows and k past
+  // the group read as zero.
   const bf16_t* a_base = A;
   uint64_t a_bytes = p.a_bytes;
   const bf16_t* b_base = B;
@@ -268,31 +518,46 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p)
   }
   const BufRsrc rsA = make_rsrc(a_base, a_bytes);
   const BufRsrc rsB = make_rsrc(b_base, b_bytes);
-  const int k_org = (GM == GM_RED) ? ti.k_lo : 0;  // k of the descriptors' origin
-  typedef typename std::conditional<A_KC, KcDma<BM, NW>, TDma<BM, NW>>::type LdA;
-  typedef typename std::conditional<B_KC, KcDma<BN, NW>, TDma<BN, NW>>::type LdB;
-  LdA la;
-  LdB lb;
-  if constexpr (A_KC) {
-    const int rows = ti.m_end - ti.m0;
-    la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
-  } else {
-    la.init(ti.m0, ti.m_end, wave, lane);
-  }
-  if constexpr (B_KC) {
-    const int n0 = ti.n0, N = p.N, I = p.inter;
-    if constexpr (EPI == EPI_SWIGLU) {
-      lb.init([&](int c) {
-        const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
-        const int gcol = n0 + w * h + (cc % h);
-        if (gcol >= I) return -1;
-        return cc < h ? gcol : I + gcol;
-      }, p.ldb, wave, lane);
+  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
+  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
+  // DMA share of "virtual wave" vw: the waves that issue DMAs take the share
+  // of their own index and, with SPLIT, that of wave + NW/2.
+  constexpr bool SPLIT = Cfg::SPLIT;
+  constexpr int DW = Cfg::DW;
+  const bool dma_wave = !SPLIT || wave < NW / 2;
+  const int vw0 = wave, vw1 = SPLIT ? wave + NW / 2 : wave;
+  auto init_a = [&](LdA& la, int vw) {
+    if constexpr (A_KC) {
+      const int rows = ti.m_end - ti.m0;
+      la.init([&](int r) { return r < rows ? r : -1; }, p.lda, vw, lane);
     } else {
-      lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, wave, lane);
+      la.init(ti.m0, ti.m_end, vw, lane);
     }
-  } else {
-    lb.init(ti.n0, p.N, wave, lane);
+  };
+  auto init_b = [&](LdB& lb, int vw) {
+    if constexpr (B_KC) {
+      const int n0 = ti.n0, N = p.N, I = p.inter;
+      if constexpr (EPI == EPI_SWIGLU) {
+        lb.init([&](int c) {
+          const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
+          const int gcol = n0 + w * h + (cc % h);
+          if (gcol >= I) return -1;
+          return cc < h ? gcol : I + gcol;
+        }, p.ldb, vw, lane);
+      } else {
+        lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, vw, lane);
+      }
+    } else {
+      lb.init(ti.n0, p.N, vw, lane);
+    }
+  };
+  LdA la0, la1;
+  LdB lb0, lb1;
+  init_a(la0, vw0);
+  init_b(lb0, vw0);
+  if constexpr (SPLIT) {
+    init_a(la1, vw1);
+    init_b(lb1, vw1);
   }
 
   f32x16 acc[MI][NI];
@@ -304,75 +569,131 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_dma_kernel(GemmParams p)
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int klen = ti.k_hi - ti.k_lo;
-  const int nk = klen > 0 ? (klen + Cfg::BK - 1) / Cfg::BK : 0;
+  const int nk = klen > 0 ? (klen + BK - 1) / BK : 0;
+  const uint32_t lds0 = lds_addr(smem);
+  // descriptors of GM_RED start at k_lo; the others at k = 0
+  const int kd0 = (GM == GM_RED) ? 0 : ti.k_lo;
+  const int kd_hi = ti.k_hi - ((GM == GM_RED) ? ti.k_lo : 0);
 
-  auto issue = [&](int kt) {
-    char* st = smem + (kt % NS) * Cfg::STAGE_BYTES;
-    const int k0 = ti.k_lo + kt * Cfg::BK - k_org;  // relative to the descriptors' origin
-    const int kh = ti.k_hi - k_org;
-    if constexpr (A_KC) la.issue(rsA, st, k0, kh, wave);
-    else la.issue(rsA, st, k0, kh, p.lda, wave);
-    if constexpr (B_KC) lb.issue(rsB, st + Cfg::A_BYTES, k0, kh, wave);
-    else lb.issue(rsB, st + Cfg::A_BYTES, k0, kh, p.ldb, wave);
+  // DMA instruction J (0 .. DW-1) of stage kt: J < D is the share of vw0
+  // (A's instructions, then B's), J >= D that of vw1.
+  auto dma_share = [&](int kt, auto jc, const LdA& la, const LdB& lb, int vw) {
+    constexpr int J = decltype(jc)::value;
+    const uint32_t st = lds0 + (uint32_t)((kt % NS) * Cfg::STAGE_BYTES);
+    const int k0 = kd0 + kt * BK;
+    if constexpr (J < Cfg::A_INSTR) {
+      if constexpr (A_KC) la.template issue1<J>(rsA, st, k0, kd_hi, k0 + BK > kd_hi, vw);
+      else la.template issue1<J>(rsA, st, k0, p.lda, vw);
+    } else {
+      constexpr int JB = J - Cfg::A_INSTR;
+      if constexpr (B_KC) lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, kd_hi, k0 + BK > kd_hi, vw);
+      else lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, p.ldb, vw);
+    }
   };
-
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s);
+  auto dma_one = [&](int kt, auto jc) {
+    constexpr int J = decltype(jc)::value;
+    if constexpr (J < D) dma_share(kt, jc, la0, lb0, vw0);
+    else dma_share(kt, std::integral_constant<int, J - D>(), la1, lb1, vw1);
+  };
+  auto issue = [&](int kt) {
+    if (dma_wave) static_for<0, DW>([&](auto jc) { dma_one(kt, jc); });
+  };
 
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
   // Fragments of k-substep ks (16 deep) of the stage at sa / sb.
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      if constexpr (A_KC) af[i] = kc_frag(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
       else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      if constexpr (B_KC) bfr[j] = kc_frag(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
       else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
     }
   };
-  constexpr int KS = Cfg::BK / 16;
-  // LDS reads per substep (a [k][r] fragment takes two transposing reads)
-  constexpr int NREAD = MI * (A_KC ? 1 : 2) + NI * (B_KC ? 1 : 2);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * Cfg::D>();
-    else wait_vmcnt<0>();
+  constexpr int KS = BK / 16;
+  static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
+  // MFMAs of a stage before its end-of-stage barrier; the D DMAs of the stage
+  // being refilled are spread evenly among them.
+  constexpr int TOTM = (KS - 1) * MI * NI;
+  static_assert(DW <= TOTM, "every DMA of a stage needs an MFMA slot");
+
+  // MFMAs of substep KSC (a compile-time constant); with DMA_ST >= 0 the DMAs
+  // of stage DMA_ST whose slots fall in this substep follow their MFMA.
+  auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], int dma_st) {
+    constexpr int KSI = decltype(ksc)::value;
+    static_for<0, MI * NI>([&](auto mc) {
+      constexpr int M = decltype(mc)::value;
+      acc[M / NI][M % NI] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
+      constexpr int G = KSI * MI * NI + M;  // MFMA index within the stage
+      static_for<0, DW>([&](auto dc) {
+        constexpr int DI = decltype(dc)::value;
+        if constexpr ((DI * TOTM) / DW == G) {
+          if (dma_st >= 0 && dma_wave) dma_one(dma_st, dc);
+        }
+      });
+    });
+  };
+
+  // ---- pipeline. The prologue fills all NS ring slots. During stage kt the
+  // DMAs of stage kt-1+NS (into the slot stage kt-1 used) are interleaved
+  // with the MFMAs, so address issue overlaps matrix work. At the end of each
+  // stage but the last (before its last substep's MFMAs) every wave waits for
+  // stage kt+1 and the block synchronises (which also retires every read of
+  // stage kt and makes stage kt+1 visible); the first fragments of stage kt+1
+  // are read while the last MFMAs of stage kt run. The loop body is
+  // straight-line code; the last stage is peeled.
+  PMOE_MARK(1);
+#pragma unroll
+  for (int s0 = 0; s0 < NS; ++s0)
+    if (s0 < nk) issue(s0);
+  bf16x8 af[2][MI], bfr[2][NI];
+  if (nk > 0) {
+    wait_stages<DW, NS>(min(NS, nk) - 1);
+    PMOE_MARK(2);
     lds_barrier();
+    PMOE_MARK(3);
+    load_frags(smem, smem + Cfg::A_BYTES, 0, af[0], bfr[0]);
+  }
+  for (int kt = 0; kt + 1 < nk; ++kt) {
     const char* sa = smem + (kt % NS) * Cfg::STAGE_BYTES;
     const char* sb = sa + Cfg::A_BYTES;
-    // Software pipeline over the substeps: the fragments of substep ks + 1 are
-    // read while the MFMAs of substep ks run. The first reads go out ahead of
-    // the next stage's DMA issue so their latency overlaps it.
-    bf16x8 af[2][MI], bfr[2][NI];
-    load_frags(sa, sb, 0, af[0], bfr[0]);
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < KS) load_frags(sa, sb, ks + 1, af[cur ^ 1], bfr[cur ^ 1]);
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
-      if (ks + 1 < KS) {
-        // interleave: one LDS read, one MFMA, ...; remaining MFMAs after
-#pragma unroll
-        for (int q = 0; q < (NREAD < MI * NI ? NREAD : MI * NI); ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        }
-        if constexpr (NREAD < MI * NI) __builtin_amdgcn_sched_group_barrier(0x008, MI * NI - NREAD, 0);
-        else if constexpr (NREAD > MI * NI) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - MI * NI, 0);
-      }
-    }
+    const int dma_st = (kt >= 1 && kt - 1 + NS < nk) ? kt - 1 + NS : -1;
+    static_for<0, KS - 1>([&](auto ksc) {
+      constexpr int KSI = decltype(ksc)::value;
+      load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+      substep(ksc, af[KSI & 1], bfr[KSI & 1], dma_st);
+    });
+    // stages kt+2 .. min(kt+NS-1, nk-1) may stay in flight
+    PMOE_MARK(10);
+    wait_stages<DW, NS>(min(NS - 1, nk - 1 - kt) - 1);
+    PMOE_MARK(11);
+    lds_barrier();
+    PMOE_MARK(12);
+    const char* na = smem + ((kt + 1) % NS) * Cfg::STAGE_BYTES;
+    load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
+    substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], -1);
+    PMOE_MARK(13);
   }
+  if (nk > 0) {
+    const char* sa = smem + ((nk - 1) % NS) * Cfg::STAGE_BYTES;
+    const char* sb = sa + Cfg::A_BYTES;
+    static_for<0, KS>([&](auto ksc) {
+      constexpr int KSI = decltype(ksc)::value;
+      if constexpr (KSI + 1 < KS) load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+      substep(ksc, af[KSI & 1], bfr[KSI & 1], -1);
+    });
+  }
+  PMOE_MARK(20);
   wait_vmcnt<0>();
   lds_barrier();
-  store_tile<Cfg, Tout, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
+  PMOE_MARK(21);
+  store_tile_dma<Cfg, Tout, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
+  PMOE_MARK(22);
+  PMOE_BTIME(1);
 }
 
 template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
@@ -382,8 +703,9 @@ hipError_t launch_gemm_dma(const GemmParams& p, hipStream_t s) {
   if (GM == GM_ROWS) slots = (p.M + Cfg::BM - 1) / Cfg::BM + p.groups;
   else if (GM == GM_RED || GM == GM_BATCH) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);
   else slots = (p.M + Cfg::BM - 1) / Cfg::BM;
-  const int64_t grid = slots * ntn;
+  int64_t grid = slots * ntn;
   if (grid <= 0) return hipSuccess;
+  if (GM == GM_ROWS) grid = (grid + 7) / 8 * 8;  // xcd_tile spreads up to 8*ceil(tiles/8) blocks
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((grouped_gemm_dma_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid), dim3(Cfg::NT), 0,
                      s, p);
