@@ -1,5 +1,5 @@
 // Launchers of the grouped expert GEMMs and the router GEMMs.
-#include "gemm_dma.h"
+#include "gemm_persist.h"
 #include "kernels.h"
 
 namespace pmoe {
@@ -41,20 +41,33 @@ typedef DmaCfg<256, 256, 128, 64, 4, 32, 1, 0> DmaExpert;
 #define PMOE_CFG_GATE_UP_WGRAD DmaExpert
 #endif
 
+// Compute units of the current device (the persistent kernels launch one
+// block per CU).
+int num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
 template <typename T>
 hipError_t run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P, int E, int H,
                int I, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {
+#ifdef PMOE_NO_PERSIST
+#define PMOE_EG(CFG) expert_gemm_dma<CFG>(kind, A, B, aux, C, C2, offs, P, E, H, I, s)
+#else
+#define PMOE_EG(CFG) expert_gemm_persist<CFG>(kind, A, B, aux, C, C2, offs, P, E, H, I, num_cus(), s)
+#endif
     switch (kind) {
-      case EG_GATE_UP_FWD: return expert_gemm_dma<PMOE_CFG_GATE_UP_FWD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-      case EG_DOWN_FWD: return expert_gemm_dma<PMOE_CFG_DOWN_FWD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-      case EG_DOWN_DGRAD: return expert_gemm_dma<PMOE_CFG_DOWN_DGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-      case EG_DOWN_WGRAD: return expert_gemm_dma<PMOE_CFG_DOWN_WGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-      case EG_GATE_UP_DGRAD:
-        return expert_gemm_dma<PMOE_CFG_GATE_UP_DGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
-      case EG_GATE_UP_WGRAD:
-        return expert_gemm_dma<PMOE_CFG_GATE_UP_WGRAD>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+      case EG_GATE_UP_FWD: return PMOE_EG(PMOE_CFG_GATE_UP_FWD);
+      case EG_DOWN_FWD: return PMOE_EG(PMOE_CFG_DOWN_FWD);
+      case EG_DOWN_DGRAD: return PMOE_EG(PMOE_CFG_DOWN_DGRAD);
+      case EG_DOWN_WGRAD: return PMOE_EG(PMOE_CFG_DOWN_WGRAD);
+      case EG_GATE_UP_DGRAD: return PMOE_EG(PMOE_CFG_GATE_UP_DGRAD);
+      case EG_GATE_UP_WGRAD: return PMOE_EG(PMOE_CFG_GATE_UP_WGRAD);
     }
+#undef PMOE_EG
     return hipErrorInvalidValue;
   } else {
     return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);

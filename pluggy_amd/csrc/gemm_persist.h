@@ -1,0 +1,390 @@
+// Persistent grouped GEMM for the six expert GEMMs (GM_ROWS and GM_RED).
+//
+// One block per CU loops over the tiles of its XCD. The tile list is the
+// same as the non-persistent kernel's (n fastest within an m-tile, m-tiles of
+// a group consecutive); XCD x owns a contiguous share of it, and block i of
+// the XCD takes tiles i, i + nb, i + 2 nb, ... of that share (nb = blocks on
+// the XCD), so at any moment the XCD's CUs work on neighbouring tiles that
+// share operands in its L2. Per block, the expert offsets are read into LDS
+// and scanned once; a tile's group is then a binary search in LDS.
+//
+// The k loop is the ring pipeline of grouped_gemm_dma_kernel with a global
+// stage counter, so ring slots carry over from one tile to the next: the
+// first NS-1 stages of a tile are issued right after the previous tile's
+// epilogue (the ring is idle then), and stage kt+NS-1 is issued during stage
+// kt. The epilogue stages accumulators through a separate per-wave LDS region
+// of 8-row slabs and never touches the ring.
+#pragma once
+
+#include "gemm_dma.h"
+
+namespace pmoe {
+
+template <class Cfg>
+struct PersistLayout {
+  static constexpr int RING = Cfg::NS * Cfg::STAGE_BYTES;
+  static constexpr int EPI_LD = Cfg::WN + 4;                  // floats per staged row
+  static constexpr int EPI_FLOATS = Cfg::NW * 8 * EPI_LD;     // 8 rows per wave
+  static_assert(EPI_LD % 4 == 0, "16-byte aligned staging rows");
+};
+
+// Epilogue through per-wave 8-row slabs: slab (i, q) holds rows 8q .. 8q+7 of
+// the wave's 32-row block i (lane half h holds rows 8q + 4h + r, r = 0..3).
+template <class Cfg, typename Tout, int GM, int EPI>
+__device__ __forceinline__ void store_slabs8(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
+                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN, LD = PersistLayout<Cfg>::EPI_LD;
+  static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
+  Tout* C = reinterpret_cast<Tout*>(p.C);
+  if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
+  const int half = lane >> 5, col_l = lane & 31;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stage[(4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * q + r];
+      __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
+      asm volatile("" ::: "memory");
+      const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + 8 * q;
+      if constexpr (EPI == EPI_SWIGLU) {
+        constexpr int H2 = WN / 2, CPR = H2 / 8;
+        static_assert(8 * CPR <= 64, "one 8-row slab per wave instruction");
+        bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
+        const int r = lane / CPR, c = (lane % CPR) * 8;
+        const int row = row_base + r, col = ti.n0 + wn * H2 + c;
+        if (lane < 8 * CPR && row < ti.m_end && col < p.inter) {
+          float g[8], u[8], m[8];
+          Vec8<float>::load(stage + r * LD + c, g);
+          Vec8<float>::load(stage + r * LD + H2 + c, u);
+          const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
+          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
+          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
+          unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
+          unpack8(uw, u);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
+          Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
+        }
+      } else {
+        constexpr int CPR = WN / 8;
+#pragma unroll
+        for (int e = lane; e < 8 * CPR; e += 64) {
+          const int r = e / CPR, c = (e % CPR) * 8;
+          const int row = row_base + r, col = ti.n0 + wn * WN + c;
+          if (row < ti.m_end && col < p.N) {
+            float v[8];
+            Vec8<float>::load(stage + r * LD + c, v);
+            if constexpr (EPI == EPI_SWIGLU_BWD) {
+              const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
+              float g[8], u[8], dg[8], du[8];
+              Vec8<bf16_t>::load(GU + col, g);
+              Vec8<bf16_t>::load(GU + p.inter + col, u);
+#pragma unroll
+              for (int t = 0; t < 8; ++t) {
+                const float sg = fast_sigmoid(g[t]);
+                const float silu = g[t] * sg;
+                dg[t] = v[t] * u[t] * (sg + silu * (1.0f - sg));
+                du[t] = v[t] * silu;
+              }
+              Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
+              Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
+            } else if (col + 8 <= p.N) {
+              Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
+            } else {
+              for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
+__global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, DW = Cfg::DW;
+  constexpr bool SPLIT = Cfg::SPLIT;
+  typedef PersistLayout<Cfg> L;
+  static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
+  static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
+  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && NI % 2 == 0), "SwiGLU epilogue layout");
+
+  __shared__ __attribute__((aligned(1024))) char smem[L::RING];
+  __shared__ __attribute__((aligned(16))) float s_epi[L::EPI_FLOATS];
+  __shared__ int s_scan[1025];
+  __shared__ int s_offs[1024];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
+  const int groups = p.groups;
+
+  // ---- tile list
+  for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs[g];
+  __syncthreads();
+  const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+  const int mt_red = (p.M + BM - 1) / BM;  // GM_RED: m-tiles per group
+  int total;
+  if constexpr (GM == GM_ROWS) {
+    if (tid < 64) {
+      int carry = 0;
+      for (int base = 0; base < groups; base += 64) {
+        const int g = base + lane;
+        int tiles = 0;
+        if (g < groups) tiles = (s_offs[g] - (g == 0 ? 0 : s_offs[g - 1]) + BM - 1) / BM;
+        const int inc = wave_incl_scan(tiles, lane) + carry;
+        if (g < groups) s_scan[g + 1] = inc;
+        carry = __shfl(inc, 63, kWave);
+      }
+      if (lane == 0) s_scan[0] = 0;
+    }
+    __syncthreads();
+    total = s_scan[groups] * ntiles_n;
+  } else {
+    total = groups * mt_red * ntiles_n;
+  }
+  const int xcd = blockIdx.x & 7;
+  int bi = blockIdx.x >> 3;  // this block's next position in the XCD share
+  const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
+  const int per = total >> 3, rem = total & 7;
+  const int cnt = per + (xcd < rem ? 1 : 0);
+  const int start = xcd * per + (xcd < rem ? xcd : rem);
+
+  const uint32_t lds0 = lds_addr(smem);
+  float* stage = s_epi + wave * 8 * L::EPI_LD;
+  const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
+  const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
+  const bool dma_wave = !SPLIT || wave < NW / 2;
+  const int vw0 = wave, vw1 = SPLIT ? wave + NW / 2 : wave;
+  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
+  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
+  constexpr int KS = BK / 16;
+  static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
+  constexpr int TOTM = (KS - 1) * MI * NI;
+  static_assert(DW <= TOTM, "every DMA of a stage needs an MFMA slot");
+  const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
+
+  // ---- per-tile state (current tile)
+  TileInfo ti;
+  BufRsrc rsA, rsB;
+  LdA la0, la1;
+  LdB lb0, lb1;
+  int nk = 0, kd0 = 0, kd_hi = 0;
+
+  // Sets ti, the descriptors and nk for tile t.
+  auto setup = [&](int t) {
+    const int tn = t % ntiles_n, slot = t / ntiles_n;
+    const bf16_t* A = A0;
+    const bf16_t* B = B0;
+    if constexpr (GM == GM_ROWS) {
+      const int g = rows_group(s_scan, groups, slot);
+      const int lo = g == 0 ? 0 : s_offs[g - 1];
+      ti.group = g; ti.m0 = lo + (slot - s_scan[g]) * BM; ti.m_end = s_offs[g]; ti.k_lo = 0; ti.k_hi = p.K;
+      B += (int64_t)g * p.strideB;
+    } else {
+      const int g = slot / mt_red;
+      ti.group = g; ti.m0 = (slot % mt_red) * BM; ti.m_end = p.M;
+      ti.k_lo = g == 0 ? 0 : s_offs[g - 1];
+      ti.k_hi = s_offs[g];
+    }
+    ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+    const bf16_t* a_base = A;
+    uint64_t a_bytes = p.a_bytes;
+    const bf16_t* b_base = B;
+    uint64_t b_bytes = p.b_bytes;
+    if constexpr (A_KC) {
+      a_base = A + (int64_t)ti.m0 * p.lda;
+      a_bytes = (uint64_t)(ti.m_end - ti.m0) * p.lda * 2;
+    } else {
+      a_base = A + (int64_t)ti.k_lo * p.lda;
+      a_bytes = (uint64_t)(ti.k_hi - ti.k_lo) * p.lda * 2;
+    }
+    if constexpr (GM == GM_RED) {
+      b_base = B + (int64_t)ti.k_lo * p.ldb;
+      b_bytes = (uint64_t)(ti.k_hi - ti.k_lo) * p.ldb * 2;
+    }
+    rsA = make_rsrc(a_base, a_bytes);
+    rsB = make_rsrc(b_base, b_bytes);
+    auto init_a = [&](LdA& la, int vw) {
+      if constexpr (A_KC) {
+        const int rows = ti.m_end - ti.m0;
+        la.init([&](int r) { return r < rows ? r : -1; }, p.lda, vw, lane);
+      } else {
+        la.init(ti.m0, ti.m_end, vw, lane);
+      }
+    };
+    auto init_b = [&](LdB& lb, int vw) {
+      if constexpr (B_KC) {
+        const int n0 = ti.n0, N = p.N, I = p.inter;
+        if constexpr (EPI == EPI_SWIGLU) {
+          lb.init([&](int c) {
+            const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
+            const int gcol = n0 + w * h + (cc % h);
+            if (gcol >= I) return -1;
+            return cc < h ? gcol : I + gcol;
+          }, p.ldb, vw, lane);
+        } else {
+          lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, vw, lane);
+        }
+      } else {
+        lb.init(ti.n0, p.N, vw, lane);
+      }
+    };
+    init_a(la0, vw0);
+    init_b(lb0, vw0);
+    if constexpr (SPLIT) {
+      init_a(la1, vw1);
+      init_b(lb1, vw1);
+    }
+    const int klen = ti.k_hi - ti.k_lo;
+    nk = klen > 0 ? (klen + BK - 1) / BK : 0;
+    kd0 = (GM == GM_RED) ? 0 : ti.k_lo;
+    kd_hi = ti.k_hi - ((GM == GM_RED) ? ti.k_lo : 0);
+  };
+
+  int gs = 0;  // global stage counter: stage kt of the current tile lives in slot (gs + kt) % NS
+  auto slot_addr = [&](int kt) { return (uint32_t)(((gs + kt) % NS) * Cfg::STAGE_BYTES); };
+
+  auto dma_share = [&](int kt, auto jc, const LdA& la, const LdB& lb, int vw) {
+    constexpr int J = decltype(jc)::value;
+    const uint32_t st = lds0 + slot_addr(kt);
+    const int k0 = kd0 + kt * BK;
+    if constexpr (J < Cfg::A_INSTR) {
+      if constexpr (A_KC) la.template issue1<J>(rsA, st, k0, kd_hi, k0 + BK > kd_hi, vw);
+      else la.template issue1<J>(rsA, st, k0, p.lda, vw);
+    } else {
+      constexpr int JB = J - Cfg::A_INSTR;
+      if constexpr (B_KC) lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, kd_hi, k0 + BK > kd_hi, vw);
+      else lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, p.ldb, vw);
+    }
+  };
+  auto dma_one = [&](int kt, auto jc) {
+    constexpr int J = decltype(jc)::value;
+    if constexpr (J < D) dma_share(kt, jc, la0, lb0, vw0);
+    else dma_share(kt, std::integral_constant<int, J - D>(), la1, lb1, vw1);
+  };
+  auto issue = [&](int kt) {
+    if (dma_wave) static_for<0, DW>([&](auto jc) { dma_one(kt, jc); });
+  };
+  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
+    }
+  };
+
+  f32x16 acc[MI][NI];
+  auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], int dma_st) {
+    constexpr int KSI = decltype(ksc)::value;
+    static_for<0, MI * NI>([&](auto mc) {
+      constexpr int M = decltype(mc)::value;
+      acc[M / NI][M % NI] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
+      constexpr int G = KSI * MI * NI + M;
+      static_for<0, DW>([&](auto dc) {
+        constexpr int DI = decltype(dc)::value;
+        if constexpr ((DI * TOTM) / DW == G) {
+          if (dma_st >= 0 && dma_wave) dma_one(dma_st, dc);
+        }
+      });
+    });
+  };
+
+  bf16x8 af[2][MI], bfr[2][NI];
+  int t = bi < cnt ? start + bi : -1;
+  if (t >= 0) {
+    setup(t);
+    for (int s0 = 0; s0 < NS - 1; ++s0)
+      if (s0 < nk) issue(s0);
+  }
+  while (t >= 0) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    if (nk > 0) {
+      wait_stages<DW, NS>(min(NS - 1, nk) - 1);
+      lds_barrier();  // stage 0 visible; every wave is past the previous tile
+      const char* s0 = smem + slot_addr(0);
+      load_frags(s0, s0 + Cfg::A_BYTES, 0, af[0], bfr[0]);
+    }
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      const char* sa = smem + slot_addr(kt);
+      const char* sb = sa + Cfg::A_BYTES;
+      const int dma_st = kt + NS - 1 < nk ? kt + NS - 1 : -1;
+      static_for<0, KS - 1>([&](auto ksc) {
+        constexpr int KSI = decltype(ksc)::value;
+        load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+        substep(ksc, af[KSI & 1], bfr[KSI & 1], dma_st);
+      });
+      // stages kt+2 .. min(kt+NS-1, nk-1) may stay in flight
+      wait_stages<DW, NS>(min(NS - 2, nk - 2 - kt));
+      lds_barrier();
+      const char* na = smem + slot_addr(kt + 1);
+      load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
+      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], -1);
+    }
+    if (nk > 0) {
+      const char* sa = smem + slot_addr(nk - 1);
+      const char* sb = sa + Cfg::A_BYTES;
+      static_for<0, KS>([&](auto ksc) {
+        constexpr int KSI = decltype(ksc)::value;
+        if constexpr (KSI + 1 < KS) load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+        substep(ksc, af[KSI & 1], bfr[KSI & 1], -1);
+      });
+    }
+    store_slabs8<Cfg, Tout, GM, EPI>(acc, stage, ti, p, wm, wn, lane);
+    // next tile: its first NS-1 stages go into the slots after this tile's
+    gs += nk;
+    bi += nb;
+    t = bi < cnt ? start + bi : -1;
+    if (t >= 0) {
+      // Stages 0 .. NS-2 go to the slots after the previous tile's last one,
+      // all retired at its last barrier; the slot of its last stage is reused
+      // only by stage NS-1, issued after this tile's first barrier.
+      setup(t);
+      for (int s0 = 0; s0 < NS - 1; ++s0)
+        if (s0 < nk) issue(s0);
+    }
+  }
+}
+
+template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
+hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) {
+  if (p.groups > 1024) return hipErrorInvalidValue;
+  const int grid = num_cus > 0 ? num_cus : 256;
+  hipLaunchKernelGGL((grouped_gemm_persist_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3(grid), dim3(Cfg::NT), 0, s,
+                     p);
+  return hipGetLastError();
+}
+
+// The six expert GEMMs on the persistent kernel.
+template <class Cfg>
+hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
+                               bf16_t* C2, const int32_t* offs, int P, int E, int H, int I, int num_cus,
+                               hipStream_t s) {
+  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I);
+  switch (kind) {
+    case EG_GATE_UP_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
+    case EG_DOWN_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
+    case EG_DOWN_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+    case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
+    case EG_GATE_UP_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace pmoe
