@@ -11,6 +11,10 @@ Prints one JSON line: tokens/s (whole job), expert-GEMM TFLOP/s and its
 fraction of the bf16 dense MFMA peak, per-stage HIP-event timings, the
 roofline of the dominant kernel, HBM GB/s of the row-movement kernels, and a
 CPU baseline (the restated reference CPU path) timed on this host.
+
+Two timed regions of --steps steps each: the first, bracketed by two events,
+gives ms_per_step and tokens/s; the second records an event pair around each
+stage (kernel) for the per-kernel durations.
 """
 
 from __future__ import annotations
@@ -181,18 +185,27 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
+    # Timed region 1: K whole steps, bracketed by two HIP events only (an event
+    # record between kernels leaves a gap of ~10 us on the GPU, so per-stage
+    # events would inflate the step time).
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    # Timed region 2: K more steps with HIP events around every stage (each
+    # kernel's duration on the stream it runs on) for the roofline and the
+    # per-stage breakdown.
     with stage_timer() as timer:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record()
         for _ in range(args.steps):
             step()
-        end.record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    ms = start.elapsed_time(end) / args.steps
     stages = timer.summary()
 
     traffic = profiled_traffic(cfg.name)

@@ -87,9 +87,11 @@ PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int6
                           int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos, void* workspace,
                           size_t workspace_bytes, void* stream);
 
-/* Row gather hidden[sorted_token] (moe.py:104): x_perm[p] = hidden[sorted_pair[p] / K]. */
-PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* sorted_pair, int64_t T, int64_t K,
-                           int64_t H, void* x_perm, void* stream);
+/* Row gather hidden[sorted_token] (moe.py:104), done in scatter form:
+ * x_perm[inv_pos[t*K + k]] = hidden[t] for every token t and slot k (each
+ * hidden row is read once), which equals x_perm[p] = hidden[sorted_pair[p] / K]. */
+PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
+                           void* x_perm, void* stream);
 
 /* Grouped gate_up GEMM + SwiGLU (moe.py:113-118, swiglu.py:14-16):
  * gate_up_out[p] = x_perm[p] . gate_up_proj[e(p)]^T  (P, 2I), rounded to dtype;
@@ -128,9 +130,11 @@ PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_p
                                    const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
                                    void* grad_x_perm, void* grad_gate_up_proj, void* stream);
 
-/* Backward of pmoe_dispatch: grad_hidden[t] = sum_k grad_x_perm[inv_pos[t*K+k]] (fp32 sum). */
-PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, int dtype, int64_t T,
-                                    int64_t K, int64_t H, void* grad_hidden, void* stream);
+/* Backward of pmoe_dispatch: grad_hidden[t] = grad_hidden_add[t] + sum_k
+ * grad_x_perm[inv_pos[t*K+k]] (fp32 sum, k ascending; grad_hidden_add (T,H)
+ * may be NULL, e.g. the router's share of the input gradient). */
+PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, const void* grad_hidden_add,
+                                    int dtype, int64_t T, int64_t K, int64_t H, void* grad_hidden, void* stream);
 
 /* ------------------------------------------------------ whole expert FFN ---
  * Replaces moe_expert_ffn / _expert_ffn_grouped (pluggy/kernels/moe.py:68-168):

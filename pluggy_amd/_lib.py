@@ -41,7 +41,7 @@ SIGNATURES = {
     "pmoe_combine_backward": (_INT, [_P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
-    "pmoe_dispatch_backward": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _P, _P]),
+    "pmoe_dispatch_backward": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P]),
     "pmoe_expert_ffn_forward_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_expert_ffn_forward": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                                        _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -262,32 +262,31 @@ PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int6
   return PMOE_OK;
 }
 
-PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* sorted_pair, int64_t T, int64_t K,
-                           int64_t H, void* x_perm, void* stream) {
+PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
+                           void* x_perm, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
-  PMOE_REQUIRE(hidden && sorted_pair && x_perm, "dispatch: null tensor");
-  const int P = (int)(T * K);
+  PMOE_REQUIRE(hidden && inv_pos && x_perm, "dispatch: null tensor");
   hipError_t st = dtype == PMOE_BF16
-                      ? dispatch_rows<bf16_t>((const bf16_t*)hidden, sorted_pair, P, (int)K, (int)H, (bf16_t*)x_perm,
+                      ? dispatch_rows<bf16_t>((const bf16_t*)hidden, inv_pos, (int)T, (int)K, (int)H, (bf16_t*)x_perm,
                                               as_stream(stream))
-                      : dispatch_rows<float>((const float*)hidden, sorted_pair, P, (int)K, (int)H, (float*)x_perm,
+                      : dispatch_rows<float>((const float*)hidden, inv_pos, (int)T, (int)K, (int)H, (float*)x_perm,
                                              as_stream(stream));
   return hip_status(st, "dispatch");
 }
 
-PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, int dtype, int64_t T,
-                                    int64_t K, int64_t H, void* grad_hidden, void* stream) {
+PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, const void* grad_hidden_add,
+                                    int dtype, int64_t T, int64_t K, int64_t H, void* grad_hidden, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(grad_x_perm && inv_pos && grad_hidden, "dispatch_backward: null tensor");
   hipError_t st = dtype == PMOE_BF16
-                      ? dispatch_rows_bwd<bf16_t>((const bf16_t*)grad_x_perm, inv_pos, (int)T, (int)K, (int)H,
-                                                  (bf16_t*)grad_hidden, as_stream(stream))
-                      : dispatch_rows_bwd<float>((const float*)grad_x_perm, inv_pos, (int)T, (int)K, (int)H,
-                                                 (float*)grad_hidden, as_stream(stream));
+                      ? dispatch_rows_bwd<bf16_t>((const bf16_t*)grad_x_perm, inv_pos, (const bf16_t*)grad_hidden_add,
+                                                  (int)T, (int)K, (int)H, (bf16_t*)grad_hidden, as_stream(stream))
+                      : dispatch_rows_bwd<float>((const float*)grad_x_perm, inv_pos, (const float*)grad_hidden_add,
+                                                 (int)T, (int)K, (int)H, (float*)grad_hidden, as_stream(stream));
   return hip_status(st, "dispatch_backward");
 }
 
@@ -453,7 +452,7 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
     return rc;
   if (T == 0) return PMOE_OK;
   const int64_t P = T * K;
-  if (int rc = pmoe_dispatch(hidden, dtype, sorted_pair, T, K, H, x_perm, stream)) return rc;
+  if (int rc = pmoe_dispatch(hidden, dtype, inv_pos, T, K, H, x_perm, stream)) return rc;
   if (int rc = pmoe_gate_up_swiglu(x_perm, gate_up_proj, offs, dtype, P, E, H, I, gate_up_out, mid, stream))
     return rc;
   if (int rc = pmoe_down_proj(mid, down_proj, offs, dtype, P, E, H, I, y, stream)) return rc;
@@ -509,7 +508,7 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
       return rc;
   }
   // 4. dispatch backward
-  if (grad_hidden) return pmoe_dispatch_backward(grad_y, inv_pos, dtype, T, K, H, grad_hidden, stream);
+  if (grad_hidden) return pmoe_dispatch_backward(grad_y, inv_pos, nullptr, dtype, T, K, H, grad_hidden, stream);
   return PMOE_OK;
 }
 

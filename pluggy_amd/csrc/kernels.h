@@ -71,7 +71,7 @@ hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out,
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
                          int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s);
 template <typename T>
-hipError_t dispatch_rows(const T* x, const int32_t* sorted_pair, int P, int K, int H, T* x_perm, hipStream_t s);
+hipError_t dispatch_rows(const T* x, const int32_t* inv_pos, int T_, int K, int H, T* x_perm, hipStream_t s);
 template <typename T, typename TW>
 hipError_t combine_rows(const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H, T* out,
                         hipStream_t s);
@@ -79,7 +79,8 @@ template <typename T, typename TW>
 hipError_t combine_rows_bwd(const T* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H,
                             T* dy, TW* dw, hipStream_t s);
 template <typename T>
-hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, int T_, int K, int H, T* dx,
+// dx = (add +) the K-sum; add (T_,H) may be NULL
+hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* add, int T_, int K, int H, T* dx,
                              hipStream_t s);
 
 // Chunk size (pairs) of the permutation histogram and the workspace it needs.

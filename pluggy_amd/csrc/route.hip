@@ -3,6 +3,7 @@
 #include <limits.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -391,45 +392,105 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
   }
 }
 
-// ---- row movers: one wave per destination row, 16-byte lanes
+// ---- row movers: one wave per token, 16-byte lanes. KC > 0 is the top-k
+// as a compile-time constant: the K row addresses are read once and the K row
+// loads of a chunk are all issued before the arithmetic, so each wave keeps K
+// loads in flight. Sums run over k in ascending order in fp32 (deterministic).
 
 template <typename T> struct RowVec { static constexpr int N = 16 / sizeof(T); };
 
-template <typename T>
-__global__ __launch_bounds__(256) void dispatch_kernel(const T* __restrict__ x, const int32_t* __restrict__ sorted_pair,
-                                                       int P, int K, int H, T* __restrict__ x_perm) {
-  const int lane = threadIdx.x & 63;
-  const int pos = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pos >= P) return;
-  const int t = sorted_pair[pos] / K;
-  const u32x4* src = reinterpret_cast<const u32x4*>(x + (int64_t)t * H);
-  u32x4* dst = reinterpret_cast<u32x4*>(x_perm + (int64_t)pos * H);
-  const int nvec = H / RowVec<T>::N;
-  for (int c = lane; c < nvec; c += 64) dst[c] = src[c];
-}
-
-template <typename T, typename TW>
-__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ y, const TW* __restrict__ w,
-                                                      const int32_t* __restrict__ inv_pos, int T_, int K, int H,
-                                                      T* __restrict__ out) {
+// Scatter form of the dispatch gather: token t's row is read once and written
+// to its K positions x_perm[inv_pos[t*K + k]].
+template <typename T, int KC>
+__global__ __launch_bounds__(256) void dispatch_kernel(const T* __restrict__ x, const int32_t* __restrict__ inv_pos,
+                                                       int T_, int K, int H, T* __restrict__ x_perm) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  for (int c = lane * 8; c < H; c += 64 * 8) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = 0; k < K; ++k) {
-      const int64_t q = (int64_t)t * K + k;
-      const float wk = load_scalar<TW>(w + q);
-      float v[8];
-      Vec8<T>::load(y + (int64_t)inv_pos[q] * H + c, v);
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + (int64_t)t * H);
+  const int nvec = H / RowVec<T>::N;
+  if constexpr (KC > 0) {
+    u32x4* dst[KC];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
+    for (int k = 0; k < KC; ++k)
+      dst[k] = reinterpret_cast<u32x4*>(x_perm + (int64_t)inv_pos[(int64_t)t * KC + k] * H);
+    for (int c = lane; c < nvec; c += 64) {
+      const u32x4 v = src[c];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) dst[k][c] = v;
     }
-    Vec8<T>::store(out + (int64_t)t * H + c, acc);
+  } else {
+    for (int c = lane; c < nvec; c += 64) {
+      const u32x4 v = src[c];
+      for (int k = 0; k < K; ++k)
+        reinterpret_cast<u32x4*>(x_perm + (int64_t)inv_pos[(int64_t)t * K + k] * H)[c] = v;
+    }
   }
 }
 
-template <typename T, typename TW>
+// out[t] = (add[t] +) sum_k w[t,k] * y[inv_pos[t*K + k]].
+// WEIGHTED = false: unit weights (w unused, may be null). HAS_ADD = false: no
+// addend (add unused, may be null).
+template <typename T, typename TW, int KC, bool WEIGHTED, bool HAS_ADD>
+__device__ __forceinline__ void gather_sum_row(const T* __restrict__ y, const TW* __restrict__ w,
+                                               const int32_t* __restrict__ inv_pos, const T* __restrict__ add, int t,
+                                               int K, int H, T* __restrict__ out, int lane) {
+  if constexpr (KC > 0) {
+    int64_t row[KC];
+    float wk[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int64_t q = (int64_t)t * KC + k;
+      row[k] = (int64_t)inv_pos[q] * H;
+      if constexpr (WEIGHTED) wk[k] = load_scalar<TW>(w + q);
+      else wk[k] = 1.0f;
+    }
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+      float v[KC][8];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) Vec8<T>::load(y + row[k] + c, v[k]);
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (HAS_ADD) Vec8<T>::load(add + (int64_t)t * H + c, acc);
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += WEIGHTED ? wk[k] * v[k][i] : v[k][i];
+      Vec8<T>::store(out + (int64_t)t * H + c, acc);
+    }
+  } else {
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (HAS_ADD) Vec8<T>::load(add + (int64_t)t * H + c, acc);
+      for (int k = 0; k < K; ++k) {
+        const int64_t q = (int64_t)t * K + k;
+        float v[8];
+        Vec8<T>::load(y + (int64_t)inv_pos[q] * H + c, v);
+        if constexpr (WEIGHTED) {
+          const float wk = load_scalar<TW>(w + q);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += v[i];
+        }
+      }
+      Vec8<T>::store(out + (int64_t)t * H + c, acc);
+    }
+  }
+}
+
+template <typename T, typename TW, int KC>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ y, const TW* __restrict__ w,
+                                                      const int32_t* __restrict__ inv_pos, int T_, int K, int H,
+                                                      T* __restrict__ out) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T_) return;
+  gather_sum_row<T, TW, KC, true, false>(y, w, inv_pos, nullptr, t, K, H, out, threadIdx.x & 63);
+}
+
+// grad_y[inv_pos[t*K+k]] = w[t,k] * dout[t]; dw[t,k] = <dout[t], y[inv_pos[t*K+k]]>.
+// dout[t] is read once per chunk for all k.
+template <typename T, typename TW, int KC>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ y,
                                                           const TW* __restrict__ w,
                                                           const int32_t* __restrict__ inv_pos, int T_, int K, int H,
@@ -438,44 +499,69 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
   const T* drow = dout + (int64_t)t * H;
-  for (int k = 0; k < K; ++k) {
-    const int64_t q = (int64_t)t * K + k;
-    const float wk = load_scalar<TW>(w + q);
-    const int64_t pos = inv_pos[q];
-    float dot = 0.0f;
-    for (int c = lane * 8; c < H; c += 64 * 8) {
-      float g[8], v[8], o[8];
-      Vec8<T>::load(drow + c, g);
-      Vec8<T>::load(y + pos * H + c, v);
+  if constexpr (KC > 0) {
+    int64_t row[KC];
+    float wk[KC], dot[KC];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        dot += g[i] * v[i];
-        o[i] = wk * g[i];
-      }
-      Vec8<T>::store(dy + pos * H + c, o);
+    for (int k = 0; k < KC; ++k) {
+      const int64_t q = (int64_t)t * KC + k;
+      row[k] = (int64_t)inv_pos[q] * H;
+      wk[k] = load_scalar<TW>(w + q);
+      dot[k] = 0.0f;
     }
-    dot = wave_sum(dot);
-    if (lane == 0) store_scalar<TW>(dw + q, dot);
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+      float g[8], v[KC][8];
+      Vec8<T>::load(drow + c, g);
+#pragma unroll
+      for (int k = 0; k < KC; ++k) Vec8<T>::load(y + row[k] + c, v[k]);
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dot[k] += g[i] * v[k][i];
+          o[i] = wk[k] * g[i];
+        }
+        Vec8<T>::store(dy + row[k] + c, o);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const float d = wave_sum(dot[k]);
+      if (lane == 0) store_scalar<TW>(dw + (int64_t)t * KC + k, d);
+    }
+  } else {
+    for (int k = 0; k < K; ++k) {
+      const int64_t q = (int64_t)t * K + k;
+      const float wk = load_scalar<TW>(w + q);
+      const int64_t pos = inv_pos[q];
+      float dot = 0.0f;
+      for (int c = lane * 8; c < H; c += 64 * 8) {
+        float g[8], v[8], o[8];
+        Vec8<T>::load(drow + c, g);
+        Vec8<T>::load(y + pos * H + c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dot += g[i] * v[i];
+          o[i] = wk * g[i];
+        }
+        Vec8<T>::store(dy + pos * H + c, o);
+      }
+      dot = wave_sum(dot);
+      if (lane == 0) store_scalar<TW>(dw + q, dot);
+    }
   }
 }
 
-template <typename T>
+// dx[t] = (add[t] +) sum_k dx_perm[inv_pos[t*K + k]]; HAS_ADD only with a non-null add
+template <typename T, int KC, bool HAS_ADD>
 __global__ __launch_bounds__(256) void dispatch_bwd_kernel(const T* __restrict__ dx_perm,
-                                                           const int32_t* __restrict__ inv_pos, int T_, int K, int H,
+                                                           const int32_t* __restrict__ inv_pos,
+                                                           const T* __restrict__ add, int T_, int K, int H,
                                                            T* __restrict__ dx) {
-  const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  for (int c = lane * 8; c < H; c += 64 * 8) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = 0; k < K; ++k) {
-      float v[8];
-      Vec8<T>::load(dx_perm + (int64_t)inv_pos[(int64_t)t * K + k] * H + c, v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += v[i];
-    }
-    Vec8<T>::store(dx + (int64_t)t * H + c, acc);
-  }
+  gather_sum_row<T, float, KC, false, HAS_ADD>(dx_perm, nullptr, inv_pos, add, t, K, H, dx, threadIdx.x & 63);
 }
 
 unsigned blocks_for(int64_t rows, int per_block) { return (unsigned)((rows + per_block - 1) / per_block); }
@@ -573,37 +659,64 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   return hipGetLastError();
 }
 
+// Calls F with the compile-time top-k (the common values) or 0 (runtime K).
+template <class F>
+hipError_t with_kc(int K, F&& f) {
+  switch (K) {
+    case 1: return f(std::integral_constant<int, 1>());
+    case 2: return f(std::integral_constant<int, 2>());
+    case 4: return f(std::integral_constant<int, 4>());
+    case 6: return f(std::integral_constant<int, 6>());
+    case 8: return f(std::integral_constant<int, 8>());
+    default: return f(std::integral_constant<int, 0>());
+  }
+}
+
 template <typename T>
-hipError_t dispatch_rows(const T* x, const int32_t* sorted_pair, int P, int K, int H, T* x_perm, hipStream_t s) {
-  if (P == 0) return hipSuccess;
-  hipLaunchKernelGGL((dispatch_kernel<T>), dim3(blocks_for(P, 4)), dim3(256), 0, s, x, sorted_pair, P, K, H, x_perm);
-  return hipGetLastError();
+hipError_t dispatch_rows(const T* x, const int32_t* inv_pos, int T_, int K, int H, T* x_perm, hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  return with_kc(K, [&](auto kc) {
+    hipLaunchKernelGGL((dispatch_kernel<T, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, x, inv_pos,
+                       T_, K, H, x_perm);
+    return hipGetLastError();
+  });
 }
 
 template <typename T, typename TW>
 hipError_t combine_rows(const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H, T* out,
                         hipStream_t s) {
   if (T_ == 0) return hipSuccess;
-  hipLaunchKernelGGL((combine_kernel<T, TW>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, y, w, inv_pos, T_, K, H, out);
-  return hipGetLastError();
+  return with_kc(K, [&](auto kc) {
+    hipLaunchKernelGGL((combine_kernel<T, TW, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, y, w,
+                       inv_pos, T_, K, H, out);
+    return hipGetLastError();
+  });
 }
 
 template <typename T, typename TW>
 hipError_t combine_rows_bwd(const T* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K, int H,
                             T* dy, TW* dw, hipStream_t s) {
   if (T_ == 0) return hipSuccess;
-  hipLaunchKernelGGL((combine_bwd_kernel<T, TW>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, dout, y, w, inv_pos, T_,
-                     K, H, dy, dw);
-  return hipGetLastError();
+  return with_kc(K, [&](auto kc) {
+    hipLaunchKernelGGL((combine_bwd_kernel<T, TW, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256), 0, s,
+                       dout, y, w, inv_pos, T_, K, H, dy, dw);
+    return hipGetLastError();
+  });
 }
 
 template <typename T>
-hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, int T_, int K, int H, T* dx,
+hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* add, int T_, int K, int H, T* dx,
                              hipStream_t s) {
   if (T_ == 0) return hipSuccess;
-  hipLaunchKernelGGL((dispatch_bwd_kernel<T>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, dx_perm, inv_pos, T_, K, H,
-                     dx);
-  return hipGetLastError();
+  return with_kc(K, [&](auto kc) {
+    if (add != nullptr)
+      hipLaunchKernelGGL((dispatch_bwd_kernel<T, decltype(kc)::value, true>), dim3(blocks_for(T_, 4)), dim3(256), 0,
+                         s, dx_perm, inv_pos, add, T_, K, H, dx);
+    else
+      hipLaunchKernelGGL((dispatch_bwd_kernel<T, decltype(kc)::value, false>), dim3(blocks_for(T_, 4)), dim3(256), 0,
+                         s, dx_perm, inv_pos, add, T_, K, H, dx);
+    return hipGetLastError();
+  });
 }
 
 template hipError_t router_topk<bf16_t>(const float*, int, int64_t, float*, const float*, int, int, int, int, bf16_t*,
@@ -619,7 +732,7 @@ template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*,
 
 #define PMOE_INST_ROWS(T)                                                                                      \
   template hipError_t dispatch_rows<T>(const T*, const int32_t*, int, int, int, T*, hipStream_t);              \
-  template hipError_t dispatch_rows_bwd<T>(const T*, const int32_t*, int, int, int, T*, hipStream_t);          \
+  template hipError_t dispatch_rows_bwd<T>(const T*, const int32_t*, const T*, int, int, int, T*, hipStream_t); \
   template hipError_t combine_rows<T, bf16_t>(const T*, const bf16_t*, const int32_t*, int, int, int, T*,      \
                                               hipStream_t);                                                    \
   template hipError_t combine_rows<T, float>(const T*, const float*, const int32_t*, int, int, int, T*,        \

@@ -152,7 +152,7 @@ class _ExpertFFNFunction(torch.autograd.Function):
         with _stage("permute"):
             counts, offs, sorted_pair, inv_pos = ops.permute(top_indices, E)
         with _stage("dispatch"):
-            x_perm = ops.dispatch(hidden, sorted_pair, K)
+            x_perm = ops.dispatch(hidden, inv_pos, K)
         with _stage("gate_up_fwd"):
             gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
         with _stage("down_fwd"):
@@ -195,6 +195,117 @@ class _ExpertFFNFunction(torch.autograd.Function):
             with _stage("gate_up_wgrad"):
                 g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
         return g_hidden, None, (g_w if need[2] else None), g_gu_w, g_dn_w
+
+
+# ------------------------------------------------- whole sparse MLP block
+
+
+class _SparseMoEFunction(torch.autograd.Function):
+    """Router + dropless experts as one autograd node (Qwen3MoeSparseMLP.forward).
+
+    Outputs ``(out, router_logits)``: the logits stay graph-connected for the
+    aux losses. In the backward the router's share of the input gradient is
+    computed first and folded into the dispatch-backward sum, so the two input
+    gradients are never added by a separate pass.
+    """
+
+    @staticmethod
+    def forward(ctx, x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+        E = gate_up_proj.shape[0]
+        K = int(top_k)
+        with _stage("router_fwd"):
+            logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
+                x, router_weight, K, norm_topk_prob, logit_bias)
+        with _stage("permute"):
+            _, offs, _, inv_pos = ops.permute(top_i, E)
+        with _stage("dispatch"):
+            x_perm = ops.dispatch(x, inv_pos, K)
+        with _stage("gate_up_fwd"):
+            gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
+        with _stage("down_fwd"):
+            y = ops.down_proj(mid, down_proj, offs)
+        with _stage("combine"):
+            out = ops.combine(y, top_w, inv_pos)
+        ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, top_w, gate_up_proj, down_proj, offs, inv_pos,
+                              x_perm, gu, mid, y)
+        ctx.norm_topk_prob = bool(norm_topk_prob)
+        ctx.dims = (x.shape[0], K, E)
+        ctx.mark_non_differentiable(counts, psum, lse2)
+        ctx.set_materialize_grads(False)
+        return out, logits, counts, psum, lse2
+
+    @staticmethod
+    def backward(ctx, g_out, g_logits, _gc, _gp, _gl):
+        (x, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
+         y) = ctx.saved_tensors
+        T, K, E = ctx.dims
+        need = ctx.needs_input_grad
+        if g_out is None and g_logits is None:
+            return None, None, None, None, None, None, None
+        if g_logits is not None:
+            g_logits = g_logits.float().contiguous()
+        g_x = g_rw = g_gu_w = g_dn_w = None
+        g_tw = None
+        g_y = None
+        if g_out is not None:
+            g_out = g_out.contiguous()
+            if g_out.dtype != x_perm.dtype:
+                g_out = g_out.to(x_perm.dtype)
+            with _stage("combine_bwd"):
+                g_y, g_tw = ops.combine_backward(g_out, y, top_w, inv_pos)
+        gx_router = None
+        if need[0] or need[1]:
+            with _stage("router_bwd"):
+                gx_router, g_rw = ops.router_backward(x, rw, logits, top_i, top_w32, g_tw, g_logits,
+                                                      ctx.norm_topk_prob)
+        if g_y is not None:
+            g_gu = None
+            if need[0] or need[2]:
+                with _stage("down_dgrad"):
+                    g_gu = ops.down_proj_dgrad(g_y, gu, down, offs)
+            if need[3]:
+                with _stage("down_wgrad"):
+                    g_dn_w = ops.down_proj_wgrad(g_y, mid, offs, E)
+            del g_y
+            if need[0]:
+                with _stage("gate_up_dgrad"):
+                    g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
+                with _stage("dispatch_bwd"):
+                    g_x = ops.dispatch_backward(g_xp, inv_pos, T, K, add=gx_router)
+                del g_xp
+            if need[2]:
+                with _stage("gate_up_wgrad"):
+                    g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+        elif need[0]:
+            g_x = gx_router
+        return (g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w, g_dn_w, None, None, None
+
+
+def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_proj: torch.Tensor,
+                     down_proj: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
+                     logit_bias: torch.Tensor | None = None):
+    """Router + experts of ``Qwen3MoeSparseMLP.forward`` (qwen3_moe.py:233-239) on HIP.
+
+    ``hidden`` (T, H). Returns ``(out (T,H), router_logits (T,E) fp32,
+    RouterStats)``; the logits carry the gradient of any aux loss. Same
+    arithmetic as ``router_topk`` followed by ``moe_expert_ffn``.
+    """
+    assert hidden.dim() == 2 and router_weight.dim() == 2 and router_weight.shape[1] == hidden.shape[1]
+    assert gate_up_proj.dim() == 3 and down_proj.dim() == 3
+    assert 1 <= top_k <= router_weight.shape[0]
+    require_gpu(hidden, router_weight, gate_up_proj, down_proj, logit_bias)
+    dt = hidden.dtype
+    x = hidden.contiguous()
+    rw = router_weight.contiguous()
+    if rw.dtype not in (torch.float32, torch.bfloat16):
+        rw = rw.float()
+    gu = gate_up_proj.to(dtype=dt).contiguous()
+    dn = down_proj.to(dtype=dt).contiguous()
+    if logit_bias is not None:
+        logit_bias = logit_bias.float().contiguous()
+    out, logits, counts, psum, lse2 = _SparseMoEFunction.apply(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
+                                                                logit_bias)
+    return out, logits, RouterStats(counts, psum, lse2, x.shape[0])
 
 
 def moe_expert_ffn(

@@ -68,10 +68,11 @@ def permute(top_indices, num_experts: int):
     return counts, offs, sorted_pair, inv_pos
 
 
-def dispatch(hidden, sorted_pair, top_k: int):
+def dispatch(hidden, inv_pos, top_k: int):
+    """x_perm[inv_pos[t*K + k]] = hidden[t] (the expert-sorted row gather)."""
     T, H = hidden.shape
     x_perm = torch.empty(T * top_k, H, dtype=hidden.dtype, device=hidden.device)
-    call("pmoe_dispatch", ptr(hidden), dtype_code(hidden.dtype), ptr(sorted_pair), T, top_k, H, ptr(x_perm),
+    call("pmoe_dispatch", ptr(hidden), dtype_code(hidden.dtype), ptr(inv_pos), T, top_k, H, ptr(x_perm),
          stream_of(hidden))
     return x_perm
 
@@ -174,9 +175,12 @@ def gate_up_backward(grad_gate_up_out, x_perm, gate_up_proj, offs):
     return gx, gw
 
 
-def dispatch_backward(grad_x_perm, inv_pos, tokens: int, top_k: int):
+def dispatch_backward(grad_x_perm, inv_pos, tokens: int, top_k: int, add=None):
+    """grad_hidden[t] = add[t] + sum_k grad_x_perm[inv_pos[t*K + k]] (add may be None)."""
     H = grad_x_perm.shape[1]
     gh = torch.empty(tokens, H, dtype=grad_x_perm.dtype, device=grad_x_perm.device)
-    call("pmoe_dispatch_backward", ptr(grad_x_perm), ptr(inv_pos), dtype_code(grad_x_perm.dtype), tokens, top_k, H,
-         ptr(gh), stream_of(grad_x_perm))
+    if add is not None:
+        assert add.shape == gh.shape and add.dtype == gh.dtype and add.is_contiguous()
+    call("pmoe_dispatch_backward", ptr(grad_x_perm), ptr(inv_pos), ptr(add), dtype_code(grad_x_perm.dtype), tokens,
+         top_k, H, ptr(gh), stream_of(grad_x_perm))
     return gh

@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .moe import RouterStats, moe_expert_ffn, router_topk
+from .moe import RouterStats, moe_expert_ffn, router_topk, sparse_moe_block
 
 
 class Qwen3MoeTopKRouter(nn.Module):
@@ -71,9 +71,13 @@ class Qwen3MoeSparseMLP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B, S, H = x.shape
         flat = x.reshape(B * S, H)
-        logits, weights, indices = self.router(flat)
+        r = self.router
+        # router + experts as one autograd node (same arithmetic as calling
+        # self.router then self.experts, which remain usable on their own)
+        y, logits, stats = sparse_moe_block(flat, r.weight, self.experts.gate_up_proj, self.experts.down_proj,
+                                            r.top_k, r.norm_topk_prob, logit_bias=r.logit_bias)
+        r.last_stats = stats
         self.last_router_logits = logits
-        y = self.experts(flat, indices, weights)
         return y.reshape(B, S, H)
 
 

@@ -57,7 +57,7 @@ def test_permute_deterministic():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("T,K,E,H", [(300, 4, 16, 264), (64, 8, 128, 2048)])
+@pytest.mark.parametrize("T,K,E,H", [(300, 4, 16, 264), (64, 8, 128, 2048), (200, 3, 12, 520), (128, 8, 16, 4096)])
 def test_dispatch_combine(dtype, T, K, E, H):
     say(f"dispatch/combine T={T} K={K} E={E} H={H} {dtype}")
     ops = _ops()
@@ -66,7 +66,7 @@ def test_dispatch_combine(dtype, T, K, E, H):
     idx = routing(T, K, E, seed=2)
     w = torch.rand(T, K, generator=g).to(dtype)
     counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
-    xp = ops.dispatch(x.to(DEV), sp, K)
+    xp = ops.dispatch(x.to(DEV), inv, K)
     ref_xp = x[torch.from_numpy(O.permute(idx, E)[2].astype(np.int64)) // K]
     assert torch.equal(xp.cpu(), ref_xp), "dispatch must be a bit-exact gather"
     # combine: out[t] = sum_k w[t,k] * y[inv[t,k]]
@@ -89,6 +89,10 @@ def test_dispatch_combine(dtype, T, K, E, H):
     gx = ops.dispatch_backward(gxp.to(DEV), inv, T, K)
     ref_gx = gxp.double()[inv_c].sum(1)
     assert rel(gx, ref_gx) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    # with an addend row (the router's share of the input gradient), summed first
+    add = torch.randn(T, H, generator=g).to(dtype)
+    gx2 = ops.dispatch_backward(gxp.to(DEV), inv, T, K, add=add.to(DEV))
+    assert rel(gx2, ref_gx + add.double()) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
 
 
 # -------------------------------------------------------------- GEMMs
@@ -111,7 +115,7 @@ def _gemm_inputs(T, K, E, H, I, mode, dtype, seed=0):
     wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype)
     wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype)
     counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
-    xp = ops.dispatch(x.to(DEV), sp, K)
+    xp = ops.dispatch(x.to(DEV), inv, K)
     return idx, x, wgu, wdn, offs, sp, inv, xp
 
 
