@@ -122,6 +122,11 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
   const int groups = p.groups;
+#ifdef PMOE_PROBE
+  int probe_n = 0;
+#endif
+  PMOE_MARK(0);
+  PMOE_BTIME(0);
 
   // ---- tile list
   for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs[g];
@@ -164,8 +169,16 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
-  constexpr int TOTM = (KS - 1) * MI * NI;
-  static_assert(DW <= TOTM, "every DMA of a stage needs an MFMA slot");
+  // DMAs of stage kt + NS - 1 ride on the MFMAs of the first SPREAD substeps
+  // of stage kt. With a double buffer (NS = 2) the next stage has only the
+  // current one to land in, so its DMAs go out in the first substep.
+#ifdef PMOE_DMA_SPREAD
+  constexpr int SPREAD = PMOE_DMA_SPREAD < KS - 1 ? PMOE_DMA_SPREAD : KS - 1;
+#else
+  constexpr int SPREAD = NS == 2 ? 1 : KS - 1;
+#endif
+  constexpr int TOTM = SPREAD * MI * NI;
+  static_assert(SPREAD >= 1 && DW <= TOTM, "every DMA of a stage needs an MFMA slot");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
 
   // ---- per-tile state (current tile)
@@ -324,14 +337,18 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       const char* sa = smem + slot_addr(kt);
       const char* sb = sa + Cfg::A_BYTES;
       const int dma_st = kt + NS - 1 < nk ? kt + NS - 1 : -1;
+      PMOE_MARK(10);
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
         load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
         substep(ksc, af[KSI & 1], bfr[KSI & 1], dma_st);
       });
+      PMOE_MARK(11);
       // stages kt+2 .. min(kt+NS-1, nk-1) may stay in flight
       wait_stages<DW, NS>(min(NS - 2, nk - 2 - kt));
+      PMOE_MARK(12);
       lds_barrier();
+      PMOE_MARK(13);
       const char* na = smem + slot_addr(kt + 1);
       load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], -1);
@@ -345,7 +362,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         substep(ksc, af[KSI & 1], bfr[KSI & 1], -1);
       });
     }
+    PMOE_MARK(20);
     store_slabs8<Cfg, Tout, GM, EPI>(acc, stage, ti, p, wm, wn, lane);
+    PMOE_MARK(21);
     // next tile: its first NS-1 stages go into the slots after this tile's
     gs += nk;
     bi += nb;
@@ -358,7 +377,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       for (int s0 = 0; s0 < NS - 1; ++s0)
         if (s0 < nk) issue(s0);
     }
+    PMOE_MARK(22);
   }
+  PMOE_BTIME(1);
 }
 
 template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>

@@ -104,6 +104,7 @@ GEMM_CASES = [
     (300, 2, 8, 264, 40, "uniform"),      # ragged H and I (masking along k and n)
     (1024, 8, 64, 512, 128, "zipf"),       # skewed: empty experts, heavy experts
     (37, 3, 5, 128, 64, "one"),            # tiny: every group below one tile
+    (600, 4, 12, 320, 320, "zipf"),        # partial column tiles on the 64-deep-stage engine
 ]
 
 
