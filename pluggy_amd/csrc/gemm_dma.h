@@ -69,12 +69,15 @@ constexpr uint32_t kOOB = 0x80000000u;
 
 // Raw buffer over [base, base + bytes): stride 0, bound = bytes, dword 3 as
 // for untyped raw buffers on gfx9. Offsets at or past the bound read as zero.
+// Callers pass wave-uniform values; readfirstlane states that to the compiler,
+// so the descriptor stays in SGPRs (the DMA's "s" operand) even when its
+// inputs came through LDS.
 __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint64_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   BufRsrc r;
-  r[0] = (int)(uint32_t)a;
-  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = (int)(bytes >= (uint64_t)kOOB ? kOOB - 16 : (uint32_t)bytes);
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)(bytes >= (uint64_t)kOOB ? kOOB - 16 : (uint32_t)bytes));
   r[3] = 0x00020000;
   return r;
 }
@@ -164,6 +167,14 @@ struct KcDma {
       rowoff[i] = g < 0 ? kOOB : (uint32_t)(((int64_t)g * ld + 8 * c) * 2);
     }
   }
+  // this = second ? y : x, element by element (stays in registers)
+  __device__ __forceinline__ void select(bool second, const KcDma& y, const KcDma& x) {
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      rowoff[i] = second ? y.rowoff[i] : x.rowoff[i];
+      kc[i] = second ? y.kc[i] : x.kc[i];
+    }
+  }
   // k0: first k of the stage relative to the descriptor; tail: the stage
   // reaches past k_hi (only then are lanes checked one by one).
   // instruction I of the stage at LDS byte address tile
@@ -202,6 +213,13 @@ struct TDma {
       const int col = r0 + 8 * c;
       kk[i] = k;
       coloff[i] = col < r_limit ? (uint32_t)(col * 2) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void select(bool second, const TDma& y, const TDma& x) {
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      kk[i] = second ? y.kk[i] : x.kk[i];
+      coloff[i] = second ? y.coloff[i] : x.coloff[i];
     }
   }
   template <int I>

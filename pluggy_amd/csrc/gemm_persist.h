@@ -103,12 +103,19 @@ __device__ __forceinline__ void store_slabs8(const f32x16 (&acc)[Cfg::MI][Cfg::N
   }
 }
 
+// The block's tiles form one continuous stream of k-stages: stage g lives in
+// ring slot g % NS, and the DMAs issued during stage g fetch stream stage
+// g + NS - 1, which in a tile's last NS - 1 stages is one of the next tile's
+// first stages. The pipeline therefore stays full across tile boundaries (the
+// next tile's first stages land while this tile's last stages and epilogue
+// run), every stage issues the same DMAs (no branches in the k-loop), and the
+// wait before each barrier is the same vmcnt.
 template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
 __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
-  constexpr int MI = Cfg::MI, NI = Cfg::NI, DW = Cfg::DW;
-  constexpr bool SPLIT = Cfg::SPLIT;
+  constexpr int MI = Cfg::MI, NI = Cfg::NI;
   typedef PersistLayout<Cfg> L;
+  static_assert(!Cfg::SPLIT, "every wave issues its share of the DMAs");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && NI % 2 == 0), "SwiGLU epilogue layout");
@@ -128,49 +135,34 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   PMOE_MARK(0);
   PMOE_BTIME(0);
 
-  // ---- tile list
+  // ---- tile list: GM_ROWS m-tiles follow the per-group row counts
   for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs[g];
   __syncthreads();
   const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   const int mt_red = (p.M + BM - 1) / BM;  // GM_RED: m-tiles per group
   int total;
-  if constexpr (GM == GM_ROWS) {
-    if (tid < 64) {
-      int carry = 0;
-      for (int base = 0; base < groups; base += 64) {
-        const int g = base + lane;
-        int tiles = 0;
-        if (g < groups) tiles = (s_offs[g] - (g == 0 ? 0 : s_offs[g - 1]) + BM - 1) / BM;
-        const int inc = wave_incl_scan(tiles, lane) + carry;
-        if (g < groups) s_scan[g + 1] = inc;
-        carry = __shfl(inc, 63, kWave);
-      }
-      if (lane == 0) s_scan[0] = 0;
-    }
-    __syncthreads();
-    total = s_scan[groups] * ntiles_n;
-  } else {
-    total = groups * mt_red * ntiles_n;
-  }
+  if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
+  else total = groups * mt_red * ntiles_n;
+  // XCD x (blocks with blockIdx % 8 == x) takes a contiguous share of the tiles
+  // and its blocks walk it in a stride of their count.
   const int xcd = blockIdx.x & 7;
-  int bi = blockIdx.x >> 3;  // this block's next position in the XCD share
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
   const int per = total >> 3, rem = total & 7;
   const int cnt = per + (xcd < rem ? 1 : 0);
   const int start = xcd * per + (xcd < rem ? xcd : rem);
+  int bi = blockIdx.x >> 3;  // this block's position in the XCD share
+  if (bi >= cnt) return;
 
   const uint32_t lds0 = lds_addr(smem);
   float* stage = s_epi + wave * 8 * L::EPI_LD;
   const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
-  const bool dma_wave = !SPLIT || wave < NW / 2;
-  const int vw0 = wave, vw1 = SPLIT ? wave + NW / 2 : wave;
   typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
   typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
-  // DMAs of stage kt + NS - 1 ride on the MFMAs of the first SPREAD substeps
-  // of stage kt. With a double buffer (NS = 2) the next stage has only the
+  // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
+  // of stage g. With a double buffer (NS = 2) the next stage has only the
   // current one to land in, so its DMAs go out in the first substep.
 #ifdef PMOE_DMA_SPREAD
   constexpr int SPREAD = PMOE_DMA_SPREAD < KS - 1 ? PMOE_DMA_SPREAD : KS - 1;
@@ -178,110 +170,103 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int SPREAD = NS == 2 ? 1 : KS - 1;
 #endif
   constexpr int TOTM = SPREAD * MI * NI;
-  static_assert(SPREAD >= 1 && DW <= TOTM, "every DMA of a stage needs an MFMA slot");
+  static_assert(SPREAD >= 1 && D <= TOTM, "every DMA of a stage needs an MFMA slot");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
 
-  // ---- per-tile state (current tile)
-  TileInfo ti;
-  BufRsrc rsA, rsB;
-  LdA la0, la1;
-  LdB lb0, lb1;
-  int nk = 0, kd0 = 0, kd_hi = 0;
-
-  // Sets ti, the descriptors and nk for tile t.
-  auto setup = [&](int t) {
-    const int tn = t % ntiles_n, slot = t / ntiles_n;
-    const bf16_t* A = A0;
-    const bf16_t* B = B0;
-    if constexpr (GM == GM_ROWS) {
-      const int g = rows_group(s_scan, groups, slot);
-      const int lo = g == 0 ? 0 : s_offs[g - 1];
-      ti.group = g; ti.m0 = lo + (slot - s_scan[g]) * BM; ti.m_end = s_offs[g]; ti.k_lo = 0; ti.k_hi = p.K;
-      B += (int64_t)g * p.strideB;
-    } else {
-      const int g = slot / mt_red;
-      ti.group = g; ti.m0 = (slot % mt_red) * BM; ti.m_end = p.M;
-      ti.k_lo = g == 0 ? 0 : s_offs[g - 1];
-      ti.k_hi = s_offs[g];
-    }
-    ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
-    const bf16_t* a_base = A;
-    uint64_t a_bytes = p.a_bytes;
-    const bf16_t* b_base = B;
-    uint64_t b_bytes = p.b_bytes;
-    if constexpr (A_KC) {
-      a_base = A + (int64_t)ti.m0 * p.lda;
-      a_bytes = (uint64_t)(ti.m_end - ti.m0) * p.lda * 2;
-    } else {
-      a_base = A + (int64_t)ti.k_lo * p.lda;
-      a_bytes = (uint64_t)(ti.k_hi - ti.k_lo) * p.lda * 2;
-    }
-    if constexpr (GM == GM_RED) {
-      b_base = B + (int64_t)ti.k_lo * p.ldb;
-      b_bytes = (uint64_t)(ti.k_hi - ti.k_lo) * p.ldb * 2;
-    }
-    rsA = make_rsrc(a_base, a_bytes);
-    rsB = make_rsrc(b_base, b_bytes);
-    auto init_a = [&](LdA& la, int vw) {
+  // What the DMAs of one tile need. nk is padded to at least NS - 1 stages
+  // (the extra stages read zeros), so the DMAs of a tile's last NS - 1 stages
+  // always fetch the following tile's first stages.
+  struct LoadTile {
+    TileInfo ti;
+    BufRsrc rsA, rsB;
+    LdA la;
+    LdB lb;
+    int nk, kd0, kd_hi;
+  };
+  // Tile ordinal b of this block's share (b >= cnt: past the last tile; its
+  // descriptors are empty, so every DMA reads zeros).
+  auto setup = [&](int b, LoadTile& T) {
+    T.ti.group = 0; T.ti.m0 = 0; T.ti.m_end = 0; T.ti.n0 = 0; T.ti.k_lo = 0; T.ti.k_hi = 0;
+    T.nk = NS - 1;
+    T.kd0 = 0;
+    T.kd_hi = 0;
+    const bf16_t* a_base = A0;
+    const bf16_t* b_base = B0;
+    uint64_t a_bytes = 0, b_bytes = 0;
+    if (b < cnt) {
+      const int t = start + b;
+      const int tn = t % ntiles_n, slot = t / ntiles_n;
+      if constexpr (GM == GM_ROWS) {
+        const int g = rows_group(s_scan, groups, slot);
+        const int lo = g == 0 ? 0 : s_offs[g - 1];
+        T.ti.group = g; T.ti.m0 = lo + (slot - s_scan[g]) * BM; T.ti.m_end = s_offs[g];
+        T.ti.k_lo = 0; T.ti.k_hi = p.K;
+        b_base = B0 + (int64_t)g * p.strideB;
+        b_bytes = p.b_bytes;
+      } else {
+        const int g = slot / mt_red;
+        T.ti.group = g; T.ti.m0 = (slot % mt_red) * BM; T.ti.m_end = p.M;
+        T.ti.k_lo = g == 0 ? 0 : s_offs[g - 1];
+        T.ti.k_hi = s_offs[g];
+      }
+      T.ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
       if constexpr (A_KC) {
-        const int rows = ti.m_end - ti.m0;
-        la.init([&](int r) { return r < rows ? r : -1; }, p.lda, vw, lane);
+        a_base = A0 + (int64_t)T.ti.m0 * p.lda;
+        a_bytes = (uint64_t)(T.ti.m_end - T.ti.m0) * p.lda * 2;
       } else {
-        la.init(ti.m0, ti.m_end, vw, lane);
+        a_base = A0 + (int64_t)T.ti.k_lo * p.lda;
+        a_bytes = (uint64_t)(T.ti.k_hi - T.ti.k_lo) * p.lda * 2;
       }
-    };
-    auto init_b = [&](LdB& lb, int vw) {
-      if constexpr (B_KC) {
-        const int n0 = ti.n0, N = p.N, I = p.inter;
-        if constexpr (EPI == EPI_SWIGLU) {
-          lb.init([&](int c) {
-            const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
-            const int gcol = n0 + w * h + (cc % h);
-            if (gcol >= I) return -1;
-            return cc < h ? gcol : I + gcol;
-          }, p.ldb, vw, lane);
-        } else {
-          lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, vw, lane);
-        }
-      } else {
-        lb.init(ti.n0, p.N, vw, lane);
+      if constexpr (GM == GM_RED) {
+        b_base = B0 + (int64_t)T.ti.k_lo * p.ldb;
+        b_bytes = (uint64_t)(T.ti.k_hi - T.ti.k_lo) * p.ldb * 2;
       }
-    };
-    init_a(la0, vw0);
-    init_b(lb0, vw0);
-    if constexpr (SPLIT) {
-      init_a(la1, vw1);
-      init_b(lb1, vw1);
+      const int klen = T.ti.k_hi - T.ti.k_lo;
+      T.nk = max((klen + BK - 1) / BK, NS - 1);
+      T.kd0 = (GM == GM_RED) ? 0 : T.ti.k_lo;
+      T.kd_hi = T.ti.k_hi - ((GM == GM_RED) ? T.ti.k_lo : 0);
     }
-    const int klen = ti.k_hi - ti.k_lo;
-    nk = klen > 0 ? (klen + BK - 1) / BK : 0;
-    kd0 = (GM == GM_RED) ? 0 : ti.k_lo;
-    kd_hi = ti.k_hi - ((GM == GM_RED) ? ti.k_lo : 0);
+    T.rsA = make_rsrc(a_base, a_bytes);
+    T.rsB = make_rsrc(b_base, b_bytes);
+    if constexpr (A_KC) {
+      const int rows = T.ti.m_end - T.ti.m0;
+      T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
+    } else {
+      T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
+    }
+    if constexpr (B_KC) {
+      const int n0 = T.ti.n0, N = p.N, I = p.inter;
+      if constexpr (EPI == EPI_SWIGLU) {
+        // wave column block w holds WN/2 gate columns then the matching up columns
+        T.lb.init([&](int c) {
+          const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
+          const int gcol = n0 + w * h + (cc % h);
+          if (gcol >= I) return -1;
+          return cc < h ? gcol : I + gcol;
+        }, p.ldb, wave, lane);
+      } else {
+        T.lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, wave, lane);
+      }
+    } else {
+      T.lb.init(T.ti.n0, p.N, wave, lane);
+    }
   };
 
-  int gs = 0;  // global stage counter: stage kt of the current tile lives in slot (gs + kt) % NS
-  auto slot_addr = [&](int kt) { return (uint32_t)(((gs + kt) % NS) * Cfg::STAGE_BYTES); };
-
-  auto dma_share = [&](int kt, auto jc, const LdA& la, const LdB& lb, int vw) {
+  int gs = 0;  // stream stage of the current tile's stage 0
+  auto slot_of = [&](int g) { return (uint32_t)((g % NS) * Cfg::STAGE_BYTES); };
+  // DMA J of stage ls of tile T, into the ring slot of stream stage g.
+  auto dma_one = [&](const LoadTile& T, int ls, int g, auto jc) {
     constexpr int J = decltype(jc)::value;
-    const uint32_t st = lds0 + slot_addr(kt);
-    const int k0 = kd0 + kt * BK;
+    const uint32_t st = lds0 + slot_of(g);
+    const int k0 = T.kd0 + ls * BK;
     if constexpr (J < Cfg::A_INSTR) {
-      if constexpr (A_KC) la.template issue1<J>(rsA, st, k0, kd_hi, k0 + BK > kd_hi, vw);
-      else la.template issue1<J>(rsA, st, k0, p.lda, vw);
+      if constexpr (A_KC) T.la.template issue1<J>(T.rsA, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+      else T.la.template issue1<J>(T.rsA, st, k0, p.lda, wave);
     } else {
       constexpr int JB = J - Cfg::A_INSTR;
-      if constexpr (B_KC) lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, kd_hi, k0 + BK > kd_hi, vw);
-      else lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, p.ldb, vw);
+      if constexpr (B_KC) T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+      else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
-  };
-  auto dma_one = [&](int kt, auto jc) {
-    constexpr int J = decltype(jc)::value;
-    if constexpr (J < D) dma_share(kt, jc, la0, lb0, vw0);
-    else dma_share(kt, std::integral_constant<int, J - D>(), la1, lb1, vw1);
-  };
-  auto issue = [&](int kt) {
-    if (dma_wave) static_for<0, DW>([&](auto jc) { dma_one(kt, jc); });
   };
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
 #pragma unroll
@@ -297,88 +282,89 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   };
 
   f32x16 acc[MI][NI];
-  auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], int dma_st) {
+  // One 16-k substep; with WITH_DMA the stage's D DMAs ride on its MFMAs.
+  auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], const LoadTile& T, int ls,
+                     int g) {
     constexpr int KSI = decltype(ksc)::value;
     static_for<0, MI * NI>([&](auto mc) {
       constexpr int M = decltype(mc)::value;
       acc[M / NI][M % NI] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
       constexpr int G = KSI * MI * NI + M;
-      static_for<0, DW>([&](auto dc) {
+      static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
-        if constexpr ((DI * TOTM) / DW == G) {
-          if (dma_st >= 0 && dma_wave) dma_one(dma_st, dc);
+        if constexpr ((DI * TOTM) / D == G) {
+          dma_one(T, ls, g, dc);
+          // keep the DMA between its MFMAs (MFMAs are not memory operations,
+          // so the DMA's memory clobber alone would let them drift past it)
+          __builtin_amdgcn_sched_barrier(0);
         }
       });
     });
   };
 
+  LoadTile cur, nxt;
+  setup(bi, cur);
+  setup(bi + nb, nxt);
+  // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
+  for (int s0 = 0; s0 < NS - 1; ++s0) static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, jc); });
+  wait_stages<D, NS>(NS - 2);
+  lds_barrier();
   bf16x8 af[2][MI], bfr[2][NI];
-  int t = bi < cnt ? start + bi : -1;
-  if (t >= 0) {
-    setup(t);
-    for (int s0 = 0; s0 < NS - 1; ++s0)
-      if (s0 < nk) issue(s0);
-  }
-  while (t >= 0) {
+  load_frags(smem, smem + Cfg::A_BYTES, 0, af[0], bfr[0]);
+
+  for (;;) {
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    if (nk > 0) {
-      wait_stages<DW, NS>(min(NS - 1, nk) - 1);
-      lds_barrier();  // stage 0 visible; every wave is past the previous tile
-      const char* s0 = smem + slot_addr(0);
-      load_frags(s0, s0 + Cfg::A_BYTES, 0, af[0], bfr[0]);
-    }
-    for (int kt = 0; kt + 1 < nk; ++kt) {
-      const char* sa = smem + slot_addr(kt);
+    const int nk = cur.nk;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int g = gs + kt;
+      const char* sa = smem + slot_of(g);
       const char* sb = sa + Cfg::A_BYTES;
-      const int dma_st = kt + NS - 1 < nk ? kt + NS - 1 : -1;
+      // the DMAs of this stage: stream stage g + NS - 1
+      const int s = kt + NS - 1;
+      const bool in_next = s >= nk;
+      LoadTile T;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {  // uniform: the descriptors stay in SGPRs
+        T.rsA[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsA[w] : cur.rsA[w]);
+        T.rsB[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsB[w] : cur.rsB[w]);
+      }
+      T.la.select(in_next, nxt.la, cur.la);
+      T.lb.select(in_next, nxt.lb, cur.lb);
+      T.kd0 = in_next ? nxt.kd0 : cur.kd0;
+      T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
+      const int ls = in_next ? s - nk : s;
       PMOE_MARK(10);
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
         load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
-        substep(ksc, af[KSI & 1], bfr[KSI & 1], dma_st);
+        substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1);
       });
       PMOE_MARK(11);
-      // stages kt+2 .. min(kt+NS-1, nk-1) may stay in flight
-      wait_stages<DW, NS>(min(NS - 2, nk - 2 - kt));
+      wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
       PMOE_MARK(12);
-      lds_barrier();
+      lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
       PMOE_MARK(13);
-      const char* na = smem + slot_addr(kt + 1);
+      const char* na = smem + slot_of(g + 1);
       load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
-      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], -1);
-    }
-    if (nk > 0) {
-      const char* sa = smem + slot_addr(nk - 1);
-      const char* sb = sa + Cfg::A_BYTES;
-      static_for<0, KS>([&](auto ksc) {
-        constexpr int KSI = decltype(ksc)::value;
-        if constexpr (KSI + 1 < KS) load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
-        substep(ksc, af[KSI & 1], bfr[KSI & 1], -1);
-      });
+      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1);
     }
     PMOE_MARK(20);
-    store_slabs8<Cfg, Tout, GM, EPI>(acc, stage, ti, p, wm, wn, lane);
+    store_slabs8<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
     PMOE_MARK(21);
-    // next tile: its first NS-1 stages go into the slots after this tile's
     gs += nk;
     bi += nb;
-    t = bi < cnt ? start + bi : -1;
-    if (t >= 0) {
-      // Stages 0 .. NS-2 go to the slots after the previous tile's last one,
-      // all retired at its last barrier; the slot of its last stage is reused
-      // only by stage NS-1, issued after this tile's first barrier.
-      setup(t);
-      for (int s0 = 0; s0 < NS - 1; ++s0)
-        if (s0 < nk) issue(s0);
-    }
+    if (bi >= cnt) break;
+    cur = nxt;
+    setup(bi + nb, nxt);
     PMOE_MARK(22);
   }
+  wait_vmcnt<0>();  // the zero-reading DMAs past the last tile
   PMOE_BTIME(1);
 }
 
