@@ -15,13 +15,14 @@ template <typename T> struct CfgFor;
 template <> struct CfgFor<bf16_t> { typedef CfgBf16 type; };
 template <> struct CfgFor<float> { typedef CfgF32 type; };
 
-// bf16 expert GEMMs run on the DMA engine: 256x256 blocks of eight 128x64
-// wave tiles (two waves per SIMD, one block per CU) with a four-stage ring of
-// 32-deep k tiles (128 KiB of LDS). Chosen by measurement at the
+// bf16 expert GEMMs run on the persistent DMA engine: 256x256 blocks of eight
+// 128x64 wave tiles (two waves per SIMD, one block per CU) with a three-stage
+// ring of 32-deep k tiles (96 KiB of LDS; a fourth stage measured no faster)
+// and 16-row epilogue slabs (35 KiB). Chosen by measurement at the
 // Qwen3-30B-A3B shape over 128x128 .. 256x256 tilings, 2..5 stages and
 // 32/64-deep k tiles: larger tiles fetch fewer bytes per MFMA through each
 // CU's vector-memory path, which bounds the smaller ones.
-typedef DmaCfg<256, 256, 128, 64, 4, 32, 1, 0> DmaExpert;
+typedef DmaCfg<256, 256, 128, 64, 3, 32, 1, 0> DmaExpert;
 #ifndef PMOE_CFG_GATE_UP_FWD
 #define PMOE_CFG_GATE_UP_FWD DmaExpert
 #endif

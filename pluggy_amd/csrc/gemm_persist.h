@@ -23,17 +23,22 @@ namespace pmoe {
 template <class Cfg>
 struct PersistLayout {
   static constexpr int RING = Cfg::NS * Cfg::STAGE_BYTES;
+  static constexpr int SLAB = 16;                             // rows per epilogue slab
   static constexpr int EPI_LD = Cfg::WN + 4;                  // floats per staged row
-  static constexpr int EPI_FLOATS = Cfg::NW * 8 * EPI_LD;     // 8 rows per wave
+  static constexpr int EPI_FLOATS = Cfg::NW * SLAB * EPI_LD;  // one slab per wave
   static_assert(EPI_LD % 4 == 0, "16-byte aligned staging rows");
 };
 
-// Epilogue through per-wave 8-row slabs: slab (i, q) holds rows 8q .. 8q+7 of
-// the wave's 32-row block i (lane half h holds rows 8q + 4h + r, r = 0..3).
+// Epilogue through per-wave 16-row slabs: slab (i, h2) holds rows 16 h2 ..
+// 16 h2 + 15 of the wave's 32-row block i. In the MFMA 32x32 layout lane half
+// h holds rows 8 q + 4 h + r (r = 0..3) of a block, so slab h2 gathers q =
+// 2 h2 and 2 h2 + 1: local row 8 (q - 2 h2) + 4 h + r. Each lane then reads 8
+// consecutive outputs and stores 16 bytes.
 template <class Cfg, typename Tout, int GM, int EPI>
-__device__ __forceinline__ void store_slabs8(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
-                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
-  constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN, LD = PersistLayout<Cfg>::EPI_LD;
+__device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
+                                            const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN;
+  constexpr int LD = PersistLayout<Cfg>::EPI_LD, SLAB = PersistLayout<Cfg>::SLAB;
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
@@ -41,37 +46,42 @@ __device__ __forceinline__ void store_slabs8(const f32x16 (&acc)[Cfg::MI][Cfg::N
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
+      for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) stage[(4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * q + r];
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            stage[(8 * qq + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * (2 * h2 + qq) + r];
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
       asm volatile("" ::: "memory");
-      const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + 8 * q;
+      const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * h2;
       if constexpr (EPI == EPI_SWIGLU) {
         constexpr int H2 = WN / 2, CPR = H2 / 8;
-        static_assert(8 * CPR <= 64, "one 8-row slab per wave instruction");
         bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
-        const int r = lane / CPR, c = (lane % CPR) * 8;
-        const int row = row_base + r, col = ti.n0 + wn * H2 + c;
-        if (lane < 8 * CPR && row < ti.m_end && col < p.inter) {
-          float g[8], u[8], m[8];
-          Vec8<float>::load(stage + r * LD + c, g);
-          Vec8<float>::load(stage + r * LD + H2 + c, u);
-          const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
-          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
-          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
-          unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
-          unpack8(uw, u);
 #pragma unroll
-          for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
-          Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
+        for (int e = lane; e < SLAB * CPR; e += 64) {
+          const int r = e / CPR, c = (e % CPR) * 8;
+          const int row = row_base + r, col = ti.n0 + wn * H2 + c;
+          if (row < ti.m_end && col < p.inter) {
+            float g[8], u[8], m[8];
+            Vec8<float>::load(stage + r * LD + c, g);
+            Vec8<float>::load(stage + r * LD + H2 + c, u);
+            const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
+            *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
+            *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
+            unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
+            unpack8(uw, u);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
+            Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
+          }
         }
       } else {
         constexpr int CPR = WN / 8;
 #pragma unroll
-        for (int e = lane; e < 8 * CPR; e += 64) {
+        for (int e = lane; e < SLAB * CPR; e += 64) {
           const int r = e / CPR, c = (e % CPR) * 8;
           const int row = row_base + r, col = ti.n0 + wn * WN + c;
           if (row < ti.m_end && col < p.N) {
@@ -99,6 +109,7 @@ __device__ __forceinline__ void store_slabs8(const f32x16 (&acc)[Cfg::MI][Cfg::N
           }
         }
       }
+      // (the next slab's writes follow these reads in the wave's LDS order)
     }
   }
 }
@@ -154,7 +165,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   if (bi >= cnt) return;
 
   const uint32_t lds0 = lds_addr(smem);
-  float* stage = s_epi + wave * 8 * L::EPI_LD;
+  float* stage = s_epi + wave * L::SLAB * L::EPI_LD;
   const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
   typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
@@ -195,9 +206,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     uint64_t a_bytes = 0, b_bytes = 0;
     if (b < cnt) {
       const int t = start + b;
-      const int tn = t % ntiles_n, slot = t / ntiles_n;
+      int tn = t % ntiles_n, slot = t / ntiles_n;
       if constexpr (GM == GM_ROWS) {
+        // An expert's tiles are ordered n-tile major, its m-tiles inner, so
+        // that the m-tiles sharing a weight block run next to each other.
         const int g = rows_group(s_scan, groups, slot);
+        const int ns = s_scan[g + 1] - s_scan[g], local = t - s_scan[g] * ntiles_n;
+        tn = local / ns;
+        slot = s_scan[g] + local % ns;
         const int lo = g == 0 ? 0 : s_offs[g - 1];
         T.ti.group = g; T.ti.m0 = lo + (slot - s_scan[g]) * BM; T.ti.m_end = s_offs[g];
         T.ti.k_lo = 0; T.ti.k_hi = p.K;
@@ -355,7 +371,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1);
     }
     PMOE_MARK(20);
-    store_slabs8<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
+    store_slabs<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
     PMOE_MARK(21);
     gs += nk;
     bi += nb;
