@@ -323,28 +323,72 @@ __global__ __launch_bounds__(256) void permute_hist_kernel(const int64_t* __rest
 
 // One block of 1024 threads: per-expert scan over chunks, then an exclusive
 // scan over experts. chunk_hist becomes the global base of (chunk, expert).
+// TPE threads share an expert; thread s of expert e takes a contiguous run of
+// chunks, so each pass is TPE independent streams of coalesced loads rather
+// than one dependent chain over all chunks.
 __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict__ chunk_hist, int nchunks, int E,
                                                             int32_t* __restrict__ counts, int32_t* __restrict__ offs) {
+  __shared__ int s_part[1024];
+  __shared__ int s_tot[1024];
   __shared__ int s_wsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int total = 0;
-  if (tid < E) {
-    for (int c = 0; c < nchunks; ++c) {
-      const int v = chunk_hist[(int64_t)c * E + tid];
-      chunk_hist[(int64_t)c * E + tid] = total;
+  int tpe = 1;
+  while (tpe * 2 * E <= 1024) tpe *= 2;  // threads per expert (E <= 1024)
+  const int e = tid / tpe, sub = tid % tpe;
+  const int cps = (nchunks + tpe - 1) / tpe;
+  const int c0 = min(nchunks, sub * cps), c1 = min(nchunks, c0 + cps);
+  // chunks go through registers 32 at a time, so their loads are issued
+  // together instead of one dependent load per chunk
+  constexpr int RUN = 32;
+  int part = 0;
+  if (e < E) {
+    for (int cb = c0; cb < c1; cb += RUN) {
+      int v[RUN];
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) v[i] = cb + i < c1 ? chunk_hist[(int64_t)(cb + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) part += v[i];
+    }
+  }
+  s_part[tid] = part;
+  __syncthreads();
+  // per-expert total and this thread's prefix within its expert
+  int pre = 0, total = 0;
+  if (e < E) {
+    for (int j = 0; j < tpe; ++j) {
+      const int v = s_part[e * tpe + j];
+      if (j < sub) pre += v;
       total += v;
     }
   }
-  const int inc = wave_incl_scan(total, lane);
+  // exclusive scan of the expert totals (thread t < E reads expert t's total)
+  if (e < E && sub == 0) s_tot[e] = total;
+  __syncthreads();
+  const int tv = tid < E ? s_tot[tid] : 0;
+  const int inc = wave_incl_scan(tv, lane);
   if (lane == 63) s_wsum[wave] = inc;
   __syncthreads();
   int wbase = 0;
   for (int w = 0; w < wave; ++w) wbase += s_wsum[w];
-  const int excl = wbase + inc - total;
   if (tid < E) {
-    counts[tid] = total;
-    offs[tid] = excl + total;
-    for (int c = 0; c < nchunks; ++c) chunk_hist[(int64_t)c * E + tid] += excl;
+    const int excl_t = wbase + inc - tv;
+    counts[tid] = tv;
+    offs[tid] = excl_t + tv;
+    s_part[tid] = excl_t;  // s_part is free again: expert t's exclusive base
+  }
+  __syncthreads();
+  if (e < E) {
+    int base = s_part[e] + pre;
+    for (int cb = c0; cb < c1; cb += RUN) {
+      int v[RUN];
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) v[i] = cb + i < c1 ? chunk_hist[(int64_t)(cb + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < RUN; ++i) {
+        if (cb + i < c1) chunk_hist[(int64_t)(cb + i) * E + e] = base;
+        base += v[i];
+      }
+    }
   }
 }
 
