@@ -11,9 +11,13 @@ Mirrors the reference operator surface:
   (pluggy/models/qwen3_moe/qwen3_moe.py:168-178) with fp32 logits and the
   "ties -> lower expert id" selection rule.
 
-Both are ``torch.autograd.Function``s. Each stage (router, permutation, row
-gather, each grouped GEMM, combine, and their backward) is one C-ABI call on
-the current stream; ``stage_timer()`` brackets the stages with HIP events.
+Each entry point is a ``torch.library`` custom op (namespace ``pmoe``) with a
+shape-only fake implementation and a registered autograd formula, so a block
+that calls them traces under ``torch.compile`` without graph breaks, as the
+reference's per-block ``torch.compile`` expects (pluggy/training/trainer.py:
+292-293). Each stage (router, permutation, row gather, each grouped GEMM,
+combine, and their backward) is one C-ABI call on the current stream;
+``stage_timer()`` brackets the stages with HIP events.
 """
 
 from __future__ import annotations
@@ -89,30 +93,69 @@ def _stage(name: str):
 # ------------------------------------------------------------------ router
 
 
-class _RouterFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, weight, top_k, norm_topk_prob, logit_bias):
-        with _stage("router_fwd"):
-            logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-                x, weight, top_k, norm_topk_prob, logit_bias)
-        ctx.save_for_backward(x, weight, logits, top_i, top_w32)
-        ctx.norm_topk_prob = bool(norm_topk_prob)
-        ctx.mark_non_differentiable(top_i, top_w32, counts, psum, lse2)
-        ctx.set_materialize_grads(False)  # absent gradients stay None (no zero-filled tensors)
-        return logits, top_w, top_i, top_w32, counts, psum, lse2
+def _none_if_empty(t: torch.Tensor) -> torch.Tensor | None:
+    """Custom ops cannot return None: an absent gradient travels as an empty tensor."""
+    return None if t.numel() == 0 else t
 
-    @staticmethod
-    def backward(ctx, g_logits, g_w, _gi, _gw32, _gc, _gp, _gl):
-        x, weight, logits, top_i, top_w32 = ctx.saved_tensors
-        if not (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]) or (g_logits is None and g_w is None):
-            return None, None, None, None, None
-        if g_logits is not None:
-            g_logits = g_logits.float().contiguous()
-        if g_w is not None:
-            g_w = g_w.contiguous()
-        with _stage("router_bwd"):
-            gx, gW = ops.router_backward(x, weight, logits, top_i, top_w32, g_w, g_logits, ctx.norm_topk_prob)
-        return (gx if ctx.needs_input_grad[0] else None), (gW if ctx.needs_input_grad[1] else None), None, None, None
+
+def _empty_like_none(ref: torch.Tensor) -> torch.Tensor:
+    """The empty stand-in for an absent output (same dtype and device as ref)."""
+    return ref.new_empty(0)
+
+
+@torch.library.custom_op("pmoe::router_fwd", mutates_args=(),
+                         schema="(Tensor x, Tensor weight, int top_k, bool norm_topk_prob, Tensor? logit_bias) -> "
+                                "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _router_fwd(x, weight, top_k, norm_topk_prob, logit_bias):
+    with _stage("router_fwd"):
+        return ops.router_forward(x, weight, top_k, norm_topk_prob, logit_bias)
+
+
+@_router_fwd.register_fake
+def _(x, weight, top_k, norm_topk_prob, logit_bias):
+    T, E, K = x.shape[0], weight.shape[0], top_k
+    f32 = torch.float32
+    return (x.new_empty(T, E, dtype=f32), x.new_empty(T, K), x.new_empty(T, K, dtype=torch.int64),
+            x.new_empty(T, K, dtype=f32), x.new_empty(E, dtype=torch.int32), x.new_empty(E, dtype=f32),
+            x.new_empty(1, dtype=f32))
+
+
+@torch.library.custom_op("pmoe::router_bwd", mutates_args=(),
+                         schema="(Tensor x, Tensor weight, Tensor logits, Tensor top_i, Tensor top_w32, "
+                                "Tensor? grad_top_w, Tensor? grad_logits, bool norm_topk_prob) -> (Tensor, Tensor)")
+def _router_bwd(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob):
+    with _stage("router_bwd"):
+        return ops.router_backward(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob)
+
+
+@_router_bwd.register_fake
+def _(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob):
+    return torch.empty_like(x), torch.empty_like(weight)
+
+
+def _router_setup(ctx, inputs, output):
+    x, weight, top_k, norm_topk_prob, logit_bias = inputs
+    logits, top_w, top_i, top_w32, counts, psum, lse2 = output
+    ctx.save_for_backward(x, weight, logits, top_i, top_w32)
+    ctx.norm_topk_prob = bool(norm_topk_prob)
+    ctx.mark_non_differentiable(top_i, top_w32, counts, psum, lse2)
+    ctx.set_materialize_grads(False)  # absent gradients stay None (no zero-filled tensors)
+
+
+def _router_backward(ctx, g_logits, g_w, _gi, _gw32, _gc, _gp, _gl):
+    x, weight, logits, top_i, top_w32 = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    if not (need[0] or need[1]) or (g_logits is None and g_w is None):
+        return None, None, None, None, None
+    if g_logits is not None:
+        g_logits = g_logits.float().contiguous()
+    if g_w is not None:
+        g_w = g_w.contiguous()
+    gx, gW = torch.ops.pmoe.router_bwd(x, weight, logits, top_i, top_w32, g_w, g_logits, ctx.norm_topk_prob)
+    return (gx if need[0] else None), (gW if need[1] else None), None, None, None
+
+
+_router_fwd.register_autograd(_router_backward, setup_context=_router_setup)
 
 
 def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
@@ -134,7 +177,7 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
         w = w.float()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
-    logits, top_w, top_i, _w32, counts, psum, lse2 = _RouterFunction.apply(
+    logits, top_w, top_i, _w32, counts, psum, lse2 = torch.ops.pmoe.router_fwd(
         x, w, int(top_k), bool(norm_topk_prob), logit_bias)
     if return_stats:
         return logits, top_w, top_i, RouterStats(counts, psum, lse2, x.shape[0])
@@ -144,141 +187,205 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
 # -------------------------------------------------------------- expert FFN
 
 
-class _ExpertFFNFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, hidden, top_indices, top_weights, gate_up_proj, down_proj):
-        E = gate_up_proj.shape[0]
-        K = top_indices.shape[1]
-        with _stage("permute"):
-            counts, offs, sorted_pair, inv_pos = ops.permute(top_indices, E)
-        with _stage("dispatch"):
-            x_perm = ops.dispatch(hidden, inv_pos, K)
-        with _stage("gate_up_fwd"):
-            gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
-        with _stage("down_fwd"):
-            y = ops.down_proj(mid, down_proj, offs)
-        with _stage("combine"):
-            out = ops.combine(y, top_weights, inv_pos)
-        ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
-        ctx.dims = (hidden.shape[0], K, E)
-        ctx.set_materialize_grads(False)
-        return out
+def _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+    """-> out and what the backward reads: offs, inv_pos, x_perm, gu, mid, y."""
+    E = gate_up_proj.shape[0]
+    K = top_indices.shape[1]
+    with _stage("permute"):
+        _, offs, _, inv_pos = ops.permute(top_indices, E)
+    with _stage("dispatch"):
+        x_perm = ops.dispatch(hidden, inv_pos, K)
+    with _stage("gate_up_fwd"):
+        gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
+    with _stage("down_fwd"):
+        y = ops.down_proj(mid, down_proj, offs)
+    with _stage("combine"):
+        out = ops.combine(y, top_weights, inv_pos)
+    return out, offs, inv_pos, x_perm, gu, mid, y
 
-    @staticmethod
-    def backward(ctx, grad_out):
-        if grad_out is None:
-            return None, None, None, None, None
-        top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
-        T, K, E = ctx.dims
-        need = ctx.needs_input_grad
-        grad_out = grad_out.contiguous()
-        if grad_out.dtype != x_perm.dtype:
-            grad_out = grad_out.to(x_perm.dtype)
-        with _stage("combine_bwd"):
-            g_y, g_w = ops.combine_backward(grad_out, y, top_w, inv_pos)
-        g_hidden = g_gu_w = g_dn_w = None
-        g_gu = None
-        if need[0] or need[3]:
-            with _stage("down_dgrad"):
-                g_gu = ops.down_proj_dgrad(g_y, gu, down, offs)
-        if need[4]:
-            with _stage("down_wgrad"):
-                g_dn_w = ops.down_proj_wgrad(g_y, mid, offs, E)
-        del g_y
-        if need[0]:
-            with _stage("gate_up_dgrad"):
-                g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
-            with _stage("dispatch_bwd"):
-                g_hidden = ops.dispatch_backward(g_xp, inv_pos, T, K)
-            del g_xp
-        if need[3]:
-            with _stage("gate_up_wgrad"):
-                g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
-        return g_hidden, None, (g_w if need[2] else None), g_gu_w, g_dn_w
+
+def _ffn_fake_saved(hidden, K, E, I):
+    T, H = hidden.shape
+    P = T * K
+    i32 = torch.int32
+    return (hidden.new_empty(E, dtype=i32), hidden.new_empty(P, dtype=i32), hidden.new_empty(P, H),
+            hidden.new_empty(P, 2 * I), hidden.new_empty(P, I), hidden.new_empty(P, H))
+
+
+@torch.library.custom_op("pmoe::expert_ffn_fwd", mutates_args=(),
+                         schema="(Tensor hidden, Tensor top_indices, Tensor top_weights, Tensor gate_up_proj, "
+                                "Tensor down_proj) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _expert_ffn_fwd(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+    return _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj)
+
+
+@_expert_ffn_fwd.register_fake
+def _(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+    E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
+    return (torch.empty_like(hidden),) + _ffn_fake_saved(hidden, top_indices.shape[1], E, I2 // 2)
+
+
+@torch.library.custom_op("pmoe::combine_bwd", mutates_args=(),
+                         schema="(Tensor grad_out, Tensor y, Tensor top_weights, Tensor inv_pos) -> (Tensor, Tensor)")
+def _combine_bwd(grad_out, y, top_weights, inv_pos):
+    """-> grad_y (P,H) = w * grad_out gathered, grad_top_weights (T,K)."""
+    with _stage("combine_bwd"):
+        return ops.combine_backward(grad_out, y, top_weights, inv_pos)
+
+
+@_combine_bwd.register_fake
+def _(grad_out, y, top_weights, inv_pos):
+    return torch.empty_like(y), torch.empty_like(top_weights)
+
+
+@torch.library.custom_op("pmoe::expert_bwd", mutates_args=(),
+                         schema="(Tensor grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
+                                "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_hidden_add, int tokens, int top_k, "
+                                "bool[] needs) -> (Tensor, Tensor, Tensor)")
+def _expert_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs):
+    """The expert GEMMs' backward from grad_y: -> grad_hidden (+ grad_hidden_add),
+    grad_gate_up, grad_down; an empty tensor where needs[i] is false (needs:
+    hidden, gate_up, down)."""
+    E = gate_up.shape[0]
+    g_hidden = g_gu_w = g_dn_w = None
+    g_gu = None
+    if needs[0] or needs[1]:
+        with _stage("down_dgrad"):
+            g_gu = ops.down_proj_dgrad(grad_y, gu, down, offs)
+    if needs[2]:
+        with _stage("down_wgrad"):
+            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E)
+    if needs[0]:
+        with _stage("gate_up_dgrad"):
+            g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
+        with _stage("dispatch_bwd"):
+            g_hidden = ops.dispatch_backward(g_xp, inv_pos, tokens, top_k, add=grad_hidden_add)
+        del g_xp
+    if needs[1]:
+        with _stage("gate_up_wgrad"):
+            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+    e = _empty_like_none
+    return (g_hidden if g_hidden is not None else e(grad_y), g_gu_w if g_gu_w is not None else e(gate_up),
+            g_dn_w if g_dn_w is not None else e(down))
+
+
+@_expert_bwd.register_fake
+def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs):
+    e = _empty_like_none
+    return (grad_y.new_empty(tokens, grad_y.shape[1]) if needs[0] else e(grad_y),
+            torch.empty_like(gate_up) if needs[1] else e(gate_up), torch.empty_like(down) if needs[2] else e(down))
+
+
+def _ffn_setup(ctx, inputs, output):
+    hidden, top_indices, top_weights, gate_up_proj, down_proj = inputs
+    out, offs, inv_pos, x_perm, gu, mid, y = output
+    ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
+    ctx.dims = (hidden.shape[0], top_indices.shape[1])
+    ctx.mark_non_differentiable(offs, inv_pos, x_perm, gu, mid, y)
+    ctx.set_materialize_grads(False)
+
+
+def _ffn_backward(ctx, grad_out, *_saved_grads):
+    if grad_out is None:
+        return None, None, None, None, None
+    top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
+    T, K = ctx.dims
+    need = ctx.needs_input_grad
+    grad_out = grad_out.contiguous()
+    if grad_out.dtype != x_perm.dtype:
+        grad_out = grad_out.to(x_perm.dtype)
+    g_y, g_w = torch.ops.pmoe.combine_bwd(grad_out, y, top_w, inv_pos)
+    g_hidden = g_gu_w = g_dn_w = None
+    if need[0] or need[3] or need[4]:
+        g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid,
+                                                             None, T, K,
+                                                             [bool(need[0]), bool(need[3]), bool(need[4])])
+    return (_none_if_empty(g_hidden) if g_hidden is not None else None, None, (g_w if need[2] else None),
+            _none_if_empty(g_gu_w) if g_gu_w is not None else None,
+            _none_if_empty(g_dn_w) if g_dn_w is not None else None)
+
+
+_expert_ffn_fwd.register_autograd(_ffn_backward, setup_context=_ffn_setup)
 
 
 # ------------------------------------------------- whole sparse MLP block
 
 
-class _SparseMoEFunction(torch.autograd.Function):
-    """Router + dropless experts as one autograd node (Qwen3MoeSparseMLP.forward).
+@torch.library.custom_op("pmoe::sparse_moe_fwd", mutates_args=(),
+                         schema="(Tensor x, Tensor router_weight, Tensor gate_up_proj, Tensor down_proj, int top_k, "
+                                "bool norm_topk_prob, Tensor? logit_bias) -> (Tensor, Tensor, Tensor, Tensor, Tensor, "
+                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+    """Router + dropless experts (Qwen3MoeSparseMLP.forward) as one op.
 
-    Outputs ``(out, router_logits)``: the logits stay graph-connected for the
-    aux losses. In the backward the router's share of the input gradient is
-    computed first and folded into the dispatch-backward sum, so the two input
-    gradients are never added by a separate pass.
+    -> out, router_logits, counts, prob_sum, lse_sq_sum, then what the backward
+    reads: top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y.
     """
+    with _stage("router_fwd"):
+        logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
+            x, router_weight, top_k, norm_topk_prob, logit_bias)
+    out, offs, inv_pos, x_perm, gu, mid, y = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
+    return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y
 
-    @staticmethod
-    def forward(ctx, x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
-        E = gate_up_proj.shape[0]
-        K = int(top_k)
-        with _stage("router_fwd"):
-            logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-                x, router_weight, K, norm_topk_prob, logit_bias)
-        with _stage("permute"):
-            _, offs, _, inv_pos = ops.permute(top_i, E)
-        with _stage("dispatch"):
-            x_perm = ops.dispatch(x, inv_pos, K)
-        with _stage("gate_up_fwd"):
-            gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
-        with _stage("down_fwd"):
-            y = ops.down_proj(mid, down_proj, offs)
-        with _stage("combine"):
-            out = ops.combine(y, top_w, inv_pos)
-        ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, top_w, gate_up_proj, down_proj, offs, inv_pos,
-                              x_perm, gu, mid, y)
-        ctx.norm_topk_prob = bool(norm_topk_prob)
-        ctx.dims = (x.shape[0], K, E)
-        ctx.mark_non_differentiable(counts, psum, lse2)
-        ctx.set_materialize_grads(False)
-        return out, logits, counts, psum, lse2
 
-    @staticmethod
-    def backward(ctx, g_out, g_logits, _gc, _gp, _gl):
-        (x, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
-         y) = ctx.saved_tensors
-        T, K, E = ctx.dims
-        need = ctx.needs_input_grad
-        if g_out is None and g_logits is None:
-            return None, None, None, None, None, None, None
-        if g_logits is not None:
-            g_logits = g_logits.float().contiguous()
-        g_x = g_rw = g_gu_w = g_dn_w = None
-        g_tw = None
-        g_y = None
-        if g_out is not None:
-            g_out = g_out.contiguous()
-            if g_out.dtype != x_perm.dtype:
-                g_out = g_out.to(x_perm.dtype)
-            with _stage("combine_bwd"):
-                g_y, g_tw = ops.combine_backward(g_out, y, top_w, inv_pos)
-        gx_router = None
-        if need[0] or need[1]:
-            with _stage("router_bwd"):
-                gx_router, g_rw = ops.router_backward(x, rw, logits, top_i, top_w32, g_tw, g_logits,
-                                                      ctx.norm_topk_prob)
-        if g_y is not None:
-            g_gu = None
-            if need[0] or need[2]:
-                with _stage("down_dgrad"):
-                    g_gu = ops.down_proj_dgrad(g_y, gu, down, offs)
-            if need[3]:
-                with _stage("down_wgrad"):
-                    g_dn_w = ops.down_proj_wgrad(g_y, mid, offs, E)
-            del g_y
-            if need[0]:
-                with _stage("gate_up_dgrad"):
-                    g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
-                with _stage("dispatch_bwd"):
-                    g_x = ops.dispatch_backward(g_xp, inv_pos, T, K, add=gx_router)
-                del g_xp
-            if need[2]:
-                with _stage("gate_up_wgrad"):
-                    g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
-        elif need[0]:
-            g_x = gx_router
-        return (g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w, g_dn_w, None, None, None
+@_sparse_moe_fwd.register_fake
+def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+    T, E, K = x.shape[0], router_weight.shape[0], top_k
+    I = gate_up_proj.shape[1] // 2
+    f32 = torch.float32
+    return ((torch.empty_like(x), x.new_empty(T, E, dtype=f32), x.new_empty(E, dtype=torch.int32),
+             x.new_empty(E, dtype=f32), x.new_empty(1, dtype=f32), x.new_empty(T, K, dtype=torch.int64),
+             x.new_empty(T, K, dtype=f32), x.new_empty(T, K))
+            + _ffn_fake_saved(x, K, E, I))
+
+
+def _sparse_setup(ctx, inputs, output):
+    x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias = inputs
+    (out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y) = output
+    ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, top_w, gate_up_proj, down_proj, offs, inv_pos,
+                          x_perm, gu, mid, y)
+    ctx.norm_topk_prob = bool(norm_topk_prob)
+    ctx.dims = (x.shape[0], int(top_k))
+    ctx.mark_non_differentiable(counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y)
+    ctx.set_materialize_grads(False)
+
+
+def _sparse_backward(ctx, g_out, g_logits, *_rest):
+    """The router's share of the input gradient is computed first and added
+    inside the dispatch backward, so the two input gradients are never summed
+    by a separate pass."""
+    (x, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
+     y) = ctx.saved_tensors
+    T, K = ctx.dims
+    need = ctx.needs_input_grad
+    if g_out is None and g_logits is None:
+        return None, None, None, None, None, None, None
+    if g_logits is not None:
+        g_logits = g_logits.float().contiguous()
+    g_x = g_rw = g_gu_w = g_dn_w = None
+    g_y = g_tw = None
+    if g_out is not None:
+        g_out = g_out.contiguous()
+        if g_out.dtype != x_perm.dtype:
+            g_out = g_out.to(x_perm.dtype)
+        g_y, g_tw = torch.ops.pmoe.combine_bwd(g_out, y, top_w, inv_pos)
+    gx_router = None
+    if need[0] or need[1]:
+        gx_router, g_rw = torch.ops.pmoe.router_bwd(x, rw, logits, top_i, top_w32, g_tw, g_logits,
+                                                    ctx.norm_topk_prob)
+    if g_y is not None and (need[0] or need[2] or need[3]):
+        g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
+            g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if need[0] else None, T, K,
+            [bool(need[0]), bool(need[2]), bool(need[3])])
+        g_x = _none_if_empty(g_hidden)
+        g_gu_w = _none_if_empty(g_gu_w)
+        g_dn_w = _none_if_empty(g_dn_w)
+    elif need[0]:
+        g_x = gx_router
+    return (g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w, g_dn_w, None, None, None
+
+
+_sparse_moe_fwd.register_autograd(_sparse_backward, setup_context=_sparse_setup)
 
 
 def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_proj: torch.Tensor,
@@ -303,8 +410,8 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     dn = down_proj.to(dtype=dt).contiguous()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
-    out, logits, counts, psum, lse2 = _SparseMoEFunction.apply(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
-                                                                logit_bias)
+    out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
+                                                                     logit_bias)[:5]
     return out, logits, RouterStats(counts, psum, lse2, x.shape[0])
 
 
@@ -334,5 +441,5 @@ def moe_expert_ffn(
     gu = gate_up_proj.to(dtype=dt).contiguous()
     dn = down_proj.to(dtype=dt).contiguous()
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
-    return _ExpertFFNFunction.apply(hidden.contiguous(), top_indices.to(torch.int64).contiguous(), tw.contiguous(),
-                                    gu, dn)
+    return torch.ops.pmoe.expert_ffn_fwd(hidden.contiguous(), top_indices.to(torch.int64).contiguous(),
+                                         tw.contiguous(), gu, dn)[0]

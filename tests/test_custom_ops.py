@@ -1,0 +1,70 @@
+"""Shape-only (fake) implementations of the pmoe custom ops, on the CPU.
+
+These are what ``torch.compile`` and FakeTensor tracing see in place of the
+HIP kernels; the GPU tests compare them with the real outputs
+(``tests/test_gpu_compile.py``).
+"""
+
+import pytest
+import torch
+
+pytestmark = []
+
+T, H, E, K, I = 64, 32, 8, 2, 16
+P = T * K
+
+
+def _meta(*shape, dtype=torch.bfloat16):
+    return torch.empty(*shape, dtype=dtype, device="meta")
+
+
+def _sig(ts):
+    return [(tuple(t.shape), t.dtype) for t in ts]
+
+
+@pytest.fixture(scope="module")
+def pmoe_ops():
+    import pluggy_amd  # noqa: F401  (registers the ops)
+    return torch.ops.pmoe
+
+
+def test_router_fwd_fake(pmoe_ops):
+    out = pmoe_ops.router_fwd(_meta(T, H), _meta(E, H, dtype=torch.float32), K, True, None)
+    f32, bf = torch.float32, torch.bfloat16
+    assert _sig(out) == [((T, E), f32), ((T, K), bf), ((T, K), torch.int64), ((T, K), f32), ((E,), torch.int32),
+                         ((E,), f32), ((1,), f32)]
+
+
+def test_router_bwd_fake(pmoe_ops):
+    x, w = _meta(T, H), _meta(E, H, dtype=torch.float32)
+    gx, gw = pmoe_ops.router_bwd(x, w, _meta(T, E, dtype=torch.float32), _meta(T, K, dtype=torch.int64),
+                                 _meta(T, K, dtype=torch.float32), _meta(T, K), None, True)
+    assert _sig([gx, gw]) == [((T, H), torch.bfloat16), ((E, H), torch.float32)]
+
+
+def test_expert_ffn_fwd_fake(pmoe_ops):
+    out = pmoe_ops.expert_ffn_fwd(_meta(T, H), _meta(T, K, dtype=torch.int64), _meta(T, K), _meta(E, 2 * I, H),
+                                  _meta(E, H, I))
+    bf, i32 = torch.bfloat16, torch.int32
+    assert _sig(out) == [((T, H), bf), ((E,), i32), ((P,), i32), ((P, H), bf), ((P, 2 * I), bf), ((P, I), bf),
+                         ((P, H), bf)]
+
+
+def test_sparse_moe_fwd_fake(pmoe_ops):
+    out = pmoe_ops.sparse_moe_fwd(_meta(T, H), _meta(E, H, dtype=torch.float32), _meta(E, 2 * I, H), _meta(E, H, I),
+                                  K, False, None)
+    bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
+    assert _sig(out) == [((T, H), bf), ((T, E), f32), ((E,), i32), ((E,), f32), ((1,), f32), ((T, K), torch.int64),
+                         ((T, K), f32), ((T, K), bf), ((E,), i32), ((P,), i32), ((P, H), bf), ((P, 2 * I), bf),
+                         ((P, I), bf), ((P, H), bf)]
+
+
+def test_backward_fakes_drop_unneeded_grads(pmoe_ops):
+    gy, gu, dn = _meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I)
+    i32 = torch.int32
+    args = (gy, gu, dn, _meta(E, dtype=i32), _meta(P, dtype=i32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), None, T, K)
+    gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [True, False, True])
+    assert _sig([gh, gdn]) == [((T, H), torch.bfloat16), ((E, H, I), torch.bfloat16)]
+    assert ggu.numel() == 0  # absent gradient: empty stand-in
+    g_y, g_w = pmoe_ops.combine_bwd(_meta(T, H), _meta(P, H), _meta(T, K), _meta(P, dtype=i32))
+    assert _sig([g_y, g_w]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]

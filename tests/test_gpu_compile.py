@@ -1,0 +1,94 @@
+"""The pmoe custom ops under torch.library's checks and torch.compile.
+
+The reference compiles every transformer block (pluggy/training/trainer.py:
+292-293), so the drop-in must trace without graph breaks: the MoE half of a
+block (RMSNorm -> sparse MLP -> residual add, qwen3_moe.py:281) is compiled
+with ``fullgraph=True`` and must give the eager results bit for bit (the same
+kernels run), including the gradient of an aux loss through the router logits.
+"""
+
+import pytest
+import torch
+from torch import nn
+
+from _gpu_helpers import DEV, gen, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _pa():
+    import pluggy_amd
+    return pluggy_amd
+
+
+def _weights(E, H, I, seed=0):
+    g = gen(seed)
+    rw = (torch.randn(E, H, generator=g) * 0.02).to(DEV)
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    dn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    return rw, gu, dn
+
+
+def test_opcheck_custom_ops():
+    _pa()
+    T, H, E, K, I = 96, 128, 8, 2, 64
+    rw, gu, dn = _weights(E, H, I)
+    x = torch.randn(T, H, generator=gen(1)).to(torch.bfloat16).to(DEV)
+    say(f"opcheck T={T} H={H} E={E} K={K} I={I}")
+    tests = ("test_schema", "test_autograd_registration", "test_faketensor")
+    torch.library.opcheck(torch.ops.pmoe.router_fwd, (x, rw, K, True, None), test_utils=tests)
+    torch.library.opcheck(torch.ops.pmoe.sparse_moe_fwd, (x.requires_grad_(True), rw.requires_grad_(True),
+                                                          gu.requires_grad_(True), dn.requires_grad_(True), K, True,
+                                                          None), test_utils=tests)
+    logits, tw, ti = _pa().router_topk(x.detach(), rw.detach(), K)
+    torch.library.opcheck(torch.ops.pmoe.expert_ffn_fwd, (x.detach(), ti, tw, gu.detach(), dn.detach()),
+                          test_utils=tests)
+
+
+class _MoEHalfBlock(nn.Module):
+    """x + SparseMLP(RMSNorm(x)): the MoE half of Qwen3MoeTransformerBlock (qwen3_moe.py:281)."""
+
+    def __init__(self, H, I, E, K):
+        super().__init__()
+        self.norm = nn.RMSNorm(H, eps=1e-6)
+        self.ffn = _pa().Qwen3MoeSparseMLP(H, I, E, K)
+
+    def forward(self, x):
+        y = x + self.ffn(self.norm(x))
+        z = torch.logsumexp(self.ffn.last_router_logits, dim=-1).pow(2).mean()  # router z-loss (qwen3_moe.py:311-316)
+        return y, z
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_compiled_block_matches_eager(dtype):
+    B, S, H, E, K, I = 2, 128, 256, 16, 4, 128
+    say(f"compile B={B} S={S} H={H} E={E} K={K} I={I} {dtype}")
+    torch.manual_seed(0)
+    block = _MoEHalfBlock(H, I, E, K).to(DEV)
+    rw, gu, dn = _weights(E, H, I, seed=3)
+    with torch.no_grad():
+        block.ffn.router.weight.copy_(rw)
+        block.ffn.experts.gate_up_proj.copy_(gu.float())
+        block.ffn.experts.down_proj.copy_(dn.float())
+    block = block.to(dtype)
+    block.ffn.router.weight.data = block.ffn.router.weight.data.float()  # fp32 router, as BASELINE config 2
+    x0 = torch.randn(B, S, H, generator=gen(5)).to(dtype).to(DEV)
+
+    def run(mod):
+        for prm in block.parameters():
+            prm.grad = None
+        x = x0.clone().requires_grad_(True)
+        y, z = mod(x)
+        (y.float().pow(2).mean() + 1e-3 * z).backward()
+        return [y.detach(), z.detach(), x.grad] + [prm.grad.clone() for prm in block.parameters()]
+
+    eager = run(block)
+    torch._dynamo.reset()
+    compiled = torch.compile(block, backend="aot_eager", fullgraph=True)
+    got = run(compiled)
+    got2 = run(compiled)  # a second call reuses the compiled graph
+    names = ["y", "z", "dx"] + [n for n, _ in block.named_parameters()]
+    for n, a, b, c in zip(names, eager, got, got2):
+        say(f"  {n}: max|compiled - eager| = {(a.float() - b.float()).abs().max().item():.3e}")
+        assert torch.equal(a, b), n
+        assert torch.equal(b, c), n
