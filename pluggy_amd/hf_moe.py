@@ -39,7 +39,7 @@ _MOE_ANY = re.compile(r"model\.layers\.(\d+)\.mlp\.(gate\.|experts\.|shared_expe
 def weight_files(directory: str | Path) -> list[Path]:
     """safetensors files of a local checkpoint directory (single file or index-sharded).
 
-    Same resolution as pluggy/models/hf_import.py:101-131 for a local directory;
+    Same resolution as pluggy/models/hf_import.py:102-132 for a local directory;
     hub ids are not fetched (no network here).
     """
     d = Path(directory)
@@ -146,7 +146,7 @@ def load_hf_moe_weights(model: torch.nn.Module, directory: str | Path,
     """Copy the MoE layers of a local HF Qwen3-MoE checkpoint into ``model`` in place.
 
     Parameters keep their device and dtype (bf16 hub weights land in fp32
-    masters, as pluggy/models/hf_import.py:134-139). Returns ``(number of packed
+    masters, as pluggy/models/hf_import.py:135-171). Returns ``(number of packed
     tensors loaded, the remaining non-MoE tensors)`` — the latter go through the
     reference's dense mapping.
     """
