@@ -9,8 +9,10 @@ backward (upstream grad N(0,1)), inputs resident in HBM.
 
 Prints one JSON line: tokens/s (whole job), expert-GEMM TFLOP/s and its
 fraction of the bf16 dense MFMA peak, per-stage HIP-event timings, the
-roofline of the dominant kernel, HBM GB/s of the row-movement kernels, and a
-CPU baseline (the restated reference CPU path) timed on this host.
+roofline of the dominant kernel, HBM GB/s of the row-movement kernels, the
+reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
+inputs, and a CPU baseline (the restated reference CPU path) timed on this
+host.
 
 Two timed regions of --steps steps each: the first, bracketed by two events,
 gives ms_per_step and tokens/s; the second records an event pair around each
@@ -39,6 +41,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, help="workload id (BASELINE.json configs, 1-based)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-gpu", action="store_true",
+                    help="skip timing the reference's own torch path (F.grouped_mm) on this GPU")
     ap.add_argument("--cpu-tokens", type=int, default=512,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
     ap.add_argument("--copy-mib", type=int, default=256,
@@ -91,6 +95,70 @@ def cpu_baseline(cfg, tokens: int | None):
         "os_cpu_count": os.cpu_count(),
         "torch": torch.__version__,
     }
+
+
+def reference_gpu(cfg, inp, steps: int, warmup: int, dev):
+    """The reference's own GPU path, timed on this GPU on the same inputs.
+
+    ``Qwen3MoeSparseMLP.forward`` as the trainer runs it, under
+    ``torch.autocast(cuda, bf16)`` (trainer.py:469): router ``F.linear`` (bf16
+    logits), fp32 softmax, ``torch.topk``, renormalise, cast (qwen3_moe.py:
+    168-178); experts by the sorted/grouped path (moe.py:68-124: stable
+    argsort, bincount + cumsum offsets, two ``F.grouped_mm``, SwiGLU, weighted
+    ``index_add_``); torch autograd for the backward. Restated with torch ops
+    for this comparison only; the product never runs it.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    T, H, E, K = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k
+    x, gout, bias = inp["x"], inp.get("grad_out"), inp.get("logit_bias")
+    params = [inp[n].detach().clone().requires_grad_(cfg.backward)
+              for n in ("router_weight", "gate_up_proj", "down_proj")]
+    token_idx = torch.arange(T, device=dev).unsqueeze(1).expand(T, K).reshape(-1)
+
+    def step():
+        for p in params:
+            p.grad = None
+        wr, gu, dn = params
+        xg = x.detach().requires_grad_(cfg.backward)
+        dt = xg.dtype
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = F.linear(xg, wr)
+            if bias is not None:
+                logits = logits + bias
+            probs = F.softmax(logits, dim=-1, dtype=torch.float32)
+            top_w, top_i = torch.topk(probs, K, dim=-1)
+            if cfg.norm_topk_prob:
+                top_w = top_w / top_w.sum(dim=-1, keepdim=True)
+            top_w = top_w.to(dt)
+            expert_idx = top_i.reshape(-1)
+            order = torch.argsort(expert_idx, stable=True)
+            sorted_token = token_idx[order]
+            sorted_w = top_w.reshape(-1)[order]
+            offs = torch.cumsum(torch.bincount(expert_idx[order], minlength=E), dim=0).to(torch.int32)
+            gate_up = F.grouped_mm(xg[sorted_token], gu.to(dt).transpose(-2, -1), offs=offs)
+            gate, up = gate_up.chunk(2, dim=-1)
+            y = F.grouped_mm(F.silu(gate) * up, dn.to(dt).transpose(-2, -1), offs=offs)
+            y = y * sorted_w.unsqueeze(1).to(dt)
+            out = torch.zeros(T, H, device=dev, dtype=dt).index_add_(0, sorted_token, y)
+        if cfg.backward:
+            out.backward(gout)
+
+    for _ in range(warmup):
+        step()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return {"value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4), "steps": steps,
+            "path": "reference Qwen3MoeSparseMLP under bf16 autocast: F.linear router + torch.topk, "
+                    "F.grouped_mm experts (moe.py:68-124), torch autograd backward; same inputs"}
 
 
 def copy_bandwidth(mib: int, dev, reps: int = 5):
@@ -257,6 +325,10 @@ def main() -> int:
     }
     if args.copy_mib > 0:
         result["copy_reference"] = copy_bandwidth(args.copy_mib, dev)
+    if not args.no_reference_gpu:
+        ref = reference_gpu(cfg, inp, min(args.steps, 10), 2, dev)
+        ref["speedup"] = round(result["value"] / ref["value"], 2)
+        result["reference_gpu"] = ref
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(result), flush=True)

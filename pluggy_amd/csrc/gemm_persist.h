@@ -9,11 +9,11 @@
 // and scanned once; a tile's group is then a binary search in LDS.
 //
 // The k loop is the ring pipeline of grouped_gemm_dma_kernel with a global
-// stage counter, so ring slots carry over from one tile to the next: the
-// first NS-1 stages of a tile are issued right after the previous tile's
-// epilogue (the ring is idle then), and stage kt+NS-1 is issued during stage
-// kt. The epilogue stages accumulators through a separate per-wave LDS region
-// of 8-row slabs and never touches the ring.
+// stage counter, so ring slots carry over from one tile to the next: stage
+// kt+NS-1 is issued during stage kt, and in a tile's last NS-1 stages that is
+// one of the next tile's first stages, so the next tile's data lands while
+// this tile finishes and stores. The epilogue stages accumulators through a
+// separate per-wave LDS region of 16-row slabs and never touches the ring.
 #pragma once
 
 #include "gemm_dma.h"

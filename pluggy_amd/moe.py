@@ -90,6 +90,32 @@ def _stage(name: str):
     return _timer.mark(name) if _timer is not None else contextlib.nullcontext()
 
 
+# ---------------------------------------------------------------- autocast
+
+
+def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
+    """The operand dtype CUDA autocast asks for (bf16), or None when it is off.
+
+    The reference trainer runs the model under ``torch.autocast(cuda, bf16)``
+    with fp32 parameters (pluggy/training/trainer.py:469). There the router's
+    linear runs in bf16 (qwen3_moe.py:172), and the expert weights are cast to
+    the activation dtype with the stated intent "bf16 under autocast"
+    (moe.py:110-112). The drop-in therefore hands the kernels bf16 operands
+    whenever autocast is on, whatever the residual stream's dtype, and returns
+    its outputs in the input's dtype as the reference does. (torch's
+    ``F.grouped_mm`` is not on autocast's bf16 list, so with an fp32 residual
+    stream the reference's expert GEMMs actually run in fp32; this build keeps
+    the stated bf16 intent.) The kernels compute in bf16 or fp32 only, so an
+    fp16 autocast region is rejected.
+    """
+    if t.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        if dt != torch.bfloat16:
+            raise NotImplementedError(f"pluggy_amd computes in bf16 or fp32; autocast asks for {dt}")
+        return dt
+    return None
+
+
 # ------------------------------------------------------------------ router
 
 
@@ -165,20 +191,23 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     Returns ``(router_logits (T,E) fp32, top_weights (T,K) hidden.dtype,
     top_indices (T,K) int64)`` and, with ``return_stats``, a ``RouterStats``.
     Gradients flow to ``hidden`` and ``weight`` through both the logits (for
-    aux losses) and the top weights.
+    aux losses) and the top weights. Under CUDA autocast both operands are
+    taken in bf16, as the reference's ``F.linear`` takes them there.
     """
     assert hidden.dim() == 2, "router expects (T, H) hidden states"
     assert weight.dim() == 2 and weight.shape[1] == hidden.shape[1]
     assert 1 <= top_k <= weight.shape[0]
     require_gpu(hidden, weight, logit_bias)
-    x = hidden.contiguous()
-    w = weight.contiguous()
+    amp = _amp_dtype(hidden)
+    x = (hidden if amp is None else hidden.to(amp)).contiguous()
+    w = (weight if amp is None else weight.to(amp)).contiguous()
     if w.dtype not in (torch.float32, torch.bfloat16):
         w = w.float()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     logits, top_w, top_i, _w32, counts, psum, lse2 = torch.ops.pmoe.router_fwd(
         x, w, int(top_k), bool(norm_topk_prob), logit_bias)
+    top_w = top_w.to(hidden.dtype)  # the reference returns them in x.dtype (qwen3_moe.py:177)
     if return_stats:
         return logits, top_w, top_i, RouterStats(counts, psum, lse2, x.shape[0])
     return logits, top_w, top_i
@@ -395,15 +424,17 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
 
     ``hidden`` (T, H). Returns ``(out (T,H), router_logits (T,E) fp32,
     RouterStats)``; the logits carry the gradient of any aux loss. Same
-    arithmetic as ``router_topk`` followed by ``moe_expert_ffn``.
+    arithmetic as ``router_topk`` followed by ``moe_expert_ffn``, including
+    their bf16 operands under CUDA autocast (``out`` keeps ``hidden.dtype``).
     """
     assert hidden.dim() == 2 and router_weight.dim() == 2 and router_weight.shape[1] == hidden.shape[1]
     assert gate_up_proj.dim() == 3 and down_proj.dim() == 3
     assert 1 <= top_k <= router_weight.shape[0]
     require_gpu(hidden, router_weight, gate_up_proj, down_proj, logit_bias)
-    dt = hidden.dtype
-    x = hidden.contiguous()
-    rw = router_weight.contiguous()
+    amp = _amp_dtype(hidden)
+    dt = hidden.dtype if amp is None else amp
+    x = hidden.to(dt).contiguous()
+    rw = (router_weight if amp is None else router_weight.to(amp)).contiguous()
     if rw.dtype not in (torch.float32, torch.bfloat16):
         rw = rw.float()
     gu = gate_up_proj.to(dtype=dt).contiguous()
@@ -412,7 +443,7 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
         logit_bias = logit_bias.float().contiguous()
     out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
                                                                      logit_bias)[:5]
-    return out, logits, RouterStats(counts, psum, lse2, x.shape[0])
+    return out.to(hidden.dtype), logits, RouterStats(counts, psum, lse2, x.shape[0])
 
 
 def moe_expert_ffn(
@@ -428,8 +459,9 @@ def moe_expert_ffn(
 
     ``out[t] = sum_k w[t,k] * down[e](silu(gate[e] x_t) * up[e] x_t)`` with
     e = top_indices[t,k]. Weights are cast to ``hidden.dtype`` first, as the
-    reference does (moe.py:110-112). The permutation, both grouped GEMMs and
-    the fp32-accumulating combine run as HIP kernels; there is no CPU path.
+    reference does (moe.py:110-112), and to bf16 under CUDA autocast, with the
+    output in ``hidden.dtype``. The permutation, both grouped GEMMs and the
+    fp32-accumulating combine run as HIP kernels; there is no CPU path.
     """
     assert hidden.dim() == 2
     assert top_indices.shape == top_weights.shape
@@ -437,9 +469,11 @@ def moe_expert_ffn(
     assert gate_up_proj.dim() == 3 and down_proj.dim() == 3
     del use_grouped_mm  # one code path: the HIP grouped kernels
     require_gpu(hidden, top_indices, top_weights, gate_up_proj, down_proj)
-    dt = hidden.dtype
+    amp = _amp_dtype(hidden)
+    dt = hidden.dtype if amp is None else amp
     gu = gate_up_proj.to(dtype=dt).contiguous()
     dn = down_proj.to(dtype=dt).contiguous()
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
-    return torch.ops.pmoe.expert_ffn_fwd(hidden.contiguous(), top_indices.to(torch.int64).contiguous(),
-                                         tw.contiguous(), gu, dn)[0]
+    out = torch.ops.pmoe.expert_ffn_fwd(hidden.to(dt).contiguous(), top_indices.to(torch.int64).contiguous(),
+                                        tw.contiguous(), gu, dn)[0]
+    return out.to(hidden.dtype)
