@@ -11,8 +11,9 @@ Prints one JSON line: tokens/s (whole job), expert-GEMM TFLOP/s and its
 fraction of the bf16 dense MFMA peak, per-stage HIP-event timings, the
 roofline of the dominant kernel, HBM GB/s of the row-movement kernels, the
 reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
-inputs, and a CPU baseline (the restated reference CPU path) timed on this
-host.
+inputs, the MoE half-block with and without the fused RMSNorm / residual add
+(``neighbours``), and a CPU baseline (the restated reference CPU path) timed
+on this host.
 
 Two timed regions of --steps steps each: the first, bracketed by two events,
 gives ms_per_step and tokens/s; the second records an event pair around each
@@ -43,6 +44,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's own torch path (F.grouped_mm) on this GPU")
+    ap.add_argument("--no-neighbours", action="store_true",
+                    help="skip timing the MoE half-block with and without the fused RMSNorm / residual add")
     ap.add_argument("--cpu-tokens", type=int, default=512,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
     ap.add_argument("--copy-mib", type=int, default=256,
@@ -159,6 +162,55 @@ def reference_gpu(cfg, inp, steps: int, warmup: int, dev):
     return {"value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4), "steps": steps,
             "path": "reference Qwen3MoeSparseMLP under bf16 autocast: F.linear router + torch.topk, "
                     "F.grouped_mm experts (moe.py:68-124), torch autograd backward; same inputs"}
+
+
+def neighbours(cfg, inp, steps: int, warmup: int, dev):
+    """The MoE half of a transformer block, ``x + SparseMLP(RMSNorm(x))``
+    (qwen3_moe.py:281), fwd+bwd as the trainer runs it: fp32 residual stream and
+    fp32 master weights under bf16 autocast (trainer.py:469). Unfused = torch's
+    RMSNorm, the drop-in MLP and torch's add; fused = ``moe_sublayer`` (norm in
+    the row kernel that feeds the router, residual add in the combine, their
+    backward in the dispatch backward)."""
+    import torch
+
+    import pluggy_amd
+
+    T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    B = cfg.batch
+    norm = torch.nn.RMSNorm(H).to(dev)
+    mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
+    with torch.no_grad():
+        mlp.router.weight.copy_(inp["router_weight"])
+        mlp.experts.gate_up_proj.copy_(inp["gate_up_proj"].float())
+        mlp.experts.down_proj.copy_(inp["down_proj"].float())
+    x = inp["x"].float().reshape(B, T // B, H)
+    gout = inp["grad_out"].float().reshape(B, T // B, H)
+    params = list(norm.parameters()) + list(mlp.parameters())
+
+    def step(fused):
+        for p in params:
+            p.grad = None
+        xg = x.detach().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = pluggy_amd.moe_sublayer(xg, norm, mlp) if fused else xg + mlp(norm(xg))
+        out.backward(gout)
+
+    res = {}
+    for name, fused in (("unfused_ms", False), ("fused_ms", True)):
+        for _ in range(warmup):
+            step(fused)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            step(fused)
+        end.record()
+        torch.cuda.synchronize()
+        res[name] = round(start.elapsed_time(end) / steps, 4)
+    res["saved_ms"] = round(res["unfused_ms"] - res["fused_ms"], 4)
+    res["regime"] = "x + SparseMLP(RMSNorm(x)) fwd+bwd, fp32 residual stream and fp32 master weights, bf16 autocast"
+    return res
 
 
 def copy_bandwidth(mib: int, dev, reps: int = 5):
@@ -325,6 +377,8 @@ def main() -> int:
     }
     if args.copy_mib > 0:
         result["copy_reference"] = copy_bandwidth(args.copy_mib, dev)
+    if not args.no_neighbours and cfg.backward and cfg.hidden <= 4096:
+        result["neighbours"] = neighbours(cfg, inp, min(args.steps, 10), 2, dev)
     if not args.no_reference_gpu:
         ref = reference_gpu(cfg, inp, min(args.steps, 10), 2, dev)
         ref["speedup"] = round(result["value"] / ref["value"], 2)

@@ -136,6 +136,53 @@ PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_p
 PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, const void* grad_hidden_add,
                                     int dtype, int64_t T, int64_t K, int64_t H, void* grad_hidden, void* stream);
 
+/* ------------------------------------------------------ block neighbours ---
+ * The RMSNorm in front of the sparse MLP and the residual add behind it, as
+ * Qwen3MoeTransformerBlock.forward computes them (pluggy/models/qwen3_moe/
+ * qwen3_moe.py:281, x = x + ffn(norm2(x)); norm2 = torch.nn.RMSNorm, :260),
+ * fused into the row kernels of the block. */
+
+/* torch.nn.RMSNorm forward (elementwise weight): out[t] = (x[t] * r_t) * weight,
+ * r_t = 1 / sqrt(sum_j x[t,j]^2 / H + eps), fp32 arithmetic; rstd[t] = r_t.
+ * x: (T,H) x_dtype; weight: (H,) fp32; out: (T,H) out_dtype (the operand of the
+ * router and the dispatch, e.g. bf16 from an fp32 residual stream, so no
+ * separate cast); rstd: (T,) fp32. torch's default eps is finfo(x.dtype).eps. */
+PMOE_API int pmoe_rmsnorm_forward(const void* x, int x_dtype, const float* weight, float eps, int64_t T, int64_t H,
+                                  void* out, int out_dtype, float* rstd, void* stream);
+
+/* pmoe_combine with the residual add fused (moe.py:120-123 + qwen3_moe.py:281):
+ * out[t] = residual[t] + sum_k top_weights[t,k] * y[inv_pos[t*K+k]], fp32
+ * accumulation starting from the residual, k ascending. residual and out:
+ * (T,H) res_dtype (e.g. an fp32 residual stream over bf16 expert rows). */
+PMOE_API int pmoe_combine_residual(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos,
+                                   int dtype, const void* residual, int res_dtype, int64_t T, int64_t K, int64_t H,
+                                   void* out, void* stream);
+
+/* Backward of pmoe_combine_residual (the residual's gradient is grad_out
+ * itself): grad_y[p] = w * grad_out[t]; grad_top_weights[t,k] = <grad_out[t],
+ * y[inv_pos[t*K+k]]>. grad_out: (T,H) res_dtype; grad_y: (P,H) dtype. */
+PMOE_API int pmoe_combine_residual_backward(const void* grad_out, int res_dtype, const void* y,
+                                            const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
+                                            int64_t T, int64_t K, int64_t H, void* grad_y, void* grad_top_weights,
+                                            void* stream);
+
+/* Backward of the dispatch, the RMSNorm and the residual add in one row pass
+ * (autograd of qwen3_moe.py:281 through moe.py:104 and torch.nn.RMSNorm):
+ *   g[t]      = grad_normed_add[t] + sum_k grad_x_perm[inv_pos[t*K+k]]  (dL/d norm output)
+ *   grad_x[t] = grad_residual[t] + r_t * weight * g[t] - (r_t^3 / H) <g[t] * weight, x[t]> x[t]
+ *   grad_weight = sum_t g[t] * x[t] * r_t  (fixed-order partial sums; deterministic)
+ * grad_x_perm (T*K,H) and grad_normed_add (T,H) have dtype `dtype`; x,
+ * grad_residual and grad_x are (T,H) x_dtype; weight and rstd (from
+ * pmoe_rmsnorm_forward) fp32; grad_weight (H,) w_dtype. grad_x_perm,
+ * grad_normed_add, grad_residual and grad_weight may each be NULL (no term /
+ * not wanted). H <= 4096 (PMOE_ERR_UNSUPPORTED beyond). */
+PMOE_API size_t pmoe_dispatch_rmsnorm_backward_workspace_size(int64_t T, int64_t H);
+PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32_t* inv_pos,
+                                            const void* grad_normed_add, int dtype, const void* x, int x_dtype,
+                                            const float* weight, const float* rstd, const void* grad_residual,
+                                            int64_t T, int64_t K, int64_t H, void* grad_x, void* grad_weight,
+                                            int w_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------ whole expert FFN ---
  * Replaces moe_expert_ffn / _expert_ffn_grouped (pluggy/kernels/moe.py:68-168):
  * permute, dispatch, gate_up+SwiGLU, down, combine. The saved tensors

@@ -5,7 +5,7 @@ and operator (pluggy/kernels/moe.py:127-168), backed by hand-written HIP kernels
 in ``libpmoe.so`` (C ABI in ``include/pmoe.h``).
 """
 
-from .moe import RouterStats, moe_expert_ffn, router_topk, sparse_moe_block
+from .moe import RouterStats, moe_expert_ffn, moe_sublayer, router_topk, sparse_moe_block
 from .qwen3_moe import (
     Qwen3MoeExperts,
     Qwen3MoeSparseMLP,
@@ -21,6 +21,7 @@ __all__ = [
     "RouterStats",
     "load_balancing_loss_from_stats",
     "moe_expert_ffn",
+    "moe_sublayer",
     "router_topk",
     "router_z_loss_from_stats",
     "sparse_moe_block",

@@ -21,6 +21,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
+_F32 = ctypes.c_float
 
 # name -> (restype, argtypes); mirrors include/pmoe.h
 SIGNATURES = {
@@ -42,6 +43,12 @@ SIGNATURES = {
     "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_dispatch_backward": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P]),
+    "pmoe_rmsnorm_forward": (_INT, [_P, _INT, _P, _F32, _I64, _I64, _P, _INT, _P, _P]),
+    "pmoe_combine_residual": (_INT, [_P, _P, _INT, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),
+    "pmoe_combine_residual_backward": (_INT, [_P, _INT, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P]),
+    "pmoe_dispatch_rmsnorm_backward_workspace_size": (_SZ, [_I64, _I64]),
+    "pmoe_dispatch_rmsnorm_backward": (_INT, [_P, _P, _P, _INT, _P, _INT, _P, _P, _P, _I64, _I64, _I64, _P, _P,
+                                              _INT, _P, _SZ, _P]),
     "pmoe_expert_ffn_forward_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_expert_ffn_forward": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                                        _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -4,6 +4,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/pmoe.h"
 #include "kernels.h"
@@ -77,6 +78,14 @@ int check_moe_dims(int64_t T, int64_t K, int64_t E, int64_t H, int64_t I) {
                "problem too large (T*K=%lld)", (long long)(T * K));
   return PMOE_OK;
 }
+
+// Calls f with a null pointer of the element type of a dtype code.
+template <class F>
+hipError_t by_dtype(int code, F&& f) {
+  if (code == PMOE_BF16) return f(static_cast<bf16_t*>(nullptr));
+  return f(static_cast<float*>(nullptr));
+}
+#define PMOE_ELEM(p) std::remove_pointer_t<decltype(p)>
 
 }  // namespace
 
@@ -509,6 +518,114 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
   }
   // 4. dispatch backward
   if (grad_hidden) return pmoe_dispatch_backward(grad_y, inv_pos, nullptr, dtype, T, K, H, grad_hidden, stream);
+  return PMOE_OK;
+}
+
+// ------------------------------------------------------- block neighbours
+
+PMOE_API int pmoe_rmsnorm_forward(const void* x, int x_dtype, const float* weight, float eps, int64_t T, int64_t H,
+                                  void* out, int out_dtype, float* rstd, void* stream) {
+  PMOE_REQUIRE(T >= 0 && H > 0 && H % 8 == 0 && T <= kMaxIndex, "rmsnorm_forward: bad sizes T=%lld H=%lld",
+               (long long)T, (long long)H);
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype), "unknown dtype code");
+  PMOE_REQUIRE(eps >= 0.0f, "rmsnorm_forward: eps must be non-negative");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(x && weight && out && rstd, "rmsnorm_forward: null tensor");
+  hipError_t st = by_dtype(x_dtype, [&](auto xp) {
+    return by_dtype(out_dtype, [&](auto op) {
+      return rmsnorm_fwd<PMOE_ELEM(xp), PMOE_ELEM(op)>(static_cast<const PMOE_ELEM(xp)*>(x), weight, eps, (int)T,
+                                                       (int)H, static_cast<PMOE_ELEM(op)*>(out), rstd,
+                                                       as_stream(stream));
+    });
+  });
+  return hip_status(st, "rmsnorm_forward");
+}
+
+PMOE_API int pmoe_combine_residual(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos,
+                                   int dtype, const void* residual, int res_dtype, int64_t T, int64_t K, int64_t H,
+                                   void* out, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(y && top_weights && inv_pos && residual && out, "combine_residual: null tensor");
+  hipError_t st = by_dtype(dtype, [&](auto yp) {
+    return by_dtype(w_dtype, [&](auto wp) {
+      return by_dtype(res_dtype, [&](auto rp) {
+        return combine_rows_residual<PMOE_ELEM(yp), PMOE_ELEM(wp), PMOE_ELEM(rp)>(
+            static_cast<const PMOE_ELEM(yp)*>(y), static_cast<const PMOE_ELEM(wp)*>(top_weights), inv_pos,
+            static_cast<const PMOE_ELEM(rp)*>(residual), (int)T, (int)K, (int)H, static_cast<PMOE_ELEM(rp)*>(out),
+            as_stream(stream));
+      });
+    });
+  });
+  return hip_status(st, "combine_residual");
+}
+
+PMOE_API int pmoe_combine_residual_backward(const void* grad_out, int res_dtype, const void* y,
+                                            const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
+                                            int64_t T, int64_t K, int64_t H, void* grad_y, void* grad_top_weights,
+                                            void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(grad_out && y && top_weights && inv_pos && grad_y && grad_top_weights,
+               "combine_residual_backward: null tensor");
+  hipError_t st = by_dtype(dtype, [&](auto yp) {
+    return by_dtype(w_dtype, [&](auto wp) {
+      return by_dtype(res_dtype, [&](auto rp) {
+        return combine_rows_residual_bwd<PMOE_ELEM(yp), PMOE_ELEM(wp), PMOE_ELEM(rp)>(
+            static_cast<const PMOE_ELEM(rp)*>(grad_out), static_cast<const PMOE_ELEM(yp)*>(y),
+            static_cast<const PMOE_ELEM(wp)*>(top_weights), inv_pos, (int)T, (int)K, (int)H,
+            static_cast<PMOE_ELEM(yp)*>(grad_y), static_cast<PMOE_ELEM(wp)*>(grad_top_weights), as_stream(stream));
+      });
+    });
+  });
+  return hip_status(st, "combine_residual_backward");
+}
+
+PMOE_API size_t pmoe_dispatch_rmsnorm_backward_workspace_size(int64_t T, int64_t H) {
+  if (T <= 0 || H <= 0 || T > kMaxIndex) return 0;
+  return align_up((size_t)rmsnorm_bwd_blocks((int)T) * (size_t)H * sizeof(float)) +
+         align_up((size_t)rmsnorm_bwd_groups((int)T) * (size_t)H * sizeof(float));
+}
+
+PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32_t* inv_pos,
+                                            const void* grad_normed_add, int dtype, const void* x, int x_dtype,
+                                            const float* weight, const float* rstd, const void* grad_residual,
+                                            int64_t T, int64_t K, int64_t H, void* grad_x, void* grad_weight,
+                                            int w_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(x_dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  if (H > kRmsnormMaxH)
+    return fail(PMOE_ERR_UNSUPPORTED, "dispatch_rmsnorm_backward: hidden size %lld > %d", (long long)H,
+                kRmsnormMaxH);
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(x && weight && rstd && grad_x, "dispatch_rmsnorm_backward: null tensor");
+  PMOE_REQUIRE(!grad_x_perm || inv_pos, "dispatch_rmsnorm_backward: grad_x_perm without inv_pos");
+  const size_t need = grad_weight ? pmoe_dispatch_rmsnorm_backward_workspace_size(T, H) : 0;
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(PMOE_ERR_WORKSPACE, "dispatch_rmsnorm_backward: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  Carver cv(workspace);
+  const int nb = rmsnorm_bwd_blocks((int)T), ng = rmsnorm_bwd_groups((int)T);
+  float* partial = grad_weight ? cv.take<float>((size_t)nb * H) : nullptr;
+  float* grouped = grad_weight ? cv.take<float>((size_t)ng * H) : nullptr;
+  hipError_t st = by_dtype(dtype, [&](auto gp) {
+    return by_dtype(x_dtype, [&](auto xp) {
+      using TX = PMOE_ELEM(xp);
+      return dispatch_rmsnorm_bwd<PMOE_ELEM(gp), TX>(
+          static_cast<const PMOE_ELEM(gp)*>(grad_x_perm), inv_pos, static_cast<const PMOE_ELEM(gp)*>(grad_normed_add),
+          static_cast<const TX*>(x), weight, rstd, static_cast<const TX*>(grad_residual), (int)T, (int)K, (int)H,
+          static_cast<TX*>(grad_x), partial, s);
+    });
+  });
+  PMOE_TRY(st, "dispatch_rmsnorm_backward");
+  if (grad_weight) {
+    PMOE_TRY(sum_row_groups(partial, nb, (int)H, grouped, s), "dispatch_rmsnorm_backward (weight)");
+    st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(grouped, ng, H, static_cast<bf16_t*>(grad_weight), s)
+                              : reduce_partials<float>(grouped, ng, H, static_cast<float*>(grad_weight), s);
+    PMOE_TRY(st, "dispatch_rmsnorm_backward (weight)");
+  }
   return PMOE_OK;
 }
 

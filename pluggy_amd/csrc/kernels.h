@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace pmoe {
@@ -82,6 +84,32 @@ template <typename T>
 // dx = (add +) the K-sum; add (T_,H) may be NULL
 hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* add, int T_, int K, int H, T* dx,
                              hipStream_t s);
+
+// out = res + the weighted K-sum (the block's residual add fused into the combine)
+template <typename T, typename TW, typename TR>
+hipError_t combine_rows_residual(const T* y, const TW* w, const int32_t* inv_pos, const TR* res, int T_, int K, int H,
+                                 TR* out, hipStream_t s);
+// combine backward with the upstream gradient in its own dtype TD
+template <typename T, typename TW, typename TD>
+hipError_t combine_rows_residual_bwd(const TD* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K,
+                                     int H, T* dy, TW* dw, hipStream_t s);
+
+// ---- RMSNorm neighbours (norm.hip). w: (H,) fp32 norm weight; rstd: (T,) fp32.
+template <typename TX, typename TO>
+hipError_t rmsnorm_fwd(const TX* x, const float* w, float eps, int T_, int H, TO* out, float* rstd, hipStream_t s);
+// gx = res + RMSNorm-backward(add + K-sum of gxp); gw_partial: (rmsnorm_bwd_blocks(T), H) fp32 or NULL.
+template <typename T, typename TX>
+hipError_t dispatch_rmsnorm_bwd(const T* gxp, const int32_t* inv_pos, const T* add, const TX* x, const float* w,
+                                const float* rstd, const TX* res, int T_, int K, int H, TX* gx, float* gw_partial,
+                                hipStream_t s);
+constexpr int kRmsnormMaxH = 4096;
+constexpr int kRmsnormBwdMaxBlocks = 1024;
+int rmsnorm_bwd_blocks(int T_);
+// Tall partial matrices (rows x n) are reduced in two passes: groups of
+// kRowGroup rows into tmp (rmsnorm_bwd_groups(T) x n), then reduce_partials.
+constexpr int kRowGroup = 32;
+int rmsnorm_bwd_groups(int T_);
+hipError_t sum_row_groups(const float* partial, int rows, int n, float* tmp, hipStream_t s);
 
 // Chunk size (pairs) of the permutation histogram and the workspace it needs.
 constexpr int kPermuteChunk = 2048;

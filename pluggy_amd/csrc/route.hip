@@ -474,11 +474,12 @@ __global__ __launch_bounds__(256) void dispatch_kernel(const T* __restrict__ x, 
 
 // out[t] = (add[t] +) sum_k w[t,k] * y[inv_pos[t*K + k]].
 // WEIGHTED = false: unit weights (w unused, may be null). HAS_ADD = false: no
-// addend (add unused, may be null).
-template <typename T, typename TW, int KC, bool WEIGHTED, bool HAS_ADD>
+// addend (add unused, may be null). The addend (TA) and the output (TO) may
+// have another dtype than the rows (e.g. an fp32 residual stream).
+template <typename T, typename TW, int KC, bool WEIGHTED, bool HAS_ADD, typename TA = T, typename TO = T>
 __device__ __forceinline__ void gather_sum_row(const T* __restrict__ y, const TW* __restrict__ w,
-                                               const int32_t* __restrict__ inv_pos, const T* __restrict__ add, int t,
-                                               int K, int H, T* __restrict__ out, int lane) {
+                                               const int32_t* __restrict__ inv_pos, const TA* __restrict__ add, int t,
+                                               int K, int H, TO* __restrict__ out, int lane) {
   if constexpr (KC > 0) {
     int64_t row[KC];
     float wk[KC];
@@ -494,17 +495,17 @@ __device__ __forceinline__ void gather_sum_row(const T* __restrict__ y, const TW
 #pragma unroll
       for (int k = 0; k < KC; ++k) Vec8<T>::load(y + row[k] + c, v[k]);
       float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (HAS_ADD) Vec8<T>::load(add + (int64_t)t * H + c, acc);
+      if constexpr (HAS_ADD) Vec8<TA>::load(add + (int64_t)t * H + c, acc);
 #pragma unroll
       for (int k = 0; k < KC; ++k)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] += WEIGHTED ? wk[k] * v[k][i] : v[k][i];
-      Vec8<T>::store(out + (int64_t)t * H + c, acc);
+      Vec8<TO>::store(out + (int64_t)t * H + c, acc);
     }
   } else {
     for (int c = lane * 8; c < H; c += 64 * 8) {
       float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (HAS_ADD) Vec8<T>::load(add + (int64_t)t * H + c, acc);
+      if constexpr (HAS_ADD) Vec8<TA>::load(add + (int64_t)t * H + c, acc);
       for (int k = 0; k < K; ++k) {
         const int64_t q = (int64_t)t * K + k;
         float v[8];
@@ -518,7 +519,7 @@ __device__ __forceinline__ void gather_sum_row(const T* __restrict__ y, const TW
           for (int i = 0; i < 8; ++i) acc[i] += v[i];
         }
       }
-      Vec8<T>::store(out + (int64_t)t * H + c, acc);
+      Vec8<TO>::store(out + (int64_t)t * H + c, acc);
     }
   }
 }
@@ -529,20 +530,34 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ y, c
                                                       T* __restrict__ out) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  gather_sum_row<T, TW, KC, true, false>(y, w, inv_pos, nullptr, t, K, H, out, threadIdx.x & 63);
+  gather_sum_row<T, TW, KC, true, false>(y, w, inv_pos, static_cast<const T*>(nullptr), t, K, H, out,
+                                         threadIdx.x & 63);
+}
+
+// out[t] = res[t] + sum_k w[t,k] * y[inv_pos[t*K + k]]: the combine with the
+// block's residual add (qwen3_moe.py:281) fused; res and out share dtype TR.
+template <typename T, typename TW, typename TR, int KC>
+__global__ __launch_bounds__(256) void combine_residual_kernel(const T* __restrict__ y, const TW* __restrict__ w,
+                                                               const int32_t* __restrict__ inv_pos,
+                                                               const TR* __restrict__ res, int T_, int K, int H,
+                                                               TR* __restrict__ out) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T_) return;
+  gather_sum_row<T, TW, KC, true, true, TR, TR>(y, w, inv_pos, res, t, K, H, out, threadIdx.x & 63);
 }
 
 // grad_y[inv_pos[t*K+k]] = w[t,k] * dout[t]; dw[t,k] = <dout[t], y[inv_pos[t*K+k]]>.
-// dout[t] is read once per chunk for all k.
-template <typename T, typename TW, int KC>
-__global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ y,
+// dout[t] (dtype TD, e.g. the fp32 gradient of a residual stream) is read
+// once per chunk for all k.
+template <typename T, typename TW, int KC, typename TD = T>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const TD* __restrict__ dout, const T* __restrict__ y,
                                                           const TW* __restrict__ w,
                                                           const int32_t* __restrict__ inv_pos, int T_, int K, int H,
                                                           T* __restrict__ dy, TW* __restrict__ dw) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  const T* drow = dout + (int64_t)t * H;
+  const TD* drow = dout + (int64_t)t * H;
   if constexpr (KC > 0) {
     int64_t row[KC];
     float wk[KC], dot[KC];
@@ -555,7 +570,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
     }
     for (int c = lane * 8; c < H; c += 64 * 8) {
       float g[8], v[KC][8];
-      Vec8<T>::load(drow + c, g);
+      Vec8<TD>::load(drow + c, g);
 #pragma unroll
       for (int k = 0; k < KC; ++k) Vec8<T>::load(y + row[k] + c, v[k]);
 #pragma unroll
@@ -582,7 +597,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
       float dot = 0.0f;
       for (int c = lane * 8; c < H; c += 64 * 8) {
         float g[8], v[8], o[8];
-        Vec8<T>::load(drow + c, g);
+        Vec8<TD>::load(drow + c, g);
         Vec8<T>::load(y + pos * H + c, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -748,6 +763,35 @@ hipError_t combine_rows_bwd(const T* dout, const T* y, const TW* w, const int32_
   });
 }
 
+// Top-k values with a compile-time specialisation in the residual variants.
+template <class F>
+hipError_t with_kc8(int K, F&& f) {
+  if (K == 8) return f(std::integral_constant<int, 8>());
+  return f(std::integral_constant<int, 0>());
+}
+
+template <typename T, typename TW, typename TR>
+hipError_t combine_rows_residual(const T* y, const TW* w, const int32_t* inv_pos, const TR* res, int T_, int K, int H,
+                                 TR* out, hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  return with_kc8(K, [&](auto kc) {
+    hipLaunchKernelGGL((combine_residual_kernel<T, TW, TR, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256),
+                       0, s, y, w, inv_pos, res, T_, K, H, out);
+    return hipGetLastError();
+  });
+}
+
+template <typename T, typename TW, typename TD>
+hipError_t combine_rows_residual_bwd(const TD* dout, const T* y, const TW* w, const int32_t* inv_pos, int T_, int K,
+                                     int H, T* dy, TW* dw, hipStream_t s) {
+  if (T_ == 0) return hipSuccess;
+  return with_kc8(K, [&](auto kc) {
+    hipLaunchKernelGGL((combine_bwd_kernel<T, TW, decltype(kc)::value, TD>), dim3(blocks_for(T_, 4)), dim3(256), 0, s,
+                       dout, y, w, inv_pos, T_, K, H, dy, dw);
+    return hipGetLastError();
+  });
+}
+
 template <typename T>
 hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* add, int T_, int K, int H, T* dx,
                              hipStream_t s) {
@@ -788,5 +832,16 @@ template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*,
 
 PMOE_INST_ROWS(bf16_t)
 PMOE_INST_ROWS(float)
+
+#define PMOE_INST_RES(T, TW, TR)                                                                                  \
+  template hipError_t combine_rows_residual<T, TW, TR>(const T*, const TW*, const int32_t*, const TR*, int, int,   \
+                                                       int, TR*, hipStream_t);                                      \
+  template hipError_t combine_rows_residual_bwd<T, TW, TR>(const TR*, const T*, const TW*, const int32_t*, int,    \
+                                                           int, int, T*, TW*, hipStream_t);
+#define PMOE_INST_RES2(T, TW) PMOE_INST_RES(T, TW, bf16_t) PMOE_INST_RES(T, TW, float)
+PMOE_INST_RES2(bf16_t, bf16_t)
+PMOE_INST_RES2(bf16_t, float)
+PMOE_INST_RES2(float, bf16_t)
+PMOE_INST_RES2(float, float)
 
 }  // namespace pmoe

@@ -267,6 +267,32 @@ def _(grad_out, y, top_weights, inv_pos):
     return torch.empty_like(y), torch.empty_like(top_weights)
 
 
+def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_rows, need_gu, need_dn, reduce_rows):
+    """The expert GEMMs' backward from grad_y. With need_rows, the (P, H) input
+    gradient of the dispatched rows goes to ``reduce_rows`` (which sums each
+    token's K rows) before the gate_up weight gradient is computed, so it is
+    freed early. -> (reduce_rows result or None, grad_gate_up or None,
+    grad_down or None)."""
+    E = gate_up.shape[0]
+    reduced = g_gu_w = g_dn_w = None
+    g_gu = None
+    if need_rows or need_gu:
+        with _stage("down_dgrad"):
+            g_gu = ops.down_proj_dgrad(grad_y, gu, down, offs)
+    if need_dn:
+        with _stage("down_wgrad"):
+            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E)
+    if need_rows:
+        with _stage("gate_up_dgrad"):
+            g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
+        reduced = reduce_rows(g_xp)
+        del g_xp
+    if need_gu:
+        with _stage("gate_up_wgrad"):
+            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+    return reduced, g_gu_w, g_dn_w
+
+
 @torch.library.custom_op("pmoe::expert_bwd", mutates_args=(),
                          schema="(Tensor grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
                                 "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_hidden_add, int tokens, int top_k, "
@@ -275,24 +301,12 @@ def _expert_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidd
     """The expert GEMMs' backward from grad_y: -> grad_hidden (+ grad_hidden_add),
     grad_gate_up, grad_down; an empty tensor where needs[i] is false (needs:
     hidden, gate_up, down)."""
-    E = gate_up.shape[0]
-    g_hidden = g_gu_w = g_dn_w = None
-    g_gu = None
-    if needs[0] or needs[1]:
-        with _stage("down_dgrad"):
-            g_gu = ops.down_proj_dgrad(grad_y, gu, down, offs)
-    if needs[2]:
-        with _stage("down_wgrad"):
-            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E)
-    if needs[0]:
-        with _stage("gate_up_dgrad"):
-            g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
+    def reduce_rows(g_xp):
         with _stage("dispatch_bwd"):
-            g_hidden = ops.dispatch_backward(g_xp, inv_pos, tokens, top_k, add=grad_hidden_add)
-        del g_xp
-    if needs[1]:
-        with _stage("gate_up_wgrad"):
-            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+            return ops.dispatch_backward(g_xp, inv_pos, tokens, top_k, add=grad_hidden_add)
+
+    g_hidden, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, needs[0],
+                                                      needs[1], needs[2], reduce_rows)
     e = _empty_like_none
     return (g_hidden if g_hidden is not None else e(grad_y), g_gu_w if g_gu_w is not None else e(gate_up),
             g_dn_w if g_dn_w is not None else e(down))
@@ -477,3 +491,188 @@ def moe_expert_ffn(
     out = torch.ops.pmoe.expert_ffn_fwd(hidden.to(dt).contiguous(), top_indices.to(torch.int64).contiguous(),
                                         tw.contiguous(), gu, dn)[0]
     return out.to(hidden.dtype)
+
+
+# ------------------------------- MoE half of the block: RMSNorm -> MLP -> add
+
+
+@torch.library.custom_op("pmoe::moe_sublayer_fwd", mutates_args=(),
+                         schema="(Tensor x, Tensor norm_weight, float eps, Tensor router_weight, Tensor gate_up_proj, "
+                                "Tensor down_proj, int top_k, bool norm_topk_prob, Tensor? logit_bias) -> (Tensor, "
+                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+                                "Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
+                      logit_bias):
+    """x + SparseMLP(RMSNorm(x)) with the norm and the residual add in the row kernels.
+
+    The kernels compute in gate_up_proj's dtype; x is the residual stream (its
+    own dtype). -> out, router_logits, counts, prob_sum, lse_sq_sum, then what
+    the backward reads: normed, rstd, top_i, top_w32, top_w, offs, inv_pos,
+    x_perm, gu, mid, y.
+    """
+    with _stage("rmsnorm"):
+        normed, rstd = ops.rmsnorm_forward(x, norm_weight, eps, gate_up_proj.dtype)
+    with _stage("router_fwd"):
+        logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
+            normed, router_weight, top_k, norm_topk_prob, logit_bias)
+    with _stage("permute"):
+        _, offs, _, inv_pos = ops.permute(top_i, gate_up_proj.shape[0])
+    with _stage("dispatch"):
+        x_perm = ops.dispatch(normed, inv_pos, top_k)
+    with _stage("gate_up_fwd"):
+        gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
+    with _stage("down_fwd"):
+        y = ops.down_proj(mid, down_proj, offs)
+    with _stage("combine"):
+        out = ops.combine_residual(y, top_w, inv_pos, x)
+    return out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y
+
+
+@_moe_sublayer_fwd.register_fake
+def _(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+    T, H = x.shape
+    E, K, I = router_weight.shape[0], top_k, gate_up_proj.shape[1] // 2
+    cdt = gate_up_proj.dtype
+    f32, i32 = torch.float32, torch.int32
+    P = T * K
+    return (torch.empty_like(x), x.new_empty(T, E, dtype=f32), x.new_empty(E, dtype=i32), x.new_empty(E, dtype=f32),
+            x.new_empty(1, dtype=f32), x.new_empty(T, H, dtype=cdt), x.new_empty(T, dtype=f32),
+            x.new_empty(T, K, dtype=torch.int64), x.new_empty(T, K, dtype=f32), x.new_empty(T, K, dtype=cdt),
+            x.new_empty(E, dtype=i32), x.new_empty(P, dtype=i32), x.new_empty(P, H, dtype=cdt),
+            x.new_empty(P, 2 * I, dtype=cdt), x.new_empty(P, I, dtype=cdt), x.new_empty(P, H, dtype=cdt))
+
+
+@torch.library.custom_op("pmoe::combine_residual_bwd", mutates_args=(),
+                         schema="(Tensor grad_out, Tensor y, Tensor top_weights, Tensor inv_pos) -> (Tensor, Tensor)")
+def _combine_residual_bwd(grad_out, y, top_weights, inv_pos):
+    """-> grad_y (P,H) = w * grad_out gathered, grad_top_weights (T,K); grad_out in the stream's dtype."""
+    with _stage("combine_bwd"):
+        return ops.combine_residual_backward(grad_out, y, top_weights, inv_pos)
+
+
+@_combine_residual_bwd.register_fake
+def _(grad_out, y, top_weights, inv_pos):
+    return torch.empty_like(y), torch.empty_like(top_weights)
+
+
+@torch.library.custom_op("pmoe::sublayer_bwd", mutates_args=(),
+                         schema="(Tensor? grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
+                                "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_normed_add, Tensor x, "
+                                "Tensor norm_weight, Tensor rstd, Tensor? grad_residual, int top_k, bool[] needs) -> "
+                                "(Tensor, Tensor, Tensor, Tensor)")
+def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd,
+                  grad_residual, top_k, needs):
+    """Expert GEMM backward, then the dispatch, RMSNorm and residual backward in
+    one row pass: -> grad_x, grad_norm_weight, grad_gate_up, grad_down (empty
+    where needs[i] is false; needs: x, norm_weight, gate_up, down)."""
+    need_x = needs[0] or needs[1]
+
+    def reduce_rows(g_xp):
+        with _stage("dispatch_bwd"):
+            return ops.dispatch_rmsnorm_backward(g_xp, inv_pos, grad_normed_add, x, norm_weight, rstd, grad_residual,
+                                                 top_k, need_weight=needs[1])
+
+    reduced = g_gu_w = g_dn_w = None
+    if grad_y is not None:
+        reduced, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_x,
+                                                         needs[2], needs[3], reduce_rows)
+    elif need_x:
+        reduced = reduce_rows(None)
+    g_x, g_nw = reduced if reduced is not None else (None, None)
+    e = _empty_like_none
+    return (g_x if g_x is not None and needs[0] else e(x), g_nw if g_nw is not None else e(norm_weight),
+            g_gu_w if g_gu_w is not None else e(gate_up), g_dn_w if g_dn_w is not None else e(down))
+
+
+@_sublayer_bwd.register_fake
+def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd, grad_residual,
+      top_k, needs):
+    e = _empty_like_none
+    return (torch.empty_like(x) if needs[0] else e(x), torch.empty_like(norm_weight) if needs[1] else e(norm_weight),
+            torch.empty_like(gate_up) if needs[2] else e(gate_up), torch.empty_like(down) if needs[3] else e(down))
+
+
+def _sublayer_setup(ctx, inputs, output):
+    x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias = inputs
+    (out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid,
+     y) = output
+    ctx.save_for_backward(x, norm_weight, rstd, normed, router_weight, logits, top_i, top_w32, top_w, gate_up_proj,
+                          down_proj, offs, inv_pos, x_perm, gu, mid, y)
+    ctx.norm_topk_prob = bool(norm_topk_prob)
+    ctx.top_k = int(top_k)
+    ctx.mark_non_differentiable(counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu,
+                                mid, y)
+    ctx.set_materialize_grads(False)
+
+
+def _sublayer_backward(ctx, g_out, g_logits, *_rest):
+    """d out / d x is the identity (the residual) plus the norm-and-MLP path;
+    the residual term, the router's share and the K expert rows are all summed
+    inside the one row pass of the dispatch backward."""
+    (x, nw, rstd, normed, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
+     y) = ctx.saved_tensors
+    need = ctx.needs_input_grad  # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias
+    nones = (None,) * 9
+    if g_out is None and g_logits is None:
+        return nones
+    if g_logits is not None:
+        g_logits = g_logits.float().contiguous()
+    g_y = g_tw = None
+    if g_out is not None:
+        g_out = g_out.contiguous()
+        g_y, g_tw = torch.ops.pmoe.combine_residual_bwd(g_out, y, top_w, inv_pos)
+    gx_router = g_rw = None
+    if need[0] or need[1] or need[3]:
+        gx_router, g_rw = torch.ops.pmoe.router_bwd(normed, rw, logits, top_i, top_w32, g_tw, g_logits,
+                                                    ctx.norm_topk_prob)
+    needs = [bool(need[0]), bool(need[1]), bool(need[4]) and g_y is not None, bool(need[5]) and g_y is not None]
+    g_x = g_nw = g_gu_w = g_dn_w = None
+    if any(needs):
+        g_x, g_nw, g_gu_w, g_dn_w = torch.ops.pmoe.sublayer_bwd(
+            g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if (need[0] or need[1]) else None, x, nw,
+            rstd, g_out if need[0] else None, ctx.top_k, needs)
+        g_x, g_nw, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_x, g_nw, g_gu_w, g_dn_w))
+    return (g_x if need[0] else None, g_nw if need[1] else None, None, g_rw if need[3] else None,
+            g_gu_w if need[4] else None, g_dn_w if need[5] else None, None, None, None)
+
+
+_moe_sublayer_fwd.register_autograd(_sublayer_backward, setup_context=_sublayer_setup)
+
+
+def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
+    """``x + mlp(norm(x))`` — the MoE half of ``Qwen3MoeTransformerBlock.forward``
+    (qwen3_moe.py:281) — with the RMSNorm and the residual add fused into the
+    block's row kernels.
+
+    ``norm`` is the block's ``torch.nn.RMSNorm`` (elementwise weight; eps None
+    means ``finfo(x.dtype).eps``, as torch), ``mlp`` a
+    ``pluggy_amd.Qwen3MoeSparseMLP``, whose ``last_router_logits`` and router
+    statistics are set as its own forward sets them. ``x`` (B, S, H) is the
+    residual stream (fp32 or bf16); the experts and the router run in bf16
+    under CUDA autocast, else in the expert weights' dtype (cast to x's dtype
+    first, as ``moe_expert_ffn``). Same value as
+    ``x + mlp(norm(x))`` up to the rounding of the normed rows and of the MLP
+    output, which this path does not round to the compute dtype before the add.
+    """
+    B, S, H = x.shape
+    require_gpu(x)
+    assert isinstance(norm, torch.nn.RMSNorm) and tuple(norm.normalized_shape) == (H,) and norm.weight is not None
+    if H > 4096:  # the fused backward keeps a row in registers; wider rows take the unfused path
+        return x + mlp(norm(x))
+    r = mlp.router
+    flat = x.reshape(B * S, H).contiguous()
+    amp = _amp_dtype(flat)
+    cdt = flat.dtype if amp is None else amp
+    eps = norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
+    nw = norm.weight if norm.weight.dtype == torch.float32 else norm.weight.float()
+    rw = r.weight if amp is None else r.weight.to(amp)
+    if rw.dtype not in (torch.float32, torch.bfloat16):
+        rw = rw.float()
+    gu = mlp.experts.gate_up_proj.to(dtype=cdt).contiguous()
+    dn = mlp.experts.down_proj.to(dtype=cdt).contiguous()
+    bias = r.logit_bias.float().contiguous() if r.logit_bias is not None else None
+    out, logits, counts, psum, lse2 = torch.ops.pmoe.moe_sublayer_fwd(
+        flat, nw.contiguous(), float(eps), rw.contiguous(), gu, dn, int(r.top_k), bool(r.norm_topk_prob), bias)[:5]
+    r.last_stats = RouterStats(counts, psum, lse2, flat.shape[0])
+    mlp.last_router_logits = logits
+    return out.reshape(B, S, H)

@@ -184,3 +184,57 @@ def dispatch_backward(grad_x_perm, inv_pos, tokens: int, top_k: int, add=None):
     call("pmoe_dispatch_backward", ptr(grad_x_perm), ptr(inv_pos), ptr(add), dtype_code(grad_x_perm.dtype), tokens,
          top_k, H, ptr(gh), stream_of(grad_x_perm))
     return gh
+
+
+# --------------------------------------------- block neighbours (norm2, residual)
+
+
+def rmsnorm_forward(x, weight, eps: float, out_dtype):
+    """torch.nn.RMSNorm in fp32 arithmetic -> out (T,H) out_dtype, rstd (T,) fp32. weight (H,) fp32."""
+    require_gpu(x, weight)
+    T, H = x.shape
+    out = torch.empty(T, H, dtype=out_dtype, device=x.device)
+    rstd = torch.empty(T, dtype=torch.float32, device=x.device)
+    call("pmoe_rmsnorm_forward", ptr(x), dtype_code(x.dtype), ptr(weight), float(eps), T, H, ptr(out),
+         dtype_code(out_dtype), ptr(rstd), stream_of(x))
+    return out, rstd
+
+
+def combine_residual(y, top_weights, inv_pos, residual):
+    """out (residual.dtype) = residual + the weighted K-sum of the expert rows."""
+    T, K = top_weights.shape
+    H = y.shape[1]
+    out = torch.empty_like(residual)
+    call("pmoe_combine_residual", ptr(y), ptr(top_weights), dtype_code(top_weights.dtype), ptr(inv_pos),
+         dtype_code(y.dtype), ptr(residual), dtype_code(residual.dtype), T, K, H, ptr(out), stream_of(y))
+    return out
+
+
+def combine_residual_backward(grad_out, y, top_weights, inv_pos):
+    """-> grad_y (y.dtype), grad_top_weights; grad_out in the residual stream's dtype."""
+    T, K = top_weights.shape
+    H = y.shape[1]
+    gy = torch.empty_like(y)
+    gw = torch.empty_like(top_weights)
+    call("pmoe_combine_residual_backward", ptr(grad_out), dtype_code(grad_out.dtype), ptr(y), ptr(top_weights),
+         dtype_code(top_weights.dtype), ptr(inv_pos), dtype_code(y.dtype), T, K, H, ptr(gy), ptr(gw), stream_of(y))
+    return gy, gw
+
+
+def dispatch_rmsnorm_backward(grad_x_perm, inv_pos, grad_normed_add, x, weight, rstd, grad_residual, top_k: int,
+                              need_weight: bool = True, weight_dtype=torch.float32):
+    """-> grad_x (x.dtype), grad_weight (weight_dtype, or None).
+
+    grad_x = grad_residual + RMSNorm-backward(grad_normed_add + K-sum of grad_x_perm);
+    grad_x_perm, grad_normed_add and grad_residual may each be None.
+    """
+    T, H = x.shape
+    g = grad_x_perm if grad_x_perm is not None else grad_normed_add
+    gdt = g.dtype if g is not None else torch.bfloat16
+    gx = torch.empty_like(x)
+    gw = torch.empty(H, dtype=weight_dtype, device=x.device) if need_weight else None
+    ws = workspace(size("pmoe_dispatch_rmsnorm_backward_workspace_size", T, H) if need_weight else 0, x.device)
+    call("pmoe_dispatch_rmsnorm_backward", ptr(grad_x_perm), ptr(inv_pos), ptr(grad_normed_add), dtype_code(gdt),
+         ptr(x), dtype_code(x.dtype), ptr(weight), ptr(rstd), ptr(grad_residual), T, top_k, H, ptr(gx), ptr(gw),
+         dtype_code(weight_dtype), ptr(ws), ws.numel(), stream_of(x))
+    return gx, gw

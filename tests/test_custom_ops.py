@@ -68,3 +68,26 @@ def test_backward_fakes_drop_unneeded_grads(pmoe_ops):
     assert ggu.numel() == 0  # absent gradient: empty stand-in
     g_y, g_w = pmoe_ops.combine_bwd(_meta(T, H), _meta(P, H), _meta(T, K), _meta(P, dtype=i32))
     assert _sig([g_y, g_w]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]
+
+
+def test_moe_sublayer_fwd_fake(pmoe_ops):
+    # fp32 residual stream, bf16 compute (the experts' dtype)
+    out = pmoe_ops.moe_sublayer_fwd(_meta(T, H, dtype=torch.float32), _meta(H, dtype=torch.float32), 1e-6,
+                                    _meta(E, H, dtype=torch.bfloat16), _meta(E, 2 * I, H), _meta(E, H, I), K, True,
+                                    None)
+    bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
+    assert _sig(out) == [((T, H), f32), ((T, E), f32), ((E,), i32), ((E,), f32), ((1,), f32), ((T, H), bf),
+                         ((T,), f32), ((T, K), torch.int64), ((T, K), f32), ((T, K), bf), ((E,), i32), ((P,), i32),
+                         ((P, H), bf), ((P, 2 * I), bf), ((P, I), bf), ((P, H), bf)]
+
+
+def test_sublayer_backward_fakes(pmoe_ops):
+    gy, gw = pmoe_ops.combine_residual_bwd(_meta(T, H, dtype=torch.float32), _meta(P, H), _meta(T, K),
+                                           _meta(P, dtype=torch.int32))
+    assert _sig([gy, gw]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]
+    x, nw = _meta(T, H, dtype=torch.float32), _meta(H, dtype=torch.float32)
+    outs = pmoe_ops.sublayer_bwd(_meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I), _meta(E, dtype=torch.int32),
+                                 _meta(P, dtype=torch.int32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), _meta(T, H),
+                                 x, nw, _meta(T, dtype=torch.float32), x, K, [True, False, True, True])
+    assert _sig(outs) == [((T, H), torch.float32), ((0,), torch.float32), ((E, 2 * I, H), torch.bfloat16),
+                          ((E, H, I), torch.bfloat16)]
