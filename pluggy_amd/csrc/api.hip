@@ -129,7 +129,7 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   // fp32 partials are summed in a fixed order by the top-k kernel.
   const float* lparts = logits;
   int nparts = 1;
-  int64_t pstride = 0;
+  int64_t pstride = 0, ldp = E;
   if (T > 0) {
     if (x_dtype == PMOE_BF16) {
       const bf16_t* wb = (const bf16_t*)weight;
@@ -141,7 +141,8 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
       }
       PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, nparts, t, h, e, parts, s), "router logits GEMM");
       lparts = parts;
-      pstride = T * E;
+      pstride = E;
+      ldp = (int64_t)nparts * E;
     } else {
       hipError_t st = w_dtype == PMOE_F32
                           ? router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s)
@@ -151,10 +152,10 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
     }
     hipError_t st =
         tw_dtype == PMOE_BF16
-            ? router_topk<bf16_t>(lparts, nparts, pstride, logits, logit_bias, t, e, k, norm_topk_prob,
+            ? router_topk<bf16_t>(lparts, nparts, pstride, ldp, logits, logit_bias, t, e, k, norm_topk_prob,
                                   (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
                                   kRouterRowsPerBlock, s)
-            : router_topk<float>(lparts, nparts, pstride, logits, logit_bias, t, e, k, norm_topk_prob,
+            : router_topk<float>(lparts, nparts, pstride, ldp, logits, logit_bias, t, e, k, norm_topk_prob,
                                  (float*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
                                  kRouterRowsPerBlock, s);
     PMOE_TRY(st, "router top-k");

@@ -123,18 +123,30 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
   return launch_gemm<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
 }
 
-// Router logits from bf16 pieces of the router weight on the DMA engine: one
-// batched GEMM (64x128 blocks, four 32x64 wave tiles) per piece, fp32 out.
+// Router GEMM tile configurations (overridable at build time for sweeps).
+#ifndef PMOE_CFG_ROUTER_LOGITS
+#define PMOE_CFG_ROUTER_LOGITS DmaCfg<64, 128, 32, 64, 2>
+#endif
+#ifndef PMOE_CFG_ROUTER_DX
+#define PMOE_CFG_ROUTER_DX DmaCfg<128, 128, 64, 64, 2>
+#endif
+#ifndef PMOE_CFG_ROUTER_DW
+#define PMOE_CFG_ROUTER_DW DmaCfg<128, 128, 64, 64, 2>
+#endif
+
+// Router logits from bf16 pieces of the router weight on the DMA engine: the
+// pieces are stacked along N (npieces*E columns), so the n-tiles of one
+// m-tile share its x rows in L2 and x is read from HBM once; fp32 out,
+// (T, npieces*E) row-major (64x128 blocks, four 32x64 wave tiles).
 hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
                                      float* parts, hipStream_t s) {
   GemmParams p = zero_params();
   p.A = x; p.lda = H;
-  p.B = w3; p.ldb = H; p.strideB = (int64_t)E * H;
-  p.C = parts; p.ldc = E; p.strideC = (int64_t)T * E;
-  p.groups = npieces;
-  p.M = T; p.N = E; p.K = H;
-  p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)E * H * 2;
-  return launch_gemm_dma<DmaCfg<64, 128, 32, 64, 2>, true, true, GM_BATCH, EPI_STORE, float>(p, s);
+  p.B = w3; p.ldb = H;
+  p.C = parts; p.ldc = npieces * E;
+  p.M = T; p.N = npieces * E; p.K = H;
+  p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)npieces * E * H * 2;
+  return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_NONE, EPI_STORE, float>(p, s);
 }
 
 // Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
@@ -146,7 +158,7 @@ hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, 
   p.C = dx; p.ldc = H;
   p.M = T; p.N = H; p.K = 3 * ldl;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)3 * ldl * H * 2;
-  return launch_gemm_dma<DmaCfg<128, 128, 64, 64, 2>, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
+  return launch_gemm_dma<PMOE_CFG_ROUTER_DX, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
 }
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and
@@ -161,7 +173,7 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
   p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
   p.M = E; p.N = H; p.K = T;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
-  return launch_gemm_dma<DmaCfg<128, 128, 64, 64, 2>, false, false, GM_RED, EPI_STORE, float>(p, s);
+  return launch_gemm_dma<PMOE_CFG_ROUTER_DW, false, false, GM_RED, EPI_STORE, float>(p, s);
 }
 
 template <typename TX, typename TW>

@@ -44,14 +44,17 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
                           float* partial, hipStream_t s);
 
 // ---- routing, permutation and row movement (route.hip).
-// logits = sum of nparts fp32 partial products (parts + q*part_stride), then
-// softmax / top-k / renormalisation and the per-block statistics.
+// logits = sum of nparts fp32 partial products (partial q of (t, e) at
+// parts[t*ldp + q*part_stride + e]), then softmax / top-k / renormalisation
+// and the per-block statistics.
 template <typename TW>
-hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, float* logits, const float* logit_bias,
+hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int64_t ldp, float* logits,
+                       const float* logit_bias,
                        int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
                        float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s);
 hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s);
-// parts[g] = x . w3[g]^T for g < npieces, x (T,H) bf16, w3 (npieces,E,H) bf16, parts fp32 (npieces,T,E)
+// parts (T, npieces*E) fp32 = x . [w3[0]; w3[1]; ...]^T: one GEMM over the stacked pieces, so x is
+// read once; x (T,H) bf16, w3 (npieces,E,H) bf16
 hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
                                      float* parts, hipStream_t s);
 hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,

@@ -35,18 +35,21 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
 }
 
 // Logits of row `row`: the fixed-order sum of the partial products
-// ((p0 + p1) + p2), plus the optional bias. parts may alias logits (nparts 1).
+// ((p0 + p1) + p2), plus the optional bias. Partial q of (row, e) sits at
+// parts[row * ldp + q * part_stride + e]. parts may alias logits (nparts 1).
 template <int EPL>
-__device__ __forceinline__ void load_logits(const float* parts, int nparts, int64_t part_stride, float* logits,
-                                            const float* bias, int row, int E, int lane, float (&v)[EPL]) {
+__device__ __forceinline__ void load_logits(const float* parts, int nparts, int64_t part_stride, int64_t ldp,
+                                            float* logits, const float* bias, int row, int E, int lane,
+                                            float (&v)[EPL]) {
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     float x = -INFINITY;
     if (e < E) {
       const int64_t o = (int64_t)row * E + e;
-      x = parts[o];
-      for (int q = 1; q < nparts; ++q) x += parts[q * part_stride + o];
+      const int64_t op = (int64_t)row * ldp + e;
+      x = parts[op];
+      for (int q = 1; q < nparts; ++q) x += parts[q * part_stride + op];
       if (bias != nullptr) x += bias[e];
       if (nparts > 1 || bias != nullptr || parts != logits) logits[o] = x;
     }
@@ -56,7 +59,7 @@ __device__ __forceinline__ void load_logits(const float* parts, int nparts, int6
 
 template <int EPL, typename TW>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ parts, int nparts,
-                                                          int64_t part_stride, float* logits,
+                                                          int64_t part_stride, int64_t ldp, float* logits,
                                                           const float* __restrict__ bias,
                                                           int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
                                                           int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   const int row1 = min(T, row0 + rows_per_block);
   for (int row = row0 + wave; row < row1; row += 4) {
     float v[EPL];
-    load_logits<EPL>(parts, nparts, part_stride, logits, bias, row, E, lane, v);
+    load_logits<EPL>(parts, nparts, part_stride, ldp, logits, bias, row, E, lane, v);
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
@@ -635,7 +638,8 @@ hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s) {
 }
 
 template <typename TW>
-hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, float* logits, const float* logit_bias,
+hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int64_t ldp, float* logits,
+                       const float* logit_bias,
                        int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
                        float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
   if (T == 0) return hipSuccess;
@@ -643,7 +647,7 @@ hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, floa
   const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \
   hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, parts, nparts, part_stride,   \
-                     logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2,        \
+                     ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2,   \
                      blk_counts, rows_per_block)
   if (E <= 64) PMOE_TOPK_CASE(1);
   else if (E <= 128) PMOE_TOPK_CASE(2);
@@ -807,10 +811,10 @@ hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* 
   });
 }
 
-template hipError_t router_topk<bf16_t>(const float*, int, int64_t, float*, const float*, int, int, int, int, bf16_t*,
-                                        int64_t*, float*, float*, float*, int*, int, hipStream_t);
-template hipError_t router_topk<float>(const float*, int, int64_t, float*, const float*, int, int, int, int, float*,
-                                       int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
+                                        bf16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<float>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
+                                       float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
                                            int, int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
