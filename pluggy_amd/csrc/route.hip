@@ -13,9 +13,48 @@ namespace {
 
 __device__ __forceinline__ float nan_to_neg_inf(float v) { return v != v ? -INFINITY : v; }
 
-// Ranking key of top-k: larger logit first, equal logits -> lower expert id.
-__device__ __forceinline__ bool better(float v, int e, float bv, int be) {
-  return v > bv || (v == bv && e < be);
+// Top-k ranks larger logits first, equal logits -> lower expert id. Keys are
+// the logits mapped to ints in the same order (-0 folded into +0, so the two
+// zeros tie as they do as floats), so a wave-wide max is an integer max.
+__device__ __forceinline__ int rank_key(float v) {
+  const int b = __float_as_int(v + 0.0f);
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float key_value(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_max(int v) {
+  return max(v, __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xf, false));
+}
+
+// Max over the 64 lanes in six DPP steps (no LDS round trips): pairs, quads,
+// half rows, rows, then rows 1 and 3 take lane 15 of the row before, rows 2
+// and 3 take lane 31; lane 63 ends with the total.
+__device__ __forceinline__ int wave_max_dpp(int v) {
+  v = dpp_max<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_max<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_max<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_max<0x140, 0xf>(v);  // row_mirror
+  v = dpp_max<0x142, 0xa>(v);  // row_bcast:15
+  v = dpp_max<0x143, 0xc>(v);  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// fmaxf over the 64 lanes by the same DPP steps (fmaxf is order-free: the
+// result equals the butterfly's, NaN lanes ignored as fmaxf ignores them).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_fmax(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK,
+                                                             0xf, false)));
+}
+__device__ __forceinline__ float wave_fmax_dpp(float v) {
+  v = dpp_fmax<0xB1, 0xf>(v);
+  v = dpp_fmax<0x4E, 0xf>(v);
+  v = dpp_fmax<0x141, 0xf>(v);
+  v = dpp_fmax<0x140, 0xf>(v);
+  v = dpp_fmax<0x142, 0xa>(v);
+  v = dpp_fmax<0x143, 0xc>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // One wave per row. EPL = experts per lane (E <= 64 * EPL).
@@ -86,7 +125,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
-    m = wave_max(m);
+    m = wave_fmax_dpp(m);
     float ex[EPL];
     float s = 0.0f;
 #pragma unroll
@@ -101,27 +140,28 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 #pragma unroll
     for (int j = 0; j < EPL; ++j) psum[j] += ex[j] * inv_s;
 
-    // top-k by (logit desc, id asc); NaN ranks as -inf so a valid id is always found
-    float key[EPL];
+    // top-k by (logit desc, id asc); NaN ranks as -inf so a valid id is always
+    // found. Each pick: the wave max of the unpicked keys, then the lowest id
+    // holding it (ballot over each lane slot in id order).
+    int key[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) key[j] = nan_to_neg_inf(v[j]);
+    for (int j = 0; j < EPL; ++j) key[j] = rank_key(nan_to_neg_inf(v[j]));
     unsigned selmask = 0;
     float p_sel = 0.0f, psum_sel = 0.0f;
     int e_sel = 0;
     for (int k = 0; k < K; ++k) {
-      float bv = -INFINITY;
-      int be = INT_MAX;
+      int lm = INT_MIN;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (lane + 64 * j < E && !((selmask >> j) & 1u)) lm = max(lm, key[j]);
+      const int km = wave_max_dpp(lm);
+      int be = -1;
 #pragma unroll
       for (int j = 0; j < EPL; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && !((selmask >> j) & 1u) && better(key[j], e, bv, be)) { bv = key[j]; be = e; }
+        const unsigned long long hit = __ballot(lane + 64 * j < E && !((selmask >> j) & 1u) && key[j] == km);
+        if (be < 0 && hit != 0ull) be = 64 * j + __builtin_ctzll(hit);
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, kWave);
-        const int oe = __shfl_xor(be, o, kWave);
-        if (better(ov, oe, bv, be)) { bv = ov; be = oe; }
-      }
+      const float bv = key_value(km);
       if ((be & 63) == lane) selmask |= 1u << (be >> 6);
       const float pk = expf(bv - m) * inv_s;
       psum_sel += pk;
