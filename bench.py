@@ -340,7 +340,9 @@ def main() -> int:
     es = 2 if cfg.dtype == torch.bfloat16 else 4
     hbm = {}
     for name, nbytes in (("dispatch", dispatch_bytes(cfg)), ("combine", combine_bytes(cfg)),
-                         ("dispatch_bwd", P * H * es + P * 4 + T * H * es),
+                         # the block's backward hands the router's input gradient to
+                         # the dispatch backward as its addend: one more (T, H) read
+                         ("dispatch_bwd", P * H * es + P * 4 + 2 * T * H * es),
                          ("combine_bwd", T * H * es + 2 * P * H * es + P * (4 + 2 * es))):
         if name in stages:
             gbs = nbytes / (stages[name]["mean_ms"] * 1e-3) / 1e9

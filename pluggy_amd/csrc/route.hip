@@ -76,26 +76,43 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
 // Logits of row `row`: the fixed-order sum of the partial products
 // ((p0 + p1) + p2), plus the optional bias. Partial q of (row, e) sits at
 // parts[row * ldp + q * part_stride + e]. parts may alias logits (nparts 1).
+// fetch_parts issues the loads of a row (up to kMaxParts partials), so the
+// top-k kernel can fetch row r + 4 while it ranks row r; finish_logits sums
+// them in that fixed order and writes the logits.
+constexpr int kMaxParts = 3;
 template <int EPL>
-__device__ __forceinline__ void load_logits(const float* parts, int nparts, int64_t part_stride, int64_t ldp,
-                                            float* logits, const float* bias, int row, int E, int lane,
-                                            float (&v)[EPL]) {
+struct RowParts {
+  float p[kMaxParts][EPL];
+};
+template <int EPL>
+__device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int64_t part_stride, int64_t ldp, int row,
+                                            int E, int lane, RowParts<EPL>& rp) {
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    const int64_t op = (int64_t)row * ldp + e;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) rp.p[q][j] = (e < E && q < nparts) ? parts[q * part_stride + op] : 0.0f;
+  }
+}
+template <int EPL>
+__device__ __forceinline__ void finish_logits(const RowParts<EPL>& rp, int nparts, bool write, float* logits,
+                                              const float* bias, int row, int E, int lane, float (&v)[EPL]) {
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     float x = -INFINITY;
     if (e < E) {
-      const int64_t o = (int64_t)row * E + e;
-      const int64_t op = (int64_t)row * ldp + e;
-      x = parts[op];
-      for (int q = 1; q < nparts; ++q) x += parts[q * part_stride + op];
+      x = rp.p[0][j];
+#pragma unroll
+      for (int q = 1; q < kMaxParts; ++q)
+        if (q < nparts) x += rp.p[q][j];
       if (bias != nullptr) x += bias[e];
-      if (nparts > 1 || bias != nullptr || parts != logits) logits[o] = x;
+      if (write) logits[(int64_t)row * E + e] = x;
     }
     v[j] = x;
   }
 }
-
 template <int EPL, typename TW>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ parts, int nparts,
                                                           int64_t part_stride, int64_t ldp, float* logits,
@@ -119,9 +136,15 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 
   const int row0 = blockIdx.x * rows_per_block;
   const int row1 = min(T, row0 + rows_per_block);
+  const bool write_logits = nparts > 1 || bias != nullptr || parts != logits;
+  RowParts<EPL> cur;
+  if (row0 + wave < row1) fetch_parts<EPL>(parts, nparts, part_stride, ldp, row0 + wave, E, lane, cur);
   for (int row = row0 + wave; row < row1; row += 4) {
+    RowParts<EPL> nxt;
+    if (row + 4 < row1) fetch_parts<EPL>(parts, nparts, part_stride, ldp, row + 4, E, lane, nxt);
     float v[EPL];
-    load_logits<EPL>(parts, nparts, part_stride, ldp, logits, bias, row, E, lane, v);
+    finish_logits<EPL>(cur, nparts, write_logits, logits, bias, row, E, lane, v);
+    cur = nxt;
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
@@ -683,6 +706,7 @@ hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int6
                        int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
                        float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
   if (T == 0) return hipSuccess;
+  if (nparts < 1 || nparts > kMaxParts) return hipErrorInvalidValue;
   const unsigned grid = blocks_for(T, rows_per_block);
   const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \
