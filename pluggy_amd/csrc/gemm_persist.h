@@ -119,8 +119,10 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
 // g + NS - 1, which in a tile's last NS - 1 stages is one of the next tile's
 // first stages. The pipeline therefore stays full across tile boundaries (the
 // next tile's first stages land while this tile's last stages and epilogue
-// run), every stage issues the same DMAs (no branches in the k-loop), and the
-// wait before each barrier is the same vmcnt.
+// run) and every stage issues the same DMAs (no branches in the k-loop). A
+// tile's first NS - 1 stages have fully landed before its stage 0 (the
+// prologue, and each epilogue, waits for them), so stage 0 goes straight to
+// its barrier and every later stage waits for the same vmcnt.
 template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
 __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   setup(bi + nb, nxt);
   // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
   for (int s0 = 0; s0 < NS - 1; ++s0) static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, jc); });
-  wait_stages<D, NS>(NS - 2);
+  wait_vmcnt<0>();  // stages 0 .. NS-2 have landed: a tile's stage 0 never waits
   lds_barrier();
   bf16x8 af[2][MI], bfr[2][NI];
   load_frags(smem, smem + Cfg::A_BYTES, 0, af[0], bfr[0]);
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1);
       });
       PMOE_MARK(11);
-      wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
+      if (kt > 0) wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
       PMOE_MARK(12);
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
       PMOE_MARK(13);
@@ -371,6 +373,13 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1);
     }
     PMOE_MARK(20);
+    // The next tile's first NS - 1 stages were issued during this tile's last
+    // stages; wait for them before the epilogue issues its stores. The vector
+    // memory counter also counts stores, so a wait placed after them (at the
+    // next tile's stage 0) would hold every wave until its stores drained;
+    // here the stores get a whole stage to drain before the next wait.
+    wait_vmcnt<0>();
+    PMOE_MARK(24);
     store_slabs<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
     PMOE_MARK(21);
     gs += nk;
