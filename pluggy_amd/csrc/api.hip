@@ -58,11 +58,24 @@ struct Carver {
 bool dtype_ok(int d) { return d == PMOE_F32 || d == PMOE_BF16; }
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-constexpr int kRouterRowsPerBlock = 16;
 constexpr int kRouterSplitChunk = 512;
 constexpr int64_t kMaxIndex = 0x7fffffffLL;
 
-int64_t router_blocks(int64_t T) { return (T + kRouterRowsPerBlock - 1) / kRouterRowsPerBlock; }
+// Rows per block of the router top-k kernel (4 waves, one row at a time per
+// wave): 16 when there are enough rows to fill the GPU, else one row per wave.
+int router_rows(int64_t T) { return T >= 2048 ? 16 : 4; }
+int64_t router_blocks(int64_t T) { return (T + router_rows(T) - 1) / router_rows(T); }
+// Split-K planes of the bf16-pieces router logits GEMM: its 64-row m-tiles
+// times three piece n-tiles fall short of the 256 CUs when tokens are few
+// (decode), so the reduction over H is split (chunks of at least 256) until
+// there are about 256 tiles; the top-k kernel sums the planes in order.
+int router_logit_splits(int64_t T, int64_t H) {
+  if (T <= 0) return 1;
+  const int64_t tiles = 3 * ((T + 63) / 64);
+  int64_t s = (256 + tiles - 1) / tiles;
+  s = std::min<int64_t>(s, std::min<int64_t>(8, std::max<int64_t>(1, H / 256)));
+  return (int)std::max<int64_t>(1, s);
+}
 int64_t router_splits(int64_t T) { return std::max<int64_t>(1, (T + kRouterSplitChunk - 1) / kRouterSplitChunk); }
 int64_t ldl_of(int64_t E) { return (E + 7) / 8 * 8; }
 
@@ -99,7 +112,7 @@ PMOE_API const char* pmoe_last_error_string(void) { return g_err; }
 PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E) {
   const int64_t nb = router_blocks(T);
   return align_up(nb * E * sizeof(float)) + align_up(nb * E * sizeof(int)) + align_up(nb * sizeof(float)) +
-         align_up(3 * E * H * sizeof(bf16_t)) + align_up(3 * T * E * sizeof(float));
+         align_up(3 * E * H * sizeof(bf16_t)) + align_up(3 * router_logit_splits(T, H) * T * E * sizeof(float));
 }
 
 PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
@@ -123,13 +136,14 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   int* blk_cnt = cv.take<int>(nb * E);
   float* blk_lse2 = cv.take<float>(nb);
   bf16_t* w3 = cv.take<bf16_t>(3 * E * H);
-  float* parts = cv.take<float>(3 * T * E);
+  const int splits = router_logit_splits(T, H);
+  float* parts = cv.take<float>(3 * splits * T * E);
   // Logits in fp32 arithmetic. bf16 x: x is exact in bf16, so splitting an fp32
   // weight into three bf16 pieces makes every MFMA product exact; the three
   // fp32 partials are summed in a fixed order by the top-k kernel.
   const float* lparts = logits;
-  int nparts = 1;
-  int64_t pstride = 0, ldp = E;
+  int nparts = 1, nsplit = 1;
+  int64_t pstride = 0, ldp = E, sstride = 0;
   if (T > 0) {
     if (x_dtype == PMOE_BF16) {
       const bf16_t* wb = (const bf16_t*)weight;
@@ -139,10 +153,13 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
         wb = w3;
         nparts = 3;
       }
-      PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, nparts, t, h, e, parts, s), "router logits GEMM");
+      PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, nparts, t, h, e, splits, parts, s),
+               "router logits GEMM");
       lparts = parts;
       pstride = E;
       ldp = (int64_t)nparts * E;
+      nsplit = splits;
+      sstride = (int64_t)T * nparts * E;
     } else {
       hipError_t st = w_dtype == PMOE_F32
                           ? router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s)
@@ -152,12 +169,12 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
     }
     hipError_t st =
         tw_dtype == PMOE_BF16
-            ? router_topk<bf16_t>(lparts, nparts, pstride, ldp, logits, logit_bias, t, e, k, norm_topk_prob,
-                                  (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
-                                  kRouterRowsPerBlock, s)
-            : router_topk<float>(lparts, nparts, pstride, ldp, logits, logit_bias, t, e, k, norm_topk_prob,
-                                 (float*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
-                                 kRouterRowsPerBlock, s);
+            ? router_topk<bf16_t>(lparts, nparts, pstride, nsplit, sstride, ldp, logits, logit_bias, t, e, k,
+                                  norm_topk_prob, (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum,
+                                  blk_lse2, blk_cnt, router_rows(T), s)
+            : router_topk<float>(lparts, nparts, pstride, nsplit, sstride, ldp, logits, logit_bias, t, e, k,
+                                 norm_topk_prob, (float*)top_weights, top_indices, top_weights_f32, blk_psum,
+                                 blk_lse2, blk_cnt, router_rows(T), s);
     PMOE_TRY(st, "router top-k");
   }
   if (expert_counts || prob_sum || lse_sq_sum)

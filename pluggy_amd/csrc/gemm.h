@@ -21,7 +21,10 @@
 
 namespace pmoe {
 
-enum GroupMode { GM_NONE = 0, GM_ROWS = 1, GM_RED = 2, GM_BATCH = 3 };  // GM_BATCH: shared A, B and C per group
+// GM_BATCH: per-group B and C (strideB, strideC) over a shared A; with
+// split_chunk > 0 group g instead reduces k in [g * split_chunk, ...), a
+// split-K whose partial products land in separate C planes.
+enum GroupMode { GM_NONE = 0, GM_ROWS = 1, GM_RED = 2, GM_BATCH = 3 };
 enum EpiKind { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2 };
 
 template <typename Tc> struct Mfma;

@@ -137,16 +137,24 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
 // Router logits from bf16 pieces of the router weight on the DMA engine: the
 // pieces are stacked along N (npieces*E columns), so the n-tiles of one
 // m-tile share its x rows in L2 and x is read from HBM once; fp32 out,
-// (T, npieces*E) row-major (64x128 blocks, four 32x64 wave tiles).
+// (T, npieces*E) row-major (64x128 blocks, four 32x64 wave tiles). With
+// splits > 1 the reduction over H is split into that many chunks (a multiple
+// of the k tile), each writing its own (T, npieces*E) plane at parts + s * T *
+// npieces * E: few tokens give too few tiles to fill the GPU otherwise.
 hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
-                                     float* parts, hipStream_t s) {
+                                     int splits, float* parts, hipStream_t s) {
   GemmParams p = zero_params();
   p.A = x; p.lda = H;
   p.B = w3; p.ldb = H;
   p.C = parts; p.ldc = npieces * E;
   p.M = T; p.N = npieces * E; p.K = H;
   p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)npieces * E * H * 2;
-  return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_NONE, EPI_STORE, float>(p, s);
+  if (splits <= 1) return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_NONE, EPI_STORE, float>(p, s);
+  constexpr int BK = PMOE_CFG_ROUTER_LOGITS::BK;
+  p.groups = splits;
+  p.split_chunk = ((H + splits - 1) / splits + BK - 1) / BK * BK;
+  p.strideC = (int64_t)T * npieces * E;
+  return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_BATCH, EPI_STORE, float>(p, s);
 }
 
 // Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]

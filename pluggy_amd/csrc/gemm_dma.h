@@ -508,6 +508,10 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
     const int g = slot / mt;
     if (g >= p.groups) return;
     ti.group = g; ti.m0 = (slot % mt) * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
+    if (p.split_chunk > 0) {  // split-K: group g reduces k in [g * chunk, (g + 1) * chunk)
+      ti.k_lo = min(p.K, g * p.split_chunk);
+      ti.k_hi = min(p.K, ti.k_lo + p.split_chunk);
+    }
     B += (int64_t)g * p.strideB;
   } else {
     ti.group = 0; ti.m0 = slot * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;

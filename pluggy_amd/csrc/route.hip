@@ -74,25 +74,34 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
 }
 
 // Logits of row `row`: the fixed-order sum of the partial products
-// ((p0 + p1) + p2), plus the optional bias. Partial q of (row, e) sits at
-// parts[row * ldp + q * part_stride + e]. parts may alias logits (nparts 1).
-// fetch_parts issues the loads of a row (up to kMaxParts partials), so the
-// top-k kernel can fetch row r + 4 while it ranks row r; finish_logits sums
-// them in that fixed order and writes the logits.
+// ((p0 + p1) + p2), plus the optional bias. Partial q of (row, e) is itself
+// the in-order sum of nsplit split-K planes, plane s at parts[s * split_stride
+// + row * ldp + q * part_stride + e]. parts may alias logits (nparts 1,
+// nsplit 1). fetch_parts issues the loads of a row (up to kMaxParts
+// partials), so the top-k kernel can fetch row r + 4 while it ranks row r;
+// finish_logits sums the partials in that fixed order and writes the logits.
 constexpr int kMaxParts = 3;
 template <int EPL>
 struct RowParts {
   float p[kMaxParts][EPL];
 };
 template <int EPL>
-__device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int64_t part_stride, int64_t ldp, int row,
-                                            int E, int lane, RowParts<EPL>& rp) {
+__device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int64_t part_stride, int nsplit,
+                                            int64_t split_stride, int64_t ldp, int row, int E, int lane,
+                                            RowParts<EPL>& rp) {
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     const int64_t op = (int64_t)row * ldp + e;
 #pragma unroll
-    for (int q = 0; q < kMaxParts; ++q) rp.p[q][j] = (e < E && q < nparts) ? parts[q * part_stride + op] : 0.0f;
+    for (int q = 0; q < kMaxParts; ++q) {
+      float v = 0.0f;
+      if (e < E && q < nparts) {
+        v = parts[q * part_stride + op];
+        for (int sp = 1; sp < nsplit; ++sp) v += parts[sp * split_stride + q * part_stride + op];
+      }
+      rp.p[q][j] = v;
+    }
   }
 }
 template <int EPL>
@@ -115,7 +124,8 @@ __device__ __forceinline__ void finish_logits(const RowParts<EPL>& rp, int npart
 }
 template <int EPL, typename TW>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ parts, int nparts,
-                                                          int64_t part_stride, int64_t ldp, float* logits,
+                                                          int64_t part_stride, int nsplit, int64_t split_stride,
+                                                          int64_t ldp, float* logits,
                                                           const float* __restrict__ bias,
                                                           int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
                                                           int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
@@ -136,12 +146,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 
   const int row0 = blockIdx.x * rows_per_block;
   const int row1 = min(T, row0 + rows_per_block);
-  const bool write_logits = nparts > 1 || bias != nullptr || parts != logits;
+  const bool write_logits = nparts > 1 || nsplit > 1 || bias != nullptr || parts != logits;
   RowParts<EPL> cur;
-  if (row0 + wave < row1) fetch_parts<EPL>(parts, nparts, part_stride, ldp, row0 + wave, E, lane, cur);
+  if (row0 + wave < row1)
+    fetch_parts<EPL>(parts, nparts, part_stride, nsplit, split_stride, ldp, row0 + wave, E, lane, cur);
   for (int row = row0 + wave; row < row1; row += 4) {
     RowParts<EPL> nxt;
-    if (row + 4 < row1) fetch_parts<EPL>(parts, nparts, part_stride, ldp, row + 4, E, lane, nxt);
+    if (row + 4 < row1)
+      fetch_parts<EPL>(parts, nparts, part_stride, nsplit, split_stride, ldp, row + 4, E, lane, nxt);
     float v[EPL];
     finish_logits<EPL>(cur, nparts, write_logits, logits, bias, row, E, lane, v);
     cur = nxt;
@@ -701,18 +713,18 @@ hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s) {
 }
 
 template <typename TW>
-hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int64_t ldp, float* logits,
-                       const float* logit_bias,
+hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int nsplit, int64_t split_stride,
+                       int64_t ldp, float* logits, const float* logit_bias,
                        int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
                        float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
   if (T == 0) return hipSuccess;
-  if (nparts < 1 || nparts > kMaxParts) return hipErrorInvalidValue;
+  if (nparts < 1 || nparts > kMaxParts || nsplit < 1) return hipErrorInvalidValue;
   const unsigned grid = blocks_for(T, rows_per_block);
   const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \
   hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, parts, nparts, part_stride,   \
-                     ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, blk_lse2,   \
-                     blk_counts, rows_per_block)
+                     nsplit, split_stride, ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, \
+                     blk_psum, blk_lse2, blk_counts, rows_per_block)
   if (E <= 64) PMOE_TOPK_CASE(1);
   else if (E <= 128) PMOE_TOPK_CASE(2);
   else if (E <= 256) PMOE_TOPK_CASE(4);
@@ -875,10 +887,11 @@ hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* 
   });
 }
 
-template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
-                                        bf16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
-template hipError_t router_topk<float>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
-                                       float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int, int64_t, int64_t, float*, const float*, int,
+                                        int, int, int, bf16_t*, int64_t*, float*, float*, float*, int*, int,
+                                        hipStream_t);
+template hipError_t router_topk<float>(const float*, int, int64_t, int, int64_t, int64_t, float*, const float*, int,
+                                       int, int, int, float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
                                            int, int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
