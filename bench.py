@@ -331,13 +331,34 @@ def main() -> int:
     traffic = profiled_traffic(cfg.name)
     gemm_flops = cfg.gemm_flops()
     tflops = gemm_flops / (ms * 1e-3) / 1e12
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
     # dominant kernel: the grouped-GEMM stage with the largest total time
-    flops_of = {"gate_up": 2.0 * P * H * 2 * I, "down": 2.0 * P * I * H}
     gemm = {n: s for n, s in stages.items() if n in GEMM_STAGES}
     dom = max(gemm, key=lambda n: gemm[n]["total_ms"])
-    dom_flops = flops_of[dom.split("_")[0] if dom.startswith("down") else "gate_up"]
-    dom_tflops = dom_flops / (gemm[dom]["mean_ms"] * 1e-3) / 1e12
-    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    # algorithmic FLOPs and HBM bytes per launch of each expert GEMM: every
+    # operand read once and every output written once; an expert's weights are
+    # read only when it has rows (the last step's routing counts)
+    active = int((mlp.router.last_stats.expert_counts > 0).sum().item())
+    w_gu, w_dn = active * 2 * I * H * es, active * H * I * es
+    gemm_work = {
+        "gate_up_fwd": (2.0 * P * H * 2 * I, w_gu + P * H * es + P * 2 * I * es + P * I * es),
+        "down_fwd": (2.0 * P * I * H, w_dn + P * I * es + P * H * es),
+        "down_dgrad": (2.0 * P * H * I, P * H * es + w_dn + 2 * P * 2 * I * es),
+        "down_wgrad": (2.0 * P * H * I, P * H * es + P * I * es + w_dn),
+        "gate_up_dgrad": (2.0 * P * 2 * I * H, P * 2 * I * es + w_gu + P * H * es),
+        "gate_up_wgrad": (2.0 * P * 2 * I * H, P * 2 * I * es + P * H * es + w_gu),
+    }
+    dom_flops, dom_bytes = gemm_work[dom]
+    dom_s = gemm[dom]["mean_ms"] * 1e-3
+    dom_tflops, dom_gbs = dom_flops / dom_s / 1e12, dom_bytes / dom_s / 1e9
+    # roofline: the bound is whichever peak gives the longer minimum time
+    intensity = dom_flops / dom_bytes
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    mfma_view = {"achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4)}
+    hbm_view = {"achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(dom_gbs / PEAK_HBM_GBS, 4)}
+    bound = "mfma" if intensity >= ridge else "hbm"
     hbm = {}
     for name, nbytes in (("dispatch", dispatch_bytes(cfg)), ("combine", combine_bytes(cfg)),
                          # the block's backward hands the router's input gradient to
@@ -369,10 +390,15 @@ def main() -> int:
         "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
         "gemm_gflop_per_step": round(gemm_flops / 1e9, 1),
         "wall_s": round(wall, 3),
-        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(dom_tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"kernel": dom, "bound": bound, **(mfma_view if bound == "mfma" else hbm_view),
                      "traffic": traffic.get(dom), "traffic_source": traffic.get("_source"),
-                     "flop_per_launch": dom_flops, "mean_ms": round(gemm[dom]["mean_ms"], 4)},
+                     "flop_per_launch": dom_flops, "bytes_per_launch": dom_bytes,
+                     "intensity_flop_per_byte": round(intensity, 1), "ridge_flop_per_byte": round(ridge, 1),
+                     "mfma_view": mfma_view, "hbm_view": hbm_view, "mean_ms": round(gemm[dom]["mean_ms"], 4)},
+        "gemm_stages": {n: {"TFLOP/s": round(f / (gemm[n]["mean_ms"] * 1e-3) / 1e12, 1),
+                            "GB/s": round(b / (gemm[n]["mean_ms"] * 1e-3) / 1e9, 1),
+                            "intensity": round(f / b, 1)}
+                        for n, (f, b) in gemm_work.items() if n in gemm},
         "hbm": hbm,
         "stages_ms": {n: round(s["mean_ms"], 4) for n, s in sorted(stages.items(), key=lambda kv: -kv[1]["total_ms"])},
         "cpu_baseline": None,
