@@ -58,7 +58,9 @@ struct Carver {
 bool dtype_ok(int d) { return d == PMOE_F32 || d == PMOE_BF16; }
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-constexpr int kRouterSplitChunk = 512;
+// Tokens per split-K chunk of the router weight-gradient GEMM (fp32 partials
+// summed in order by reduce_partials).
+constexpr int kRouterSplitChunk = 1024;
 constexpr int64_t kMaxIndex = 0x7fffffffLL;
 
 // Rows per block of the router top-k kernel (4 waves, one row at a time per

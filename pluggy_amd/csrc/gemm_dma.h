@@ -9,7 +9,8 @@
 //    and each slot is refilled as soon as the block has finished reading it,
 //    so NS-1 stages are in flight while one is consumed;
 //  * LDS tiles are unpadded and XOR-swizzled at 16-byte granularity:
-//      k-contiguous tile [r][BK]:  chunk' = chunk ^ ((r >> 1) & 7)  (BK 64)
+//      k-contiguous tile [r][BK]:  chunk' = chunk ^ (r & 15)         (BK 128)
+//                                  chunk' = chunk ^ ((r >> 1) & 7)  (BK 64)
 //                                  chunk' = chunk ^ ((r >> 2) & 3)  (BK 32)
 //      [k][r] tile, R columns:     chunk' = chunk ^ (4 * (k & 3))
 //    so fragment reads of 16 consecutive lanes hit distinct banks;
@@ -53,7 +54,7 @@ struct DmaCfg {
   static constexpr int MAIN_BYTES = NS * STAGE_BYTES;
   static constexpr int SMEM_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % WM == 0 && BN % WN == 0, "tile shape");
-  static_assert(BK == 32 || BK == 64, "k extent of a stage");
+  static_assert(BK == 32 || BK == 64 || BK == 128, "k extent of a stage");
   static_assert(A_INSTR * NW * 1024 == A_BYTES && B_INSTR * NW * 1024 == B_BYTES,
                 "DMA instructions must divide among waves");
   static_assert(NS >= 2 && (NS - 1) * DW < 64, "ring depth");
@@ -142,7 +143,8 @@ __device__ __forceinline__ int swz_t(int k) { return 4 * (k & 3); }
 // fall in 16 distinct 16-byte bank groups.
 template <int BK>
 __device__ __forceinline__ int swz_kc(int r) {
-  if constexpr (BK == 64) return (r >> 1) & 7;
+  if constexpr (BK == 128) return r & 15;
+  else if constexpr (BK == 64) return (r >> 1) & 7;
   else return (r >> 2) & 3;
 }
 

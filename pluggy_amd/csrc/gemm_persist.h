@@ -131,7 +131,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   static_assert(!Cfg::SPLIT, "every wave issues its share of the DMAs");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
-  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && NI % 2 == 0), "SwiGLU epilogue layout");
+  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");
 
   __shared__ __attribute__((aligned(1024))) char smem[L::RING];
   __shared__ __attribute__((aligned(16))) float s_epi[L::EPI_FLOATS];
@@ -182,8 +182,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
 #else
   constexpr int SPREAD = NS == 2 ? 1 : KS - 1;
 #endif
-  constexpr int TOTM = SPREAD * MI * NI;
-  static_assert(SPREAD >= 1 && D <= TOTM, "every DMA of a stage needs an MFMA slot");
+  constexpr int TOTM = SPREAD * MI * NI;  // MFMA slots the DMAs are spread over (several may share one)
+  static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
 
   // What the DMAs of one tile need. nk is padded to at least NS - 1 stages
@@ -400,6 +400,19 @@ hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) 
   hipLaunchKernelGGL((grouped_gemm_persist_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3(grid), dim3(Cfg::NT), 0, s,
                      p);
   return hipGetLastError();
+}
+
+// The two forward expert GEMMs on the persistent kernel (the tile shapes used
+// for few-token batches serve the forward only).
+template <class Cfg>
+hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, bf16_t* C, bf16_t* C2,
+                                   const int32_t* offs, int P, int E, int H, int I, int num_cus, hipStream_t s) {
+  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, C, C2, offs, P, E, H, I);
+  switch (kind) {
+    case EG_GATE_UP_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 // The six expert GEMMs on the persistent kernel.

@@ -105,6 +105,10 @@ GEMM_CASES = [
     (1024, 8, 64, 512, 128, "zipf"),       # skewed: empty experts, heavy experts
     (37, 3, 5, 128, 64, "one"),            # tiny: every group below one tile
     (600, 4, 12, 320, 320, "zipf"),        # partial column tiles on the 64-deep-stage engine
+    # at most 32 rows per expert on average: the forward GEMMs take the few-token
+    # tiles (32 rows x 128 columns, 128-deep stages)
+    (64, 8, 128, 2048, 768, "uniform"),    # the decode layer shape
+    (100, 4, 32, 264, 72, "zipf"),         # ragged k tail, partial column tiles, experts over 32 rows
 ]
 
 
