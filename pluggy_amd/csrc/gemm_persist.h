@@ -114,6 +114,48 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   }
 }
 
+// GM_RED cost model: a tile of group g runs max(ceil(rows_g / BK), NS - 1)
+// k-stages plus an epilogue worth about kRedEpiStages stages (measured: a
+// 256x256 bf16 tile drains in ~3 stage times). s_cost[g] = cost of one tile of
+// each group before g (inclusive scan to groups + 1 entries, computed by wave
+// 0); every thread gets s_cost[groups].
+constexpr int kRedEpiStages = 3;
+template <int BK, int NS>
+__device__ __forceinline__ int red_cost_scan(const int32_t* offs, int groups, int* s_cost) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    int carry = 0;
+    for (int base = 0; base < groups; base += 64) {
+      const int g = base + lane;
+      int c = 0;
+      if (g < groups) {
+        const int rows = offs[g] - (g == 0 ? 0 : offs[g - 1]);
+        c = max((rows + BK - 1) / BK, NS - 1) + kRedEpiStages;
+      }
+      const int inc = wave_incl_scan(c, lane) + carry;
+      if (g < groups) s_cost[g + 1] = inc;
+      carry = __shfl(inc, 63, kWave);
+    }
+    if (lane == 0) s_cost[0] = 0;
+  }
+  __syncthreads();
+  return s_cost[groups];
+}
+
+// First tile (in list order: group-major, tpg tiles per group) whose
+// cumulative cost reaches `target` (0 <= target <= total cost).
+__device__ __forceinline__ int red_cost_tile(const int* s_cost, int groups, int tpg, int64_t target) {
+  int lo = 0, hi = groups - 1;  // the last group g with s_cost[g] * tpg <= target
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)s_cost[mid] * tpg <= target) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t c = s_cost[lo + 1] - s_cost[lo];  // cost of one tile of group lo (> 0)
+  const int64_t k = (target - (int64_t)s_cost[lo] * tpg + c - 1) / c;
+  return lo * tpg + (int)min<int64_t>(k, tpg);
+}
+
 // The block's tiles form one continuous stream of k-stages: stage g lives in
 // ring slot g % NS, and the DMAs issued during stage g fetch stream stage
 // g + NS - 1, which in a tile's last NS - 1 stages is one of the next tile's
@@ -157,12 +199,26 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
   else total = groups * mt_red * ntiles_n;
   // XCD x (blocks with blockIdx % 8 == x) takes a contiguous share of the tiles
-  // and its blocks walk it in a stride of their count.
+  // and its blocks walk it in a stride of their count. GM_ROWS tiles all run
+  // the full reduction, so the shares hold equal tile counts; a GM_RED tile
+  // runs its group's reduction range, so there the shares hold equal cost.
   const int xcd = blockIdx.x & 7;
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
-  const int per = total >> 3, rem = total & 7;
-  const int cnt = per + (xcd < rem ? 1 : 0);
-  const int start = xcd * per + (xcd < rem ? xcd : rem);
+  int cnt, start;
+  if (total == 0) {
+    return;
+  } else if constexpr (GM == GM_RED) {
+    const int tpg = mt_red * ntiles_n;  // tiles per group
+    const int64_t c_all = red_cost_scan<BK, NS>(s_offs, groups, s_scan) * (int64_t)tpg;
+    const int b0 = red_cost_tile(s_scan, groups, tpg, c_all * xcd / 8);
+    const int b1 = xcd == 7 ? total : red_cost_tile(s_scan, groups, tpg, c_all * (xcd + 1) / 8);
+    start = b0;
+    cnt = b1 - b0;
+  } else {
+    const int per = total >> 3, rem = total & 7;
+    cnt = per + (xcd < rem ? 1 : 0);
+    start = xcd * per + (xcd < rem ? xcd : rem);
+  }
   int bi = blockIdx.x >> 3;  // this block's position in the XCD share
   if (bi >= cnt) return;
 
