@@ -120,12 +120,16 @@ def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
 
 
 def _none_if_empty(t: torch.Tensor) -> torch.Tensor | None:
-    """Custom ops cannot return None: an absent gradient travels as an empty tensor."""
-    return None if t.numel() == 0 else t
+    """Custom ops cannot return None: an absent gradient travels as the 1-D
+    empty stand-in of ``_empty_like_none``. A real gradient of an empty batch,
+    e.g. (0, H) for no tokens, keeps its shape and is returned as is."""
+    return None if (t.dim() == 1 and t.numel() == 0) else t
 
 
 def _empty_like_none(ref: torch.Tensor) -> torch.Tensor:
-    """The empty stand-in for an absent output (same dtype and device as ref)."""
+    """The empty stand-in for an absent output (same dtype and device as ref; 1-D,
+    which no gradient of these ops can be: every tensor argument with a
+    gradient has at least two dimensions or a nonzero size)."""
     return ref.new_empty(0)
 
 

@@ -122,6 +122,65 @@ def test_sparse_mlp_module(dtype, norm):
     _check_routing_vs_cpu(x.reshape(B * S, H), Wr, logits.detach().cpu(), K)
 
 
+@pytest.mark.parametrize("E,K", [(4, 4), (1, 1)])
+def test_sparse_mlp_every_expert_and_single_expert(E, K):
+    """K = E (every token uses every expert) and E = K = 1 (a dense SwiGLU MLP) vs fp64 autograd."""
+    pa = _mod()
+    B, S, H, I = 1, 200, 256, 64
+    say(f"sparse MLP edge E={E} K={K}")
+    g = gen(31 + E)
+    x = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    Wr = torch.randn(E, H, generator=g) * 0.05
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    gout = torch.randn(B * S, H, generator=g).to(torch.bfloat16)
+    glog = torch.randn(B * S, E, generator=g) * 0.01
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K, True).to(DEV)
+    with torch.no_grad():
+        mlp.router.weight.copy_(Wr)
+        mlp.experts.gate_up_proj.data = Wgu.to(DEV)
+        mlp.experts.down_proj.data = Wdn.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    out = mlp(xg)
+    logits = mlp.last_router_logits
+    loss = (out.reshape(B * S, H).float() * gout.to(DEV).float()).sum() + (logits * glog.to(DEV)).sum()
+    loss.backward()
+    idx = torch.from_numpy(O.select_topk(logits.detach().cpu(), K))
+    # every expert is selected, in id order of the logits; all counts equal T
+    assert sorted(set(idx.reshape(-1).tolist())) == list(range(E))
+    ref = _ref_block_fp64(x.reshape(B * S, H), Wr, Wgu, Wdn, idx, True, gout, glog)
+    names = ["out", "logits", "dx", "dWr", "dWgu", "dWdn"]
+    got = [out.reshape(B * S, H), logits, xg.grad.reshape(B * S, H), mlp.router.weight.grad,
+           mlp.experts.gate_up_proj.grad, mlp.experts.down_proj.grad]
+    # (E = 1: the routing weight is the constant 1, so the router's gradient comes from the logits
+    # term alone)
+    for n, a, b in zip(names, got, ref):
+        r = rel(a, b)
+        say(f"  {n}: rel={r:.2e} maxabs={max_abs(a, b):.2e}")
+        assert r < 1e-2, n
+    counts = mlp.router.last_stats.expert_counts
+    assert to_np(counts).tolist() == [B * S] * E
+
+
+def test_sparse_mlp_empty_batch():
+    """No tokens: empty output, zero parameter gradients, zero counts (torch's semantics on empty tensors)."""
+    pa = _mod()
+    H, E, K, I = 256, 8, 2, 64
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K, True).to(DEV)
+    with torch.no_grad():
+        mlp.experts.gate_up_proj.data = (torch.randn(E, 2 * I, H, generator=gen(3)) * 0.05).to(DEV)
+        mlp.experts.down_proj.data = (torch.randn(E, H, I, generator=gen(4)) * 0.05).to(DEV)
+    x = torch.zeros(1, 0, H, device=DEV, requires_grad=True)
+    out = mlp(x)
+    assert out.shape == (1, 0, H)
+    assert mlp.last_router_logits.shape == (0, E)
+    out.sum().backward()
+    assert x.grad is not None and x.grad.shape == (1, 0, H)
+    for name, prm in mlp.named_parameters():
+        assert prm.grad is None or torch.count_nonzero(prm.grad).item() == 0, name
+    assert to_np(mlp.router.last_stats.expert_counts).tolist() == [0] * E
+
+
 def _check_routing_vs_cpu(x, Wr, gpu_logits, K, bias=None):
     """GPU ids == oracle ids on the GPU logits (bit-exact); vs CPU logits except near-ties."""
     cpu_logits = torch.nn.functional.linear(x.float(), Wr.float())
