@@ -136,7 +136,7 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
 
 // Router GEMM tile configurations (overridable at build time for sweeps).
 #ifndef PMOE_CFG_ROUTER_LOGITS
-#define PMOE_CFG_ROUTER_LOGITS DmaCfg<64, 128, 32, 64, 2>
+#define PMOE_CFG_ROUTER_LOGITS DmaCfg<64, 64, 32, 32, 2>
 #endif
 #ifndef PMOE_CFG_ROUTER_DX
 #define PMOE_CFG_ROUTER_DX DmaCfg<128, 128, 64, 64, 2>

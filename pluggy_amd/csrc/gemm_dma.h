@@ -640,9 +640,10 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   // MFMAs of a stage before its end-of-stage barrier; the D DMAs of the stage
-  // being refilled are spread evenly among them.
+  // being refilled are spread evenly among them (several follow one MFMA when
+  // a stage has more DMAs than MFMAs).
   constexpr int TOTM = (KS - 1) * MI * NI;
-  static_assert(DW <= TOTM, "every DMA of a stage needs an MFMA slot");
+  static_assert(TOTM >= 1, "the DMAs of a stage need MFMA slots");
 
   // MFMAs of substep KSC (a compile-time constant); with DMA_ST >= 0 the DMAs
   // of stage DMA_ST whose slots fall in this substep follow their MFMA.
