@@ -118,17 +118,21 @@ PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const vo
 
 /* Backward of pmoe_down_proj and the SwiGLU: grad_gate_up_out = SwiGLU'(gate_up_out) *
  * (grad_y . down_proj[e]) and grad_down_proj[e] = grad_y_e^T . mid_e (zeros for
- * an empty expert). Either output may be NULL. */
+ * an empty expert). Either output may be NULL. grad_weight_dtype is grad_down_proj's
+ * dtype: `dtype`, or PMOE_F32 with bf16 operands (the gradient of an fp32 master
+ * weight that the forward cast to bf16, written without a separate cast). */
 PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
                                      const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
                                      int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
-                                     void* stream);
+                                     int grad_weight_dtype, void* stream);
 
 /* Backward of the gate_up GEMM: grad_x_perm = grad_gate_up_out . gate_up_proj[e];
- * grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e. Either output may be NULL. */
+ * grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e. Either output may be NULL.
+ * grad_weight_dtype is grad_gate_up_proj's dtype, as for pmoe_down_proj_backward. */
 PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
                                    const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
-                                   void* grad_x_perm, void* grad_gate_up_proj, void* stream);
+                                   void* grad_x_perm, void* grad_gate_up_proj, int grad_weight_dtype,
+                                   void* stream);
 
 /* Backward of pmoe_dispatch: grad_hidden[t] = grad_hidden_add[t] + sum_k
  * grad_x_perm[inv_pos[t*K+k]] (fp32 sum, k ascending; grad_hidden_add (T,H)

@@ -40,8 +40,8 @@ SIGNATURES = {
     "pmoe_down_proj": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P]),
     "pmoe_combine": (_INT, [_P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),
     "pmoe_combine_backward": (_INT, [_P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P]),
-    "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
-    "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _INT, _P]),
+    "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _INT, _P]),
     "pmoe_dispatch_backward": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P]),
     "pmoe_rmsnorm_forward": (_INT, [_P, _INT, _P, _F32, _I64, _I64, _P, _INT, _P, _P]),
     "pmoe_combine_residual": (_INT, [_P, _P, _INT, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),

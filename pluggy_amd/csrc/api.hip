@@ -354,9 +354,11 @@ PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_
 PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
                                      const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
                                      int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
-                                     void* stream) {
+                                     int grad_weight_dtype, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+               "down_proj_backward: grad_down_proj dtype must be the operands' or fp32");
   PMOE_REQUIRE(offs && (P == 0 || grad_y), "down_proj_backward: null tensor");
   hipStream_t s = as_stream(stream);
   const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
@@ -372,10 +374,13 @@ PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const 
   }
   if (grad_down_proj) {
     PMOE_REQUIRE(P == 0 || mid, "down_proj_backward: null mid");
-    hipError_t st = dtype == PMOE_BF16 ? down_wgrad<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h,
-                                                            i, (bf16_t*)grad_down_proj, s)
-                                       : down_wgrad<float>((const float*)grad_y, (const float*)mid, offs, p, e, h, i,
-                                                           (float*)grad_down_proj, s);
+    hipError_t st =
+        dtype == PMOE_F32
+            ? down_wgrad<float>((const float*)grad_y, (const float*)mid, offs, p, e, h, i, (float*)grad_down_proj, s)
+        : grad_weight_dtype == PMOE_F32
+            ? down_wgrad_f32((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h, i, (float*)grad_down_proj, s)
+            : down_wgrad<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h, i,
+                                 (bf16_t*)grad_down_proj, s);
     PMOE_TRY(st, "down wgrad");
   }
   return PMOE_OK;
@@ -383,9 +388,12 @@ PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const 
 
 PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
                                    const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
-                                   void* grad_x_perm, void* grad_gate_up_proj, void* stream) {
+                                   void* grad_x_perm, void* grad_gate_up_proj, int grad_weight_dtype,
+                                   void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+               "gate_up_backward: grad_gate_up_proj dtype must be the operands' or fp32");
   PMOE_REQUIRE(offs && (P == 0 || grad_gate_up_out), "gate_up_backward: null tensor");
   hipStream_t s = as_stream(stream);
   const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
@@ -400,11 +408,13 @@ PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_p
   }
   if (grad_gate_up_proj) {
     PMOE_REQUIRE(P == 0 || x_perm, "gate_up_backward: null x_perm");
-    hipError_t st = dtype == PMOE_BF16
-                        ? gate_up_wgrad<bf16_t>((const bf16_t*)grad_gate_up_out, (const bf16_t*)x_perm, offs, p, e, h,
-                                                i, (bf16_t*)grad_gate_up_proj, s)
-                        : gate_up_wgrad<float>((const float*)grad_gate_up_out, (const float*)x_perm, offs, p, e, h, i,
-                                               (float*)grad_gate_up_proj, s);
+    const bf16_t* gb = (const bf16_t*)grad_gate_up_out;
+    const bf16_t* xb = (const bf16_t*)x_perm;
+    hipError_t st = dtype == PMOE_F32 ? gate_up_wgrad<float>((const float*)grad_gate_up_out, (const float*)x_perm,
+                                                             offs, p, e, h, i, (float*)grad_gate_up_proj, s)
+                    : grad_weight_dtype == PMOE_F32
+                        ? gate_up_wgrad_f32(gb, xb, offs, p, e, h, i, (float*)grad_gate_up_proj, s)
+                        : gate_up_wgrad<bf16_t>(gb, xb, offs, p, e, h, i, (bf16_t*)grad_gate_up_proj, s);
     PMOE_TRY(st, "gate_up wgrad");
   }
   return PMOE_OK;
@@ -527,13 +537,13 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
   // 2. down GEMM backward (dgrad fused with SwiGLU backward, then wgrad)
   void* ggu = (grad_hidden || grad_gate_up_proj) ? grad_gu : nullptr;
   if (int rc = pmoe_down_proj_backward(grad_y, mid, gate_up_out, down_proj, offs, dtype, P, E, H, I, ggu,
-                                       grad_down_proj, stream))
+                                       grad_down_proj, dtype, stream))
     return rc;
   // 3. gate_up GEMM backward; grad_x_perm reuses grad_y (consumed above, same stream)
   void* gxp = grad_hidden ? grad_y : nullptr;
   if (ggu) {
     if (int rc = pmoe_gate_up_backward(grad_gu, x_perm, gate_up_proj, offs, dtype, P, E, H, I, gxp,
-                                       grad_gate_up_proj, stream))
+                                       grad_gate_up_proj, dtype, stream))
       return rc;
   }
   // 4. dispatch backward

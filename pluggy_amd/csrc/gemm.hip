@@ -124,6 +124,17 @@ hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int
   return run<T>(EG_GATE_UP_WGRAD, dgu, x_perm, nullptr, dw_gu, nullptr, offs, P, E, H, I, s);
 }
 
+hipError_t down_wgrad_f32(const bf16_t* dy, const bf16_t* mid, const int32_t* offs, int P, int E, int H, int I,
+                          float* dw_dn, hipStream_t s) {
+  return expert_wgrad_persist_f32<PMOE_CFG_DOWN_WGRAD>(EG_DOWN_WGRAD, dy, mid, dw_dn, offs, P, E, H, I, num_cus(), s);
+}
+
+hipError_t gate_up_wgrad_f32(const bf16_t* dgu, const bf16_t* x_perm, const int32_t* offs, int P, int E, int H,
+                             int I, float* dw_gu, hipStream_t s) {
+  return expert_wgrad_persist_f32<PMOE_CFG_GATE_UP_WGRAD>(EG_GATE_UP_WGRAD, dgu, x_perm, dw_gu, offs, P, E, H, I,
+                                                          num_cus(), s);
+}
+
 template <typename TX, typename TW>
 hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, float* logits, hipStream_t s) {
   GemmParams p = zero_params();

@@ -471,6 +471,20 @@ hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, b
   return hipErrorInvalidValue;
 }
 
+// The two weight-gradient GEMMs with fp32 output (bf16 operands, gradients of
+// fp32 master weights): the accumulators are stored unrounded.
+template <class Cfg>
+hipError_t expert_wgrad_persist_f32(int kind, const bf16_t* A, const bf16_t* B, float* C, const int32_t* offs,
+                                    int P, int E, int H, int I, int num_cus, hipStream_t s) {
+  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, nullptr, nullptr, offs, P, E, H, I);
+  p.C = C;
+  switch (kind) {
+    case EG_DOWN_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, float>(p, num_cus, s);
+    case EG_GATE_UP_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, float>(p, num_cus, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 // The six expert GEMMs on the persistent kernel.
 template <class Cfg>
 hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,

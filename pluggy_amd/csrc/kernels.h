@@ -31,6 +31,11 @@ hipError_t gate_up_dgrad(const T* dgu, const T* w_gu, const int32_t* offs, int P
 template <typename T>
 hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int P, int E, int H, int I, T* dw_gu,
                          hipStream_t s);
+// The two weight gradients from bf16 operands, stored as fp32 (fp32 master weights).
+hipError_t down_wgrad_f32(const bf16_t* dy, const bf16_t* mid, const int32_t* offs, int P, int E, int H, int I,
+                          float* dw_dn, hipStream_t s);
+hipError_t gate_up_wgrad_f32(const bf16_t* dgu, const bf16_t* x_perm, const int32_t* offs, int P, int E, int H,
+                             int I, float* dw_gu, hipStream_t s);
 
 // ---- router GEMMs in fp32 arithmetic (gemm.hip). TX: x dtype, TW: router weight dtype.
 template <typename TX, typename TW>

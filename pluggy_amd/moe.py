@@ -116,6 +116,34 @@ def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
     return None
 
 
+def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """-> (the weight in the kernels' dtype, its fp32 master or None).
+
+    An fp32 master weight that feeds bf16 kernels (autocast training) is cast
+    outside autograd and passed to the op beside its bf16 copy. The op's
+    backward then writes the master's gradient in fp32 straight from the
+    weight-gradient GEMM, with no bf16 gradient and no cast kernel between.
+    Otherwise the cast, if any, is an ordinary differentiable one.
+    """
+    if w.dtype == torch.float32 and dt == torch.bfloat16 and w.requires_grad and torch.is_grad_enabled():
+        with torch.no_grad():
+            return w.detach().to(dt).contiguous(), w
+    return w.to(dtype=dt).contiguous(), None
+
+
+def _needs(ctx, n: int) -> tuple[bool, ...]:
+    """ctx.needs_input_grad over all n schema arguments: the dispatcher drops
+    trailing arguments left at their defaults (absent masters), and those need
+    no gradient."""
+    need = tuple(ctx.needs_input_grad)
+    return need + (False,) * (n - len(need))
+
+
+def _f32_wgrads(gate_up_master, down_master) -> list[bool]:
+    """Which weight gradients the backward writes in fp32: those of fp32 masters."""
+    return [m is not None and m.dtype == torch.float32 for m in (gate_up_master, down_master)]
+
+
 # ------------------------------------------------------------------ router
 
 
@@ -247,13 +275,17 @@ def _ffn_fake_saved(hidden, K, E, I):
 
 @torch.library.custom_op("pmoe::expert_ffn_fwd", mutates_args=(),
                          schema="(Tensor hidden, Tensor top_indices, Tensor top_weights, Tensor gate_up_proj, "
-                                "Tensor down_proj) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
-def _expert_ffn_fwd(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+                                "Tensor down_proj, Tensor? gate_up_master=None, Tensor? down_master=None) -> "
+                                "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _expert_ffn_fwd(hidden, top_indices, top_weights, gate_up_proj, down_proj, gate_up_master=None,
+                    down_master=None):
+    """The masters, when given, are the differentiable fp32 weights whose bf16
+    copies gate_up_proj / down_proj are; the forward does not read them."""
     return _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj)
 
 
 @_expert_ffn_fwd.register_fake
-def _(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+def _(hidden, top_indices, top_weights, gate_up_proj, down_proj, gate_up_master=None, down_master=None):
     E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
     return (torch.empty_like(hidden),) + _ffn_fake_saved(hidden, top_indices.shape[1], E, I2 // 2)
 
@@ -271,13 +303,15 @@ def _(grad_out, y, top_weights, inv_pos):
     return torch.empty_like(y), torch.empty_like(top_weights)
 
 
-def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_rows, need_gu, need_dn, reduce_rows):
+def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_rows, need_gu, need_dn, reduce_rows,
+                           f32_wgrads=(False, False)):
     """The expert GEMMs' backward from grad_y. With need_rows, the (P, H) input
     gradient of the dispatched rows goes to ``reduce_rows`` (which sums each
     token's K rows) before the gate_up weight gradient is computed, so it is
-    freed early. -> (reduce_rows result or None, grad_gate_up or None,
-    grad_down or None)."""
+    freed early. f32_wgrads (gate_up, down): write that weight gradient in fp32.
+    -> (reduce_rows result or None, grad_gate_up or None, grad_down or None)."""
     E = gate_up.shape[0]
+    f32 = torch.float32
     reduced = g_gu_w = g_dn_w = None
     g_gu = None
     if need_rows or need_gu:
@@ -285,7 +319,7 @@ def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_ro
             g_gu = ops.down_proj_dgrad(grad_y, gu, down, offs)
     if need_dn:
         with _stage("down_wgrad"):
-            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E)
+            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E, f32 if f32_wgrads[1] else None)
     if need_rows:
         with _stage("gate_up_dgrad"):
             g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
@@ -293,38 +327,46 @@ def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_ro
         del g_xp
     if need_gu:
         with _stage("gate_up_wgrad"):
-            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E)
+            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E, f32 if f32_wgrads[0] else None)
     return reduced, g_gu_w, g_dn_w
 
 
 @torch.library.custom_op("pmoe::expert_bwd", mutates_args=(),
                          schema="(Tensor grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
                                 "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_hidden_add, int tokens, int top_k, "
-                                "bool[] needs) -> (Tensor, Tensor, Tensor)")
-def _expert_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs):
+                                "bool[] needs, bool[] f32_wgrads) -> (Tensor, Tensor, Tensor)")
+def _expert_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs,
+                f32_wgrads):
     """The expert GEMMs' backward from grad_y: -> grad_hidden (+ grad_hidden_add),
     grad_gate_up, grad_down; an empty tensor where needs[i] is false (needs:
-    hidden, gate_up, down)."""
+    hidden, gate_up, down). f32_wgrads (gate_up, down): that weight gradient
+    is fp32 (an fp32 master's) instead of the operands' dtype."""
     def reduce_rows(g_xp):
         with _stage("dispatch_bwd"):
             return ops.dispatch_backward(g_xp, inv_pos, tokens, top_k, add=grad_hidden_add)
 
     g_hidden, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, needs[0],
-                                                      needs[1], needs[2], reduce_rows)
+                                                      needs[1], needs[2], reduce_rows, f32_wgrads)
     e = _empty_like_none
     return (g_hidden if g_hidden is not None else e(grad_y), g_gu_w if g_gu_w is not None else e(gate_up),
             g_dn_w if g_dn_w is not None else e(down))
 
 
+def _wgrad_fake(w, f32):
+    return torch.empty_like(w, dtype=torch.float32 if f32 else w.dtype)
+
+
 @_expert_bwd.register_fake
-def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs):
+def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs, f32_wgrads):
     e = _empty_like_none
     return (grad_y.new_empty(tokens, grad_y.shape[1]) if needs[0] else e(grad_y),
-            torch.empty_like(gate_up) if needs[1] else e(gate_up), torch.empty_like(down) if needs[2] else e(down))
+            _wgrad_fake(gate_up, f32_wgrads[0]) if needs[1] else e(gate_up),
+            _wgrad_fake(down, f32_wgrads[1]) if needs[2] else e(down))
 
 
 def _ffn_setup(ctx, inputs, output):
-    hidden, top_indices, top_weights, gate_up_proj, down_proj = inputs
+    hidden, top_indices, top_weights, gate_up_proj, down_proj, gate_up_master, down_master = inputs
+    ctx.f32_wgrads = _f32_wgrads(gate_up_master, down_master)
     out, offs, inv_pos, x_perm, gu, mid, y = output
     ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
     ctx.dims = (hidden.shape[0], top_indices.shape[1])
@@ -334,22 +376,24 @@ def _ffn_setup(ctx, inputs, output):
 
 def _ffn_backward(ctx, grad_out, *_saved_grads):
     if grad_out is None:
-        return None, None, None, None, None
+        return (None,) * 7
     top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
     T, K = ctx.dims
-    need = ctx.needs_input_grad
+    need = _needs(ctx, 7)  # hidden, indices, weights, gate_up, down, gate_up_master, down_master
+    need_gu, need_dn = need[3] or need[5], need[4] or need[6]
     grad_out = grad_out.contiguous()
     if grad_out.dtype != x_perm.dtype:
         grad_out = grad_out.to(x_perm.dtype)
     g_y, g_w = torch.ops.pmoe.combine_bwd(grad_out, y, top_w, inv_pos)
     g_hidden = g_gu_w = g_dn_w = None
-    if need[0] or need[3] or need[4]:
+    if need[0] or need_gu or need_dn:
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid,
                                                              None, T, K,
-                                                             [bool(need[0]), bool(need[3]), bool(need[4])])
-    return (_none_if_empty(g_hidden) if g_hidden is not None else None, None, (g_w if need[2] else None),
-            _none_if_empty(g_gu_w) if g_gu_w is not None else None,
-            _none_if_empty(g_dn_w) if g_dn_w is not None else None)
+                                                             [bool(need[0]), bool(need_gu), bool(need_dn)],
+                                                             ctx.f32_wgrads)
+        g_hidden, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_hidden, g_gu_w, g_dn_w))
+    return (g_hidden if need[0] else None, None, (g_w if need[2] else None), g_gu_w if need[3] else None,
+            g_dn_w if need[4] else None, g_gu_w if need[5] else None, g_dn_w if need[6] else None)
 
 
 _expert_ffn_fwd.register_autograd(_ffn_backward, setup_context=_ffn_setup)
@@ -360,13 +404,17 @@ _expert_ffn_fwd.register_autograd(_ffn_backward, setup_context=_ffn_setup)
 
 @torch.library.custom_op("pmoe::sparse_moe_fwd", mutates_args=(),
                          schema="(Tensor x, Tensor router_weight, Tensor gate_up_proj, Tensor down_proj, int top_k, "
-                                "bool norm_topk_prob, Tensor? logit_bias) -> (Tensor, Tensor, Tensor, Tensor, Tensor, "
+                                "bool norm_topk_prob, Tensor? logit_bias, Tensor? gate_up_master=None, "
+                                "Tensor? down_master=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, "
                                 "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
-def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias,
+                    gate_up_master=None, down_master=None):
     """Router + dropless experts (Qwen3MoeSparseMLP.forward) as one op.
 
     -> out, router_logits, counts, prob_sum, lse_sq_sum, then what the backward
-    reads: top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y.
+    reads: top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y. The
+    masters, when given, are the differentiable fp32 weights whose bf16 copies
+    gate_up_proj / down_proj are (their gradients are written in fp32).
     """
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
@@ -376,7 +424,8 @@ def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_
 
 
 @_sparse_moe_fwd.register_fake
-def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gate_up_master=None,
+      down_master=None):
     T, E, K = x.shape[0], router_weight.shape[0], top_k
     I = gate_up_proj.shape[1] // 2
     f32 = torch.float32
@@ -387,8 +436,9 @@ def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bi
 
 
 def _sparse_setup(ctx, inputs, output):
-    x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias = inputs
+    x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master, dn_master = inputs
     (out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y) = output
+    ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
     ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, top_w, gate_up_proj, down_proj, offs, inv_pos,
                           x_perm, gu, mid, y)
     ctx.norm_topk_prob = bool(norm_topk_prob)
@@ -404,9 +454,10 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     (x, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
      y) = ctx.saved_tensors
     T, K = ctx.dims
-    need = ctx.needs_input_grad
+    need = _needs(ctx, 9)  # x, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
+    need_gu, need_dn = need[2] or need[7], need[3] or need[8]
     if g_out is None and g_logits is None:
-        return None, None, None, None, None, None, None
+        return (None,) * 9
     if g_logits is not None:
         g_logits = g_logits.float().contiguous()
     g_x = g_rw = g_gu_w = g_dn_w = None
@@ -420,16 +471,17 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     if need[0] or need[1]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(x, rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
-    if g_y is not None and (need[0] or need[2] or need[3]):
+    if g_y is not None and (need[0] or need_gu or need_dn):
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
             g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if need[0] else None, T, K,
-            [bool(need[0]), bool(need[2]), bool(need[3])])
+            [bool(need[0]), bool(need_gu), bool(need_dn)], ctx.f32_wgrads)
         g_x = _none_if_empty(g_hidden)
         g_gu_w = _none_if_empty(g_gu_w)
         g_dn_w = _none_if_empty(g_dn_w)
     elif need[0]:
         g_x = gx_router
-    return (g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w, g_dn_w, None, None, None
+    return ((g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w if need[2] else None,
+            g_dn_w if need[3] else None, None, None, None, g_gu_w if need[7] else None, g_dn_w if need[8] else None)
 
 
 _sparse_moe_fwd.register_autograd(_sparse_backward, setup_context=_sparse_setup)
@@ -455,12 +507,12 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     rw = (router_weight if amp is None else router_weight.to(amp)).contiguous()
     if rw.dtype not in (torch.float32, torch.bfloat16):
         rw = rw.float()
-    gu = gate_up_proj.to(dtype=dt).contiguous()
-    dn = down_proj.to(dtype=dt).contiguous()
+    gu, gu_master = _compute_weight(gate_up_proj, dt)
+    dn, dn_master = _compute_weight(down_proj, dt)
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
-                                                                     logit_bias)[:5]
+                                                                     logit_bias, gu_master, dn_master)[:5]
     return out.to(hidden.dtype), logits, RouterStats(counts, psum, lse2, x.shape[0])
 
 
@@ -489,11 +541,11 @@ def moe_expert_ffn(
     require_gpu(hidden, top_indices, top_weights, gate_up_proj, down_proj)
     amp = _amp_dtype(hidden)
     dt = hidden.dtype if amp is None else amp
-    gu = gate_up_proj.to(dtype=dt).contiguous()
-    dn = down_proj.to(dtype=dt).contiguous()
+    gu, gu_master = _compute_weight(gate_up_proj, dt)
+    dn, dn_master = _compute_weight(down_proj, dt)
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
     out = torch.ops.pmoe.expert_ffn_fwd(hidden.to(dt).contiguous(), top_indices.to(torch.int64).contiguous(),
-                                        tw.contiguous(), gu, dn)[0]
+                                        tw.contiguous(), gu, dn, gu_master, dn_master)[0]
     return out.to(hidden.dtype)
 
 
@@ -502,17 +554,19 @@ def moe_expert_ffn(
 
 @torch.library.custom_op("pmoe::moe_sublayer_fwd", mutates_args=(),
                          schema="(Tensor x, Tensor norm_weight, float eps, Tensor router_weight, Tensor gate_up_proj, "
-                                "Tensor down_proj, int top_k, bool norm_topk_prob, Tensor? logit_bias) -> (Tensor, "
+                                "Tensor down_proj, int top_k, bool norm_topk_prob, Tensor? logit_bias, "
+                                "Tensor? gate_up_master=None, Tensor? down_master=None) -> (Tensor, "
                                 "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
                                 "Tensor, Tensor, Tensor, Tensor, Tensor)")
 def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
-                      logit_bias):
+                      logit_bias, gate_up_master=None, down_master=None):
     """x + SparseMLP(RMSNorm(x)) with the norm and the residual add in the row kernels.
 
     The kernels compute in gate_up_proj's dtype; x is the residual stream (its
     own dtype). -> out, router_logits, counts, prob_sum, lse_sq_sum, then what
     the backward reads: normed, rstd, top_i, top_w32, top_w, offs, inv_pos,
-    x_perm, gu, mid, y.
+    x_perm, gu, mid, y. The masters, when given, are the differentiable fp32
+    weights whose bf16 copies gate_up_proj / down_proj are.
     """
     with _stage("rmsnorm"):
         normed, rstd = ops.rmsnorm_forward(x, norm_weight, eps, gate_up_proj.dtype)
@@ -533,7 +587,8 @@ def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_pro
 
 
 @_moe_sublayer_fwd.register_fake
-def _(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias):
+def _(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias,
+      gate_up_master=None, down_master=None):
     T, H = x.shape
     E, K, I = router_weight.shape[0], top_k, gate_up_proj.shape[1] // 2
     cdt = gate_up_proj.dtype
@@ -562,13 +617,14 @@ def _(grad_out, y, top_weights, inv_pos):
 @torch.library.custom_op("pmoe::sublayer_bwd", mutates_args=(),
                          schema="(Tensor? grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
                                 "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_normed_add, Tensor x, "
-                                "Tensor norm_weight, Tensor rstd, Tensor? grad_residual, int top_k, bool[] needs) -> "
-                                "(Tensor, Tensor, Tensor, Tensor)")
+                                "Tensor norm_weight, Tensor rstd, Tensor? grad_residual, int top_k, bool[] needs, "
+                                "bool[] f32_wgrads) -> (Tensor, Tensor, Tensor, Tensor)")
 def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd,
-                  grad_residual, top_k, needs):
+                  grad_residual, top_k, needs, f32_wgrads):
     """Expert GEMM backward, then the dispatch, RMSNorm and residual backward in
     one row pass: -> grad_x, grad_norm_weight, grad_gate_up, grad_down (empty
-    where needs[i] is false; needs: x, norm_weight, gate_up, down)."""
+    where needs[i] is false; needs: x, norm_weight, gate_up, down). f32_wgrads
+    (gate_up, down): that weight gradient is fp32 (an fp32 master's)."""
     need_x = needs[0] or needs[1]
 
     def reduce_rows(g_xp):
@@ -579,7 +635,7 @@ def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_no
     reduced = g_gu_w = g_dn_w = None
     if grad_y is not None:
         reduced, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_x,
-                                                         needs[2], needs[3], reduce_rows)
+                                                         needs[2], needs[3], reduce_rows, f32_wgrads)
     elif need_x:
         reduced = reduce_rows(None)
     g_x, g_nw = reduced if reduced is not None else (None, None)
@@ -590,14 +646,17 @@ def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_no
 
 @_sublayer_bwd.register_fake
 def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd, grad_residual,
-      top_k, needs):
+      top_k, needs, f32_wgrads):
     e = _empty_like_none
     return (torch.empty_like(x) if needs[0] else e(x), torch.empty_like(norm_weight) if needs[1] else e(norm_weight),
-            torch.empty_like(gate_up) if needs[2] else e(gate_up), torch.empty_like(down) if needs[3] else e(down))
+            _wgrad_fake(gate_up, f32_wgrads[0]) if needs[2] else e(gate_up),
+            _wgrad_fake(down, f32_wgrads[1]) if needs[3] else e(down))
 
 
 def _sublayer_setup(ctx, inputs, output):
-    x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias = inputs
+    (x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master,
+     dn_master) = inputs
+    ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
     (out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid,
      y) = output
     ctx.save_for_backward(x, norm_weight, rstd, normed, router_weight, logits, top_i, top_w32, top_w, gate_up_proj,
@@ -615,8 +674,10 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
     inside the one row pass of the dispatch backward."""
     (x, nw, rstd, normed, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
      y) = ctx.saved_tensors
-    need = ctx.needs_input_grad  # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias
-    nones = (None,) * 9
+    # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
+    need = _needs(ctx, 11)
+    need_gu, need_dn = need[4] or need[9], need[5] or need[10]
+    nones = (None,) * 11
     if g_out is None and g_logits is None:
         return nones
     if g_logits is not None:
@@ -629,15 +690,16 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
     if need[0] or need[1] or need[3]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(normed, rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
-    needs = [bool(need[0]), bool(need[1]), bool(need[4]) and g_y is not None, bool(need[5]) and g_y is not None]
+    needs = [bool(need[0]), bool(need[1]), bool(need_gu) and g_y is not None, bool(need_dn) and g_y is not None]
     g_x = g_nw = g_gu_w = g_dn_w = None
     if any(needs):
         g_x, g_nw, g_gu_w, g_dn_w = torch.ops.pmoe.sublayer_bwd(
             g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if (need[0] or need[1]) else None, x, nw,
-            rstd, g_out if need[0] else None, ctx.top_k, needs)
+            rstd, g_out if need[0] else None, ctx.top_k, needs, ctx.f32_wgrads)
         g_x, g_nw, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_x, g_nw, g_gu_w, g_dn_w))
     return (g_x if need[0] else None, g_nw if need[1] else None, None, g_rw if need[3] else None,
-            g_gu_w if need[4] else None, g_dn_w if need[5] else None, None, None, None)
+            g_gu_w if need[4] else None, g_dn_w if need[5] else None, None, None, None, g_gu_w if need[9] else None,
+            g_dn_w if need[10] else None)
 
 
 _moe_sublayer_fwd.register_autograd(_sublayer_backward, setup_context=_sublayer_setup)
@@ -672,11 +734,12 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     rw = r.weight if amp is None else r.weight.to(amp)
     if rw.dtype not in (torch.float32, torch.bfloat16):
         rw = rw.float()
-    gu = mlp.experts.gate_up_proj.to(dtype=cdt).contiguous()
-    dn = mlp.experts.down_proj.to(dtype=cdt).contiguous()
+    gu, gu_master = _compute_weight(mlp.experts.gate_up_proj, cdt)
+    dn, dn_master = _compute_weight(mlp.experts.down_proj, cdt)
     bias = r.logit_bias.float().contiguous() if r.logit_bias is not None else None
     out, logits, counts, psum, lse2 = torch.ops.pmoe.moe_sublayer_fwd(
-        flat, nw.contiguous(), float(eps), rw.contiguous(), gu, dn, int(r.top_k), bool(r.norm_topk_prob), bias)[:5]
+        flat, nw.contiguous(), float(eps), rw.contiguous(), gu, dn, int(r.top_k), bool(r.norm_topk_prob), bias,
+        gu_master, dn_master)[:5]
     r.last_stats = RouterStats(counts, psum, lse2, flat.shape[0])
     mlp.last_router_logits = logits
     return out.reshape(B, S, H)

@@ -121,7 +121,7 @@ def down_proj_backward(grad_y, mid, gate_up_out, down_proj_w, offs):
     ggu = torch.empty(P, 2 * I, dtype=grad_y.dtype, device=grad_y.device)
     gdn = torch.empty_like(down_proj_w)
     call("pmoe_down_proj_backward", ptr(grad_y), ptr(mid), ptr(gate_up_out), ptr(down_proj_w), ptr(offs),
-         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), ptr(gdn), stream_of(grad_y))
+         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), ptr(gdn), dtype_code(gdn.dtype), stream_of(grad_y))
     return ggu, gdn
 
 
@@ -131,17 +131,18 @@ def down_proj_dgrad(grad_y, gate_up_out, down_proj_w, offs):
     P = grad_y.shape[0]
     ggu = torch.empty(P, 2 * I, dtype=grad_y.dtype, device=grad_y.device)
     call("pmoe_down_proj_backward", ptr(grad_y), None, ptr(gate_up_out), ptr(down_proj_w), ptr(offs),
-         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), None, stream_of(grad_y))
+         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), None, dtype_code(grad_y.dtype), stream_of(grad_y))
     return ggu
 
 
-def down_proj_wgrad(grad_y, mid, offs, num_experts: int):
-    """grad_down_proj[e] = grad_y_e^T . mid_e (one kernel)."""
+def down_proj_wgrad(grad_y, mid, offs, num_experts: int, out_dtype=None):
+    """grad_down_proj[e] = grad_y_e^T . mid_e (one kernel), in `out_dtype`
+    (default the operands'; fp32 from bf16 operands for an fp32 master weight)."""
     P, H = grad_y.shape
     I = mid.shape[1]
-    gdn = torch.empty(num_experts, H, I, dtype=grad_y.dtype, device=grad_y.device)
+    gdn = torch.empty(num_experts, H, I, dtype=out_dtype or grad_y.dtype, device=grad_y.device)
     call("pmoe_down_proj_backward", ptr(grad_y), ptr(mid), None, None, ptr(offs), dtype_code(grad_y.dtype), P,
-         num_experts, H, I, None, ptr(gdn), stream_of(grad_y))
+         num_experts, H, I, None, ptr(gdn), dtype_code(gdn.dtype), stream_of(grad_y))
     return gdn
 
 
@@ -151,17 +152,18 @@ def gate_up_dgrad(grad_gate_up_out, gate_up_proj, offs):
     P = grad_gate_up_out.shape[0]
     gx = torch.empty(P, H, dtype=grad_gate_up_out.dtype, device=grad_gate_up_out.device)
     call("pmoe_gate_up_backward", ptr(grad_gate_up_out), None, ptr(gate_up_proj), ptr(offs),
-         dtype_code(gx.dtype), P, E, H, I, ptr(gx), None, stream_of(gx))
+         dtype_code(gx.dtype), P, E, H, I, ptr(gx), None, dtype_code(gx.dtype), stream_of(gx))
     return gx
 
 
-def gate_up_wgrad(grad_gate_up_out, x_perm, offs, num_experts: int):
-    """grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e (one kernel)."""
+def gate_up_wgrad(grad_gate_up_out, x_perm, offs, num_experts: int, out_dtype=None):
+    """grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e (one kernel), in
+    `out_dtype` (default the operands'; fp32 from bf16 operands for an fp32 master)."""
     P, H = x_perm.shape
     I = grad_gate_up_out.shape[1] // 2
-    gw = torch.empty(num_experts, 2 * I, H, dtype=x_perm.dtype, device=x_perm.device)
+    gw = torch.empty(num_experts, 2 * I, H, dtype=out_dtype or x_perm.dtype, device=x_perm.device)
     call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x_perm), None, ptr(offs), dtype_code(x_perm.dtype),
-         P, num_experts, H, I, None, ptr(gw), stream_of(x_perm))
+         P, num_experts, H, I, None, ptr(gw), dtype_code(gw.dtype), stream_of(x_perm))
     return gw
 
 
@@ -171,7 +173,7 @@ def gate_up_backward(grad_gate_up_out, x_perm, gate_up_proj, offs):
     gx = torch.empty_like(x_perm)
     gw = torch.empty_like(gate_up_proj)
     call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x_perm), ptr(gate_up_proj), ptr(offs),
-         dtype_code(x_perm.dtype), P, E, H, I, ptr(gx), ptr(gw), stream_of(x_perm))
+         dtype_code(x_perm.dtype), P, E, H, I, ptr(gx), ptr(gw), dtype_code(gw.dtype), stream_of(x_perm))
     return gx, gw
 
 

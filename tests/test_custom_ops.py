@@ -63,11 +63,26 @@ def test_backward_fakes_drop_unneeded_grads(pmoe_ops):
     gy, gu, dn = _meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I)
     i32 = torch.int32
     args = (gy, gu, dn, _meta(E, dtype=i32), _meta(P, dtype=i32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), None, T, K)
-    gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [True, False, True])
+    gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [True, False, True], [False, False])
     assert _sig([gh, gdn]) == [((T, H), torch.bfloat16), ((E, H, I), torch.bfloat16)]
     assert ggu.numel() == 0  # absent gradient: empty stand-in
+    # gradients of fp32 master weights come out in fp32 from bf16 operands
+    gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [False, True, True], [True, True])
+    assert _sig([ggu, gdn]) == [((E, 2 * I, H), torch.float32), ((E, H, I), torch.float32)]
+    assert gh.numel() == 0
     g_y, g_w = pmoe_ops.combine_bwd(_meta(T, H), _meta(P, H), _meta(T, K), _meta(P, dtype=i32))
     assert _sig([g_y, g_w]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]
+
+
+def test_forward_ops_take_optional_masters(pmoe_ops):
+    # the fp32 masters ride along for autograd only: outputs are those of the bf16 copies
+    f32 = torch.float32
+    out = pmoe_ops.sparse_moe_fwd(_meta(T, H), _meta(E, H, dtype=f32), _meta(E, 2 * I, H), _meta(E, H, I), K, True,
+                                  None, _meta(E, 2 * I, H, dtype=f32), _meta(E, H, I, dtype=f32))
+    assert _sig(out[:1]) == [((T, H), torch.bfloat16)] and len(out) == 14
+    out = pmoe_ops.expert_ffn_fwd(_meta(T, H), _meta(T, K, dtype=torch.int64), _meta(T, K), _meta(E, 2 * I, H),
+                                  _meta(E, H, I), None, _meta(E, H, I, dtype=f32))
+    assert _sig(out[:1]) == [((T, H), torch.bfloat16)] and len(out) == 7
 
 
 def test_moe_sublayer_fwd_fake(pmoe_ops):
@@ -88,6 +103,7 @@ def test_sublayer_backward_fakes(pmoe_ops):
     x, nw = _meta(T, H, dtype=torch.float32), _meta(H, dtype=torch.float32)
     outs = pmoe_ops.sublayer_bwd(_meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I), _meta(E, dtype=torch.int32),
                                  _meta(P, dtype=torch.int32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), _meta(T, H),
-                                 x, nw, _meta(T, dtype=torch.float32), x, K, [True, False, True, True])
+                                 x, nw, _meta(T, dtype=torch.float32), x, K, [True, False, True, True],
+                                 [False, True])
     assert _sig(outs) == [((T, H), torch.float32), ((0,), torch.float32), ((E, 2 * I, H), torch.bfloat16),
-                          ((E, H, I), torch.bfloat16)]
+                          ((E, H, I), torch.float32)]

@@ -181,6 +181,44 @@ def test_sparse_mlp_empty_batch():
     assert to_np(mlp.router.last_stats.expert_counts).tolist() == [0] * E
 
 
+@pytest.mark.parametrize("entry", ["module", "expert_ffn"])
+def test_fp32_master_weights_under_autocast(entry):
+    """The trainer's regime (fp32 parameters, bf16 autocast): the expert weight
+    gradients arrive in fp32 straight from the GEMMs, and rounded to bf16 they
+    equal, bit for bit, the gradients of bf16 copies of the same weights."""
+    pa = _mod()
+    T, H, E, K, I = 384, 256, 16, 4, 128
+    say(f"fp32 masters under autocast ({entry}) T={T} H={H} E={E} K={K} I={I}")
+    g = gen(61)
+    x = torch.randn(T, H, generator=g).to(DEV)
+    Wr = (torch.randn(E, H, generator=g) * 0.05).to(DEV)
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(DEV)
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(DEV)
+    gout = torch.randn(T, H, generator=g).to(DEV)
+    ti, tw = None, None
+    if entry == "expert_ffn":
+        _, tw, ti = pa.router_topk(x.to(torch.bfloat16), Wr, K)
+
+    def run(gu, dn):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            if entry == "module":
+                out = pa.sparse_moe_block(x, Wr, gu, dn, K)[0]
+            else:
+                out = pa.moe_expert_ffn(x, ti, tw, gu, dn)
+        out.backward(gout)
+        return out.detach()
+
+    masters = [Wgu.clone().requires_grad_(True), Wdn.clone().requires_grad_(True)]
+    out_m = run(*masters)
+    copies = [Wgu.to(torch.bfloat16).requires_grad_(True), Wdn.to(torch.bfloat16).requires_grad_(True)]
+    out_c = run(*copies)
+    assert torch.equal(out_m, out_c)
+    for name, m, c in zip(("gate_up", "down"), masters, copies):
+        assert m.grad.dtype == torch.float32 and c.grad.dtype == torch.bfloat16, name
+        assert torch.equal(m.grad.to(torch.bfloat16), c.grad), name
+        assert torch.count_nonzero(m.grad).item() > 0, name
+
+
 def _check_routing_vs_cpu(x, Wr, gpu_logits, K, bias=None):
     """GPU ids == oracle ids on the GPU logits (bit-exact); vs CPU logits except near-ties."""
     cpu_logits = torch.nn.functional.linear(x.float(), Wr.float())

@@ -210,6 +210,38 @@ def test_gate_up_backward(dtype, case):
     assert r < TOL[dtype]
 
 
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_weight_gradients_in_fp32(case):
+    """bf16 operands, fp32 weight gradients (for fp32 master weights): the
+    unrounded accumulators of the same tiles, so rounding them gives the bf16
+    entry point's output bit for bit, and they sit within fp32 summation error
+    of the fp64 product."""
+    T, K, E, H, I, mode = case
+    say(f"wgrad fp32 out {case}")
+    ops = _ops()
+    bf, f32 = torch.bfloat16, torch.float32
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, bf)
+    g = gen(8)
+    P = T * K
+    gy = torch.randn(P, H, generator=g).to(bf).to(DEV)
+    mid = torch.randn(P, I, generator=g).to(bf).to(DEV)
+    ggu = torch.randn(P, 2 * I, generator=g).to(bf).to(DEV)
+    o = offs.cpu()
+    for name, f32_out, bf_out, ref in (
+            ("down", ops.down_proj_wgrad(gy, mid, offs, E, f32), ops.down_proj_wgrad(gy, mid, offs, E),
+             ref_wgrad(gy.cpu(), mid.cpu(), o)),
+            ("gate_up", ops.gate_up_wgrad(ggu, xp, offs, E, f32), ops.gate_up_wgrad(ggu, xp, offs, E),
+             ref_wgrad(ggu.cpu(), xp.cpu(), o))):
+        assert f32_out.dtype == f32 and bf_out.dtype == bf
+        r = rel(f32_out, ref)
+        say(f"  {name}: rel={r:.2e}")
+        assert r < 2e-5, name
+        assert torch.equal(f32_out.to(bf), bf_out), name
+        for e, (lo, hi) in enumerate(seg_bounds(o)):
+            if hi == lo:
+                assert torch.count_nonzero(f32_out[e]).item() == 0, "an empty expert has a zero weight gradient"
+
+
 # ----------------------------------------------------------------- router
 
 
