@@ -46,6 +46,9 @@ def parse_args():
                     help="skip timing the reference's own torch path (F.grouped_mm) on this GPU")
     ap.add_argument("--no-neighbours", action="store_true",
                     help="skip timing the MoE half-block with and without the fused RMSNorm / residual add")
+    ap.add_argument("--neighbours-only", action="store_true",
+                    help="time only the MoE half-block in the trainer's regime and print its JSON object "
+                         "(for profiling that regime on its own)")
     ap.add_argument("--cpu-tokens", type=int, default=512,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
     ap.add_argument("--copy-mib", type=int, default=256,
@@ -288,6 +291,11 @@ def main() -> int:
     if "logit_bias" in inp:
         mlp.router.logit_bias = inp["logit_bias"]
     B = cfg.batch
+    if args.neighbours_only:
+        assert cfg.backward and cfg.hidden <= 4096, "the half-block leg needs a fwd+bwd workload with H <= 4096"
+        print(json.dumps({"workload": cfg.name, "neighbours": neighbours(cfg, inp, args.steps, args.warmup, dev)}),
+              flush=True)
+        return 0
     x = inp["x"].reshape(B, T // B, H)
     gout = inp.get("grad_out")
     gout = gout.reshape(B, T // B, H) if gout is not None else None
