@@ -101,3 +101,15 @@ def test_product_package_does_not_import_the_oracle():
     for path in (ROOT / "pluggy_amd").rglob("*.py"):
         src = path.read_text()
         assert "import oracle" not in src and "from oracle" not in src, path
+
+
+@pytest.mark.parametrize("entry", ["pmoe_down_proj_backward", "pmoe_gate_up_backward"])
+def test_weight_gradient_dtype_is_checked(lib, entry):
+    """fp32 operands cannot write bf16 weight gradients; bf16 operands may write fp32 ones."""
+    from pluggy_amd import _lib
+
+    P, E, H, I = 64, 4, 64, 32
+    nulls = (None,) * (5 if entry == "pmoe_down_proj_backward" else 4)
+    rc = getattr(lib, entry)(*nulls, _lib.PMOE_F32, P, E, H, I, None, None, _lib.PMOE_BF16, None)
+    assert rc == -1 and b"dtype must be the operands' or fp32" in lib.pmoe_last_error_string()
+
