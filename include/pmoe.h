@@ -204,8 +204,9 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      size_t workspace_bytes, void* stream);
 
 /* Autograd of pmoe_expert_ffn_forward. Any of grad_hidden, grad_top_weights,
- * grad_gate_up_proj, grad_down_proj may be NULL. Workspace holds grad_y,
- * grad_gate_up_out and grad_x_perm. */
+ * grad_gate_up_proj, grad_down_proj may be NULL. grad_weight_dtype is the dtype of
+ * the two weight gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master
+ * weights). Workspace holds grad_y, grad_gate_up_out and grad_x_perm. */
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype);
 PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weights, int w_dtype,
                                       const void* gate_up_proj, const void* down_proj, int dtype, int64_t T,
@@ -213,7 +214,8 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
                                       const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
                                       const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
                                       void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
-                                      void* workspace, size_t workspace_bytes, void* stream);
+                                      int grad_weight_dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -54,7 +54,7 @@ SIGNATURES = {
                                        _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "pmoe_expert_ffn_backward_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _INT]),
     "pmoe_expert_ffn_backward": (_INT, [_P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
-                                        _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+                                        _P, _P, _P, _P, _P, _P, _P, _INT, _P, _SZ, _P]),
 }
 
 _lock = threading.Lock()

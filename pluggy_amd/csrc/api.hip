@@ -510,9 +510,12 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
                                       const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
                                       const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
                                       void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
+                                      int grad_weight_dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+               "expert_ffn_backward: weight gradient dtype must be the operands' or fp32");
   (void)sorted_pair;
   const size_t need = pmoe_expert_ffn_backward_workspace_size(T, K, H, I, dtype);
   if (workspace_bytes < need || (need > 0 && !workspace))
@@ -524,8 +527,9 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
   char* grad_gu = cv.take<char>((size_t)P * 2 * I * es);
   hipStream_t s = as_stream(stream);
   if (T == 0) {
-    if (grad_gate_up_proj) PMOE_TRY(hipMemsetAsync(grad_gate_up_proj, 0, (size_t)E * 2 * I * H * es, s), "zero");
-    if (grad_down_proj) PMOE_TRY(hipMemsetAsync(grad_down_proj, 0, (size_t)E * H * I * es, s), "zero");
+    const size_t gs = grad_weight_dtype == PMOE_BF16 ? 2 : 4;
+    if (grad_gate_up_proj) PMOE_TRY(hipMemsetAsync(grad_gate_up_proj, 0, (size_t)E * 2 * I * H * gs, s), "zero");
+    if (grad_down_proj) PMOE_TRY(hipMemsetAsync(grad_down_proj, 0, (size_t)E * H * I * gs, s), "zero");
     return PMOE_OK;
   }
   // 1. combine backward: grad_y and grad_top_weights. grad_y is needed for any
@@ -537,13 +541,13 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weig
   // 2. down GEMM backward (dgrad fused with SwiGLU backward, then wgrad)
   void* ggu = (grad_hidden || grad_gate_up_proj) ? grad_gu : nullptr;
   if (int rc = pmoe_down_proj_backward(grad_y, mid, gate_up_out, down_proj, offs, dtype, P, E, H, I, ggu,
-                                       grad_down_proj, dtype, stream))
+                                       grad_down_proj, grad_weight_dtype, stream))
     return rc;
   // 3. gate_up GEMM backward; grad_x_perm reuses grad_y (consumed above, same stream)
   void* gxp = grad_hidden ? grad_y : nullptr;
   if (ggu) {
     if (int rc = pmoe_gate_up_backward(grad_gu, x_perm, gate_up_proj, offs, dtype, P, E, H, I, gxp,
-                                       grad_gate_up_proj, dtype, stream))
+                                       grad_gate_up_proj, grad_weight_dtype, stream))
       return rc;
   }
   // 4. dispatch backward

@@ -219,6 +219,20 @@ def test_fp32_master_weights_under_autocast(entry):
         assert torch.count_nonzero(m.grad).item() > 0, name
 
 
+def test_fp32_master_weights_empty_batch():
+    """No tokens under autocast with fp32 masters: zero fp32 weight gradients."""
+    pa = _mod()
+    H, E, K, I = 256, 8, 2, 64
+    say(f"fp32 masters, empty batch H={H} E={E} K={K} I={I}")
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K, True).to(DEV)
+    x = torch.zeros(1, 0, H, device=DEV, requires_grad=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = mlp(x)
+    out.sum().backward()
+    for prm in (mlp.experts.gate_up_proj, mlp.experts.down_proj):
+        assert prm.grad is None or (prm.grad.dtype == torch.float32 and torch.count_nonzero(prm.grad).item() == 0)
+
+
 def _check_routing_vs_cpu(x, Wr, gpu_logits, K, bias=None):
     """GPU ids == oracle ids on the GPU logits (bit-exact); vs CPU logits except near-ties."""
     cpu_logits = torch.nn.functional.linear(x.float(), Wr.float())

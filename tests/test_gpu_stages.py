@@ -362,12 +362,21 @@ def test_fused_expert_ffn_entry_points(dtype):
     gdn = torch.empty_like(wdn)
     wsb = workspace(size("pmoe_expert_ffn_backward_workspace_size", T, K, H, I, dt), DEV)
     call("pmoe_expert_ffn_backward", ptr(gout), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
-         ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(gx), ptr(gw), ptr(ggu), ptr(gdn), ptr(wsb),
-         wsb.numel(), stream)
+         ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(gx), ptr(gw), ptr(ggu), ptr(gdn), dt,
+         ptr(wsb), wsb.numel(), stream)
     torch.cuda.synchronize()
     assert torch.equal(out, out_s)
     assert torch.equal(gx, xs.grad) and torch.equal(gw, ws_.grad)
     assert torch.equal(ggu, a.grad) and torch.equal(gdn, b.grad)
+    if dtype == torch.bfloat16:
+        # weight gradients of fp32 masters: the unrounded accumulators of the same tiles
+        ggu32 = torch.empty(wgu.shape, dtype=torch.float32, device=DEV)
+        gdn32 = torch.empty(wdn.shape, dtype=torch.float32, device=DEV)
+        call("pmoe_expert_ffn_backward", ptr(gout), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
+             ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), None, None, ptr(ggu32), ptr(gdn32),
+             dtype_code(torch.float32), ptr(wsb), wsb.numel(), stream)
+        torch.cuda.synchronize()
+        assert torch.equal(ggu32.to(dtype), ggu) and torch.equal(gdn32.to(dtype), gdn)
 
 
 def test_argument_errors_raise():
