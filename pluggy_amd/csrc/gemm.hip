@@ -1,4 +1,6 @@
 // Launchers of the grouped expert GEMMs and the router GEMMs.
+#include <mutex>
+
 #include "gemm_persist.h"
 #include "kernels.h"
 
@@ -50,12 +52,20 @@ typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, 0> DmaDecode;
 constexpr int kDecodeRowsPerExpert = 32;
 
 // Compute units of the current device (the persistent kernels launch one
-// block per CU).
+// block per CU), queried once per device and cached.
+constexpr int kMaxDevices = 64;
+std::once_flag g_cus_once[kMaxDevices];
+int g_cus[kMaxDevices];
+
 int num_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-  return n;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(g_cus_once[dev], [dev] {
+    int n = 0;
+    g_cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                     ? n : 256;
+  });
+  return g_cus[dev];
 }
 
 template <typename T>
