@@ -81,6 +81,7 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
 // partials), so the top-k kernel can fetch row r + 4 while it ranks row r;
 // finish_logits sums the partials in that fixed order and writes the logits.
 constexpr int kMaxParts = 3;
+constexpr int kMaxSplits = 8;  // split-K planes of the router logits GEMM (api.hip caps them at 8)
 template <int EPL>
 struct RowParts {
   float p[kMaxParts][EPL];
@@ -97,8 +98,17 @@ __device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int6
     for (int q = 0; q < kMaxParts; ++q) {
       float v = 0.0f;
       if (e < E && q < nparts) {
-        v = parts[q * part_stride + op];
-        for (int sp = 1; sp < nsplit; ++sp) v += parts[sp * split_stride + q * part_stride + op];
+        // every plane's load is issued before the first add (plane indexes
+        // past nsplit re-read the last plane, which is then not added), so a
+        // row costs one memory latency whatever nsplit is
+        float pl[kMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplits; ++sp)
+          pl[sp] = parts[min(sp, nsplit - 1) * split_stride + q * part_stride + op];
+        v = pl[0];
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplits; ++sp)
+          if (sp < nsplit) v += pl[sp];
       }
       rp.p[q][j] = v;
     }
@@ -718,7 +728,7 @@ hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int 
                        int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
                        float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
   if (T == 0) return hipSuccess;
-  if (nparts < 1 || nparts > kMaxParts || nsplit < 1) return hipErrorInvalidValue;
+  if (nparts < 1 || nparts > kMaxParts || nsplit < 1 || nsplit > kMaxSplits) return hipErrorInvalidValue;
   const unsigned grid = blocks_for(T, rows_per_block);
   const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \
