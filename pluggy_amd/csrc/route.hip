@@ -480,21 +480,16 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
   }
 }
 
-__global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
-                                                              int chunk, const int32_t* __restrict__ chunk_base,
-                                                              int32_t* __restrict__ sorted_pair,
-                                                              int32_t* __restrict__ inv_pos) {
-  extern __shared__ int sm[];
-  int* s_base = sm;       // [E]
-  int* s_wcnt = sm + E;   // [4][E]
+// Stable scatter of pairs q0 .. q1-1 by one block of 256 threads: s_base[e]
+// holds the position of expert e's first pair of the range, s_wcnt ([4][E])
+// is zero. Within a round of 256 pairs, a pair's rank among the lower lanes
+// of its wave with the same expert comes from ballots over the expert's bits,
+// and the lower waves' counts of that expert are added from LDS.
+__device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict__ idx, int q0, int q1, int E,
+                                                      int nbits, int* s_base, int* s_wcnt,
+                                                      int32_t* __restrict__ sorted_pair,
+                                                      int32_t* __restrict__ inv_pos) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += 256) {
-    s_base[e] = chunk_base[(int64_t)blockIdx.x * E + e];
-    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
-  }
-  __syncthreads();
-  const int q0 = blockIdx.x * chunk;
-  const int q1 = min(P, q0 + chunk);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int qb = q0; qb < q1; qb += 256) {
     const int q = qb + tid;
@@ -522,6 +517,69 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
+                                                              int chunk, const int32_t* __restrict__ chunk_base,
+                                                              int32_t* __restrict__ sorted_pair,
+                                                              int32_t* __restrict__ inv_pos) {
+  extern __shared__ int sm[];
+  int* s_base = sm;       // [E]
+  int* s_wcnt = sm + E;   // [4][E]
+  for (int e = threadIdx.x; e < E; e += 256) {
+    s_base[e] = chunk_base[(int64_t)blockIdx.x * E + e];
+    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
+  }
+  __syncthreads();
+  const int q0 = blockIdx.x * chunk;
+  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos);
+}
+
+// The whole permutation of at most one chunk of pairs (decode) in one block:
+// histogram, exclusive scan over the experts, stable scatter. Same result as
+// the three-kernel path, in one launch instead of three.
+__global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
+                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offs,
+                                                            int32_t* __restrict__ sorted_pair,
+                                                            int32_t* __restrict__ inv_pos) {
+  extern __shared__ int sm[];
+  int* s_base = sm;       // [E]: counts, then exclusive bases
+  int* s_wcnt = sm + E;   // [4][E]
+  __shared__ int s_wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += 256) {
+    s_base[e] = 0;
+    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
+  }
+  __syncthreads();
+  for (int q = tid; q < P; q += 256) atomicAdd(&s_base[clamp_expert(idx[q], E)], 1);
+  __syncthreads();
+  // thread t scans experts t*per .. t*per+per-1 (E <= 1024, per <= 4)
+  const int per = (E + 255) / 256;
+  int c[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * per + j;
+    c[j] = (j < per && e < E) ? s_base[e] : 0;
+    sum += c[j];
+  }
+  const int inc = wave_incl_scan(sum, lane);
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  int excl = inc - sum;
+  for (int w = 0; w < wave; ++w) excl += s_wsum[w];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * per + j;
+    if (j < per && e < E) {
+      counts[e] = c[j];
+      offs[e] = excl + c[j];
+      s_base[e] = excl;
+      excl += c[j];
+    }
+  }
+  __syncthreads();
+  permute_scatter_range(idx, 0, P, E, nbits, s_base, s_wcnt, sorted_pair, inv_pos);
 }
 
 // ---- row movers: one wave per token, 16-byte lanes. KC > 0 is the top-k
@@ -794,17 +852,18 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   const int P = T * K;
   const int nchunks = (P + chunk - 1) / chunk;
   if (E > 1024 || E < 1) return hipErrorInvalidValue;
-  if (nchunks > 0) {
-    hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
-                       chunk_hist);
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  if (nchunks <= 1) {
+    hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits, counts,
+                       offs, sorted_pair, inv_pos);
+    return hipGetLastError();
   }
+  hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
+                     chunk_hist);
   hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_hist, nchunks, E, counts, offs);
-  if (nchunks > 0) {
-    int nbits = 0;
-    while ((1 << nbits) < E) ++nbits;
-    hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E,
-                       nbits, chunk, chunk_hist, sorted_pair, inv_pos);
-  }
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits,
+                     chunk, chunk_hist, sorted_pair, inv_pos);
   return hipGetLastError();
 }
 

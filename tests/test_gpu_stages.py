@@ -32,6 +32,8 @@ def _ops():
 @pytest.mark.parametrize("T,K,E,mode", [
     (1, 1, 1, "uniform"), (7, 2, 8, "uniform"), (2048, 2, 8, "uniform"), (3000, 4, 33, "one"),
     (100, 8, 8, "uniform"), (8192, 8, 128, "uniform"), (8192, 8, 128, "zipf"), (4099, 6, 1000, "low"),
+    # one chunk of pairs or less: the single-block path (P = 2048 is its largest case)
+    (256, 8, 128, "zipf"), (64, 8, 1000, "low"), (40, 3, 256, "one"), (257, 8, 128, "uniform"),
 ])
 def test_permute_bitexact(T, K, E, mode):
     say(f"permute T={T} K={K} E={E} mode={mode}")
