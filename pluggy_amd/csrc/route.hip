@@ -97,14 +97,16 @@ __device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int6
 #pragma unroll
     for (int q = 0; q < kMaxParts; ++q) {
       float v = 0.0f;
-      if (e < E && q < nparts) {
-        // every plane's load is issued before the first add (plane indexes
-        // past nsplit re-read the last plane, which is then not added), so a
+      if (e < E && q < nparts && nsplit == 1) {
+        v = parts[q * part_stride + op];
+      } else if (e < E && q < nparts) {
+        // every plane's load is issued before the first add (nsplit is
+        // uniform, so the loads past it are skipped by scalar branches), so a
         // row costs one memory latency whatever nsplit is
         float pl[kMaxSplits];
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp)
-          pl[sp] = parts[min(sp, nsplit - 1) * split_stride + q * part_stride + op];
+          pl[sp] = sp < nsplit ? parts[sp * split_stride + q * part_stride + op] : 0.0f;
         v = pl[0];
 #pragma unroll
         for (int sp = 1; sp < kMaxSplits; ++sp)
