@@ -75,7 +75,7 @@ int router_logit_splits(int64_t T, int64_t H) {
   if (T <= 0) return 1;
   const int64_t tiles = 3 * ((T + 63) / 64);
   int64_t s = (256 + tiles - 1) / tiles;
-  s = std::min<int64_t>(s, std::min<int64_t>(8, std::max<int64_t>(1, H / 256)));
+  s = std::min<int64_t>(s, std::min<int64_t>(kRouterMaxSplits, std::max<int64_t>(1, H / 256)));
   return (int)std::max<int64_t>(1, s);
 }
 int64_t router_splits(int64_t T) { return std::max<int64_t>(1, (T + kRouterSplitChunk - 1) / kRouterSplitChunk); }

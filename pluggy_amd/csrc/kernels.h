@@ -123,6 +123,9 @@ hipError_t sum_row_groups(const float* partial, int rows, int n, float* tmp, hip
 
 // Chunk size (pairs) of the permutation histogram and the workspace it needs.
 constexpr int kPermuteChunk = 2048;
+// Most split-K planes of the bf16-pieces router logits GEMM (the top-k kernel
+// loads all of a row's planes at once).
+constexpr int kRouterMaxSplits = 8;
 inline int64_t permute_chunks(int64_t P) { return (P + kPermuteChunk - 1) / kPermuteChunk; }
 
 }  // namespace pmoe

@@ -81,7 +81,7 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
 // partials), so the top-k kernel can fetch row r + 4 while it ranks row r;
 // finish_logits sums the partials in that fixed order and writes the logits.
 constexpr int kMaxParts = 3;
-constexpr int kMaxSplits = 8;  // split-K planes of the router logits GEMM (api.hip caps them at 8)
+constexpr int kMaxSplits = kRouterMaxSplits;
 template <int EPL>
 struct RowParts {
   float p[kMaxParts][EPL];
