@@ -81,11 +81,24 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
  * the P = T*K pairs q = t*K + k by expert top_indices[q].
  * counts (E,) int32; offs (E,) int32 inclusive end offsets (moe.py:108);
  * sorted_pair (P,) int32 (token = sorted_pair / K); inv_pos (P,) int32 with
- * inv_pos[sorted_pair[p]] = p. Ids outside [0,E) are clamped into range. */
+ * inv_pos[sorted_pair[p]] = p.
+ * Ids outside [0,E) are not rejected here (no entry point syncs the host):
+ * they are clamped into range, so such a pair is routed to expert 0 or E-1,
+ * where the reference raises (F.one_hot at moe.py:50 on its loop path,
+ * bincount and the offs length on its grouped path, moe.py:106-108). Callers
+ * whose indices do not come from pmoe_router_forward check them first with
+ * pmoe_count_invalid_ids (the Python operator moe_expert_ffn does, and
+ * raises). */
 PMOE_API size_t pmoe_permute_workspace_size(int64_t T, int64_t K, int64_t E);
 PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int64_t E, int32_t* counts,
                           int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* Number of ids in top_indices[0..n) outside [0, E), written to count[0]
+ * (int32, device memory): the check behind the RuntimeError that the
+ * reference's F.one_hot (moe.py:50) and bincount (moe.py:107) raise on such
+ * ids. One small kernel; the caller reads the count. */
+PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64_t E, int32_t* count, void* stream);
 
 /* Row gather hidden[sorted_token] (moe.py:104), done in scatter form:
  * x_perm[inv_pos[t*K + k]] = hidden[t] for every token t and slot k (each

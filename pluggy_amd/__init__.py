@@ -6,12 +6,14 @@ in ``libpmoe.so`` (C ABI in ``include/pmoe.h``).
 """
 
 from .moe import RouterStats, moe_expert_ffn, moe_sublayer, router_topk, sparse_moe_block
-from .qwen3_moe import (
-    Qwen3MoeExperts,
-    Qwen3MoeSparseMLP,
-    Qwen3MoeTopKRouter,
+from .qwen3_moe import Qwen3MoeExperts, Qwen3MoeSparseMLP, Qwen3MoeTopKRouter
+from .router_aux import (
+    expert_counts_from_stats,
+    install_stats_aux,
+    load_balancing_loss,
     load_balancing_loss_from_stats,
     router_z_loss_from_stats,
+    select_lower_id,
 )
 
 __all__ = [
@@ -19,10 +21,14 @@ __all__ = [
     "Qwen3MoeSparseMLP",
     "Qwen3MoeTopKRouter",
     "RouterStats",
+    "expert_counts_from_stats",
+    "install_stats_aux",
+    "load_balancing_loss",
     "load_balancing_loss_from_stats",
     "moe_expert_ffn",
     "moe_sublayer",
     "router_topk",
     "router_z_loss_from_stats",
+    "select_lower_id",
     "sparse_moe_block",
 ]

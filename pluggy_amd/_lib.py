@@ -35,6 +35,7 @@ SIGNATURES = {
                                     _P, _P, _SZ, _P]),
     "pmoe_permute_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_permute": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_count_invalid_ids": (_INT, [_P, _I64, _I64, _P, _P]),
     "pmoe_dispatch": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P]),
     "pmoe_gate_up_swiglu": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_down_proj": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P]),

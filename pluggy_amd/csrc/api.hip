@@ -291,6 +291,14 @@ PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int6
   return PMOE_OK;
 }
 
+PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64_t E, int32_t* count,
+                                    void* stream) {
+  PMOE_REQUIRE(n >= 0 && E >= 1, "count_invalid_ids: n %lld, E %lld", (long long)n, (long long)E);
+  PMOE_REQUIRE(count && (n == 0 || top_indices), "count_invalid_ids: null tensor");
+  PMOE_TRY(count_invalid_ids(top_indices, n, E, count, as_stream(stream)), "count_invalid_ids");
+  return PMOE_OK;
+}
+
 PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
                            void* x_perm, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;

@@ -24,31 +24,13 @@ template <> struct CfgFor<float> { typedef CfgF32 type; };
 // Qwen3-30B-A3B shape over 128x128 .. 256x256 tilings, 2..5 stages and
 // 32/64-deep k tiles: larger tiles fetch fewer bytes per MFMA through each
 // CU's vector-memory path, which bounds the smaller ones.
-typedef DmaCfg<256, 256, 128, 64, 3, 32, 1, 0> DmaExpert;
-#ifndef PMOE_CFG_GATE_UP_FWD
-#define PMOE_CFG_GATE_UP_FWD DmaExpert
-#endif
-#ifndef PMOE_CFG_DOWN_FWD
-#define PMOE_CFG_DOWN_FWD DmaExpert
-#endif
-#ifndef PMOE_CFG_DOWN_DGRAD
-#define PMOE_CFG_DOWN_DGRAD DmaExpert
-#endif
-#ifndef PMOE_CFG_DOWN_WGRAD
-#define PMOE_CFG_DOWN_WGRAD DmaExpert
-#endif
-#ifndef PMOE_CFG_GATE_UP_DGRAD
-#define PMOE_CFG_GATE_UP_DGRAD DmaExpert
-#endif
-#ifndef PMOE_CFG_GATE_UP_WGRAD
-#define PMOE_CFG_GATE_UP_WGRAD DmaExpert
-#endif
+typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaExpert;
 // Forward GEMMs of few-token (decode) batches, where each expert holds a few
 // rows and the GEMM is a stream of expert weights: 32-row x 128-column blocks
 // of four 32x32 wave tiles, 128-deep k stages (256-byte weight-row pieces, which
 // stream from HBM ≈15 % faster than the 64-byte pieces of 32-deep stages), a
 // three-stage ring (120 KiB). Used when the experts average at most 32 rows.
-typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, 0> DmaDecode;
+typedef DmaCfg<32, 128, 32, 32, 3, 128, 1> DmaDecode;
 constexpr int kDecodeRowsPerExpert = 32;
 
 // Compute units of the current device (the persistent kernels launch one
@@ -72,25 +54,9 @@ template <typename T>
 hipError_t run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P, int E, int H,
                int I, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {
-#ifdef PMOE_NO_PERSIST
-#define PMOE_EG(CFG) expert_gemm_dma<CFG>(kind, A, B, aux, C, C2, offs, P, E, H, I, s)
-#else
-#define PMOE_EG(CFG) expert_gemm_persist<CFG>(kind, A, B, aux, C, C2, offs, P, E, H, I, num_cus(), s)
-#endif
-#ifndef PMOE_NO_PERSIST
     if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
       return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, num_cus(), s);
-#endif
-    switch (kind) {
-      case EG_GATE_UP_FWD: return PMOE_EG(PMOE_CFG_GATE_UP_FWD);
-      case EG_DOWN_FWD: return PMOE_EG(PMOE_CFG_DOWN_FWD);
-      case EG_DOWN_DGRAD: return PMOE_EG(PMOE_CFG_DOWN_DGRAD);
-      case EG_DOWN_WGRAD: return PMOE_EG(PMOE_CFG_DOWN_WGRAD);
-      case EG_GATE_UP_DGRAD: return PMOE_EG(PMOE_CFG_GATE_UP_DGRAD);
-      case EG_GATE_UP_WGRAD: return PMOE_EG(PMOE_CFG_GATE_UP_WGRAD);
-    }
-#undef PMOE_EG
-    return hipErrorInvalidValue;
+    return expert_gemm_persist<DmaExpert>(kind, A, B, aux, C, C2, offs, P, E, H, I, num_cus(), s);
   } else {
     return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
   }
@@ -136,12 +102,12 @@ hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int
 
 hipError_t down_wgrad_f32(const bf16_t* dy, const bf16_t* mid, const int32_t* offs, int P, int E, int H, int I,
                           float* dw_dn, hipStream_t s) {
-  return expert_wgrad_persist_f32<PMOE_CFG_DOWN_WGRAD>(EG_DOWN_WGRAD, dy, mid, dw_dn, offs, P, E, H, I, num_cus(), s);
+  return expert_wgrad_persist_f32<DmaExpert>(EG_DOWN_WGRAD, dy, mid, dw_dn, offs, P, E, H, I, num_cus(), s);
 }
 
 hipError_t gate_up_wgrad_f32(const bf16_t* dgu, const bf16_t* x_perm, const int32_t* offs, int P, int E, int H,
                              int I, float* dw_gu, hipStream_t s) {
-  return expert_wgrad_persist_f32<PMOE_CFG_GATE_UP_WGRAD>(EG_GATE_UP_WGRAD, dgu, x_perm, dw_gu, offs, P, E, H, I,
+  return expert_wgrad_persist_f32<DmaExpert>(EG_GATE_UP_WGRAD, dgu, x_perm, dw_gu, offs, P, E, H, I,
                                                           num_cus(), s);
 }
 
@@ -155,16 +121,10 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
   return launch_gemm<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
 }
 
-// Router GEMM tile configurations (overridable at build time for sweeps).
-#ifndef PMOE_CFG_ROUTER_LOGITS
-#define PMOE_CFG_ROUTER_LOGITS DmaCfg<64, 64, 32, 32, 2>
-#endif
-#ifndef PMOE_CFG_ROUTER_DX
-#define PMOE_CFG_ROUTER_DX DmaCfg<128, 128, 64, 64, 2>
-#endif
-#ifndef PMOE_CFG_ROUTER_DW
-#define PMOE_CFG_ROUTER_DW DmaCfg<128, 128, 64, 64, 2>
-#endif
+// Router GEMM tile configurations: the logits GEMM on 64x64 blocks of four
+// 32x32 wave tiles (N = 3E is small), the two backward GEMMs on 128x128 blocks.
+typedef DmaCfg<64, 64, 32, 32, 2> DmaRouterLogits;
+typedef DmaCfg<128, 128, 64, 64, 2> DmaRouterBwd;
 
 // Router logits from bf16 pieces of the router weight on the DMA engine: the
 // pieces are stacked along N (npieces*E columns), so the n-tiles of one
@@ -181,12 +141,12 @@ hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npie
   p.C = parts; p.ldc = npieces * E;
   p.M = T; p.N = npieces * E; p.K = H;
   p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)npieces * E * H * 2;
-  if (splits <= 1) return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_NONE, EPI_STORE, float>(p, s);
-  constexpr int BK = PMOE_CFG_ROUTER_LOGITS::BK;
+  if (splits <= 1) return launch_gemm_dma<DmaRouterLogits, true, true, GM_NONE, EPI_STORE, float>(p, s);
+  constexpr int BK = DmaRouterLogits::BK;
   p.groups = splits;
   p.split_chunk = ((H + splits - 1) / splits + BK - 1) / BK * BK;
   p.strideC = (int64_t)T * npieces * E;
-  return launch_gemm_dma<PMOE_CFG_ROUTER_LOGITS, true, true, GM_BATCH, EPI_STORE, float>(p, s);
+  return launch_gemm_dma<DmaRouterLogits, true, true, GM_BATCH, EPI_STORE, float>(p, s);
 }
 
 // Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
@@ -198,7 +158,7 @@ hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, 
   p.C = dx; p.ldc = H;
   p.M = T; p.N = H; p.K = 3 * ldl;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)3 * ldl * H * 2;
-  return launch_gemm_dma<PMOE_CFG_ROUTER_DX, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
+  return launch_gemm_dma<DmaRouterBwd, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
 }
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and
@@ -213,7 +173,7 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
   p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
   p.M = E; p.N = H; p.K = T;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
-  return launch_gemm_dma<PMOE_CFG_ROUTER_DW, false, false, GM_RED, EPI_STORE, float>(p, s);
+  return launch_gemm_dma<DmaRouterBwd, false, false, GM_RED, EPI_STORE, float>(p, s);
 }
 
 template <typename TX, typename TW>

@@ -32,14 +32,10 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 
 // MINB: blocks per CU the register allocation must allow (launch bounds).
-// SPLIT: the first half of the waves issue every DMA of a stage (each wave
-// then has one DMA-issuing and one MFMA-only partner per SIMD, so a wave
-// stalled on memory-instruction issue never idles the matrix unit).
-template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1, int SPLIT_ = 0>
+template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1>
 struct DmaCfg {
   typedef bf16_t Tc;
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, BK = BK_, MINB = MINB_;
-  static constexpr bool SPLIT = SPLIT_ != 0;
   static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = kWave * NW;
@@ -47,8 +43,7 @@ struct DmaCfg {
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int A_INSTR = A_BYTES / 1024 / NW, B_INSTR = B_BYTES / 1024 / NW;  // 1 KB DMAs per wave
-  static constexpr int D = A_INSTR + B_INSTR;  // DMAs per wave-share of a stage
-  static constexpr int DW = SPLIT ? 2 * D : D;   // DMAs per issuing wave per stage
+  static constexpr int D = A_INSTR + B_INSTR;  // DMAs per wave per stage
   static constexpr int EPI_LD = WN + 4;
   static constexpr int EPI_BYTES = NW * 32 * EPI_LD * 4;
   static constexpr int MAIN_BYTES = NS * STAGE_BYTES;
@@ -57,8 +52,7 @@ struct DmaCfg {
   static_assert(BK == 32 || BK == 64 || BK == 128, "k extent of a stage");
   static_assert(A_INSTR * NW * 1024 == A_BYTES && B_INSTR * NW * 1024 == B_BYTES,
                 "DMA instructions must divide among waves");
-  static_assert(NS >= 2 && (NS - 1) * DW < 64, "ring depth");
-  static_assert(!SPLIT || NW % 2 == 0, "split DMA issue needs an even number of waves");
+  static_assert(NS >= 2 && (NS - 1) * D < 64, "ring depth");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -363,36 +357,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Timestamps of pipeline events for performance analysis builds only
-// (-DPMOE_PROBE=<block>): wave 0 of that block records (event, clock64) pairs.
-#ifdef PMOE_PROBE
-__device__ unsigned long long g_probe[4096];
-#define PMOE_MARK(ev)                                                                        \
-  do {                                                                                       \
-    if (blockIdx.x == PMOE_PROBE && threadIdx.x == 0 && probe_n < 4094) {                    \
-      g_probe[probe_n++] = (ev);                                                             \
-      g_probe[probe_n++] = clock64();                                                        \
-    }                                                                                        \
-  } while (0)
-#else
-#define PMOE_MARK(ev) \
-  do {                \
-  } while (0)
-#endif
-// Per-block start / end wall clock (-DPMOE_BLOCKTIME): g_btime[2b], g_btime[2b+1].
-#ifdef PMOE_BLOCKTIME
-__device__ unsigned long long g_btime[2 * 65536];
-#define PMOE_BTIME(slot)                                                         \
-  do {                                                                           \
-    if (threadIdx.x == 0 && blockIdx.x < 65536)                                  \
-      g_btime[2 * blockIdx.x + (slot)] = __builtin_amdgcn_s_memrealtime();       \
-  } while (0)
-#else
-#define PMOE_BTIME(slot) \
-  do {                   \
-  } while (0)
-#endif
-
 // Blocks are dispatched to the 8 XCDs round-robin; give each XCD a contiguous
 // range of logical tiles so that tiles sharing operands share an L2.
 __device__ __forceinline__ int xcd_remap(int b, int grid) {
@@ -461,11 +425,6 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-#ifdef PMOE_PROBE
-  int probe_n = 0;
-#endif
-  PMOE_MARK(0);
-  PMOE_BTIME(0);
   const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
 
   // ---- tile mapping (logical tile id, n fastest)
@@ -544,12 +503,6 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   const BufRsrc rsB = make_rsrc(b_base, b_bytes);
   typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
   typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
-  // DMA share of "virtual wave" vw: the waves that issue DMAs take the share
-  // of their own index and, with SPLIT, that of wave + NW/2.
-  constexpr bool SPLIT = Cfg::SPLIT;
-  constexpr int DW = Cfg::DW;
-  const bool dma_wave = !SPLIT || wave < NW / 2;
-  const int vw0 = wave, vw1 = SPLIT ? wave + NW / 2 : wave;
   auto init_a = [&](LdA& la, int vw) {
     if constexpr (A_KC) {
       const int rows = ti.m_end - ti.m0;
@@ -575,14 +528,10 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
       lb.init(ti.n0, p.N, vw, lane);
     }
   };
-  LdA la0, la1;
-  LdB lb0, lb1;
-  init_a(la0, vw0);
-  init_b(lb0, vw0);
-  if constexpr (SPLIT) {
-    init_a(la1, vw1);
-    init_b(lb1, vw1);
-  }
+  LdA la0;
+  LdB lb0;
+  init_a(la0, wave);
+  init_b(lb0, wave);
 
   f32x16 acc[MI][NI];
 #pragma unroll
@@ -599,8 +548,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   const int kd0 = (GM == GM_RED) ? 0 : ti.k_lo;
   const int kd_hi = ti.k_hi - ((GM == GM_RED) ? ti.k_lo : 0);
 
-  // DMA instruction J (0 .. DW-1) of stage kt: J < D is the share of vw0
-  // (A's instructions, then B's), J >= D that of vw1.
+  // DMA instruction J (0 .. D-1) of stage kt: A's instructions, then B's.
   auto dma_share = [&](int kt, auto jc, const LdA& la, const LdB& lb, int vw) {
     constexpr int J = decltype(jc)::value;
     const uint32_t st = lds0 + (uint32_t)((kt % NS) * Cfg::STAGE_BYTES);
@@ -614,14 +562,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
       else lb.template issue1<JB>(rsB, st + Cfg::A_BYTES, k0, p.ldb, vw);
     }
   };
-  auto dma_one = [&](int kt, auto jc) {
-    constexpr int J = decltype(jc)::value;
-    if constexpr (J < D) dma_share(kt, jc, la0, lb0, vw0);
-    else dma_share(kt, std::integral_constant<int, J - D>(), la1, lb1, vw1);
-  };
-  auto issue = [&](int kt) {
-    if (dma_wave) static_for<0, DW>([&](auto jc) { dma_one(kt, jc); });
-  };
+  auto dma_one = [&](int kt, auto jc) { dma_share(kt, jc, la0, lb0, wave); };
+  auto issue = [&](int kt) { static_for<0, D>([&](auto jc) { dma_one(kt, jc); }); };
 
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
   // Fragments of k-substep ks (16 deep) of the stage at sa / sb.
@@ -654,10 +596,10 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
       acc[M / NI][M % NI] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
       constexpr int G = KSI * MI * NI + M;  // MFMA index within the stage
-      static_for<0, DW>([&](auto dc) {
+      static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
-        if constexpr ((DI * TOTM) / DW == G) {
-          if (dma_st >= 0 && dma_wave) dma_one(dma_st, dc);
+        if constexpr ((DI * TOTM) / D == G) {
+          if (dma_st >= 0) dma_one(dma_st, dc);
         }
       });
     });
@@ -671,16 +613,13 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   // stage kt and makes stage kt+1 visible); the first fragments of stage kt+1
   // are read while the last MFMAs of stage kt run. The loop body is
   // straight-line code; the last stage is peeled.
-  PMOE_MARK(1);
 #pragma unroll
   for (int s0 = 0; s0 < NS; ++s0)
     if (s0 < nk) issue(s0);
   bf16x8 af[2][MI], bfr[2][NI];
   if (nk > 0) {
-    wait_stages<DW, NS>(min(NS, nk) - 1);
-    PMOE_MARK(2);
+    wait_stages<D, NS>(min(NS, nk) - 1);
     lds_barrier();
-    PMOE_MARK(3);
     load_frags(smem, smem + Cfg::A_BYTES, 0, af[0], bfr[0]);
   }
   for (int kt = 0; kt + 1 < nk; ++kt) {
@@ -693,15 +632,11 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
       substep(ksc, af[KSI & 1], bfr[KSI & 1], dma_st);
     });
     // stages kt+2 .. min(kt+NS-1, nk-1) may stay in flight
-    PMOE_MARK(10);
-    wait_stages<DW, NS>(min(NS - 1, nk - 1 - kt) - 1);
-    PMOE_MARK(11);
+    wait_stages<D, NS>(min(NS - 1, nk - 1 - kt) - 1);
     lds_barrier();
-    PMOE_MARK(12);
     const char* na = smem + ((kt + 1) % NS) * Cfg::STAGE_BYTES;
     load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
     substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], -1);
-    PMOE_MARK(13);
   }
   if (nk > 0) {
     const char* sa = smem + ((nk - 1) % NS) * Cfg::STAGE_BYTES;
@@ -712,13 +647,9 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
       substep(ksc, af[KSI & 1], bfr[KSI & 1], -1);
     });
   }
-  PMOE_MARK(20);
   wait_vmcnt<0>();
   lds_barrier();
-  PMOE_MARK(21);
   store_tile_dma<Cfg, Tout, GM, EPI>(acc, reinterpret_cast<float*>(smem), ti, p, wave, wm, wn, lane);
-  PMOE_MARK(22);
-  PMOE_BTIME(1);
 }
 
 template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
@@ -735,22 +666,6 @@ hipError_t launch_gemm_dma(const GemmParams& p, hipStream_t s) {
   hipLaunchKernelGGL((grouped_gemm_dma_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3((unsigned)grid), dim3(Cfg::NT), 0,
                      s, p);
   return hipGetLastError();
-}
-
-// The six expert GEMMs (see ExpertGemm in gemm.h) on the DMA engine, bf16 only.
-template <class Cfg>
-hipError_t expert_gemm_dma(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C, bf16_t* C2,
-                           const int32_t* offs, int P, int E, int H, int I, hipStream_t s) {
-  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I);
-  switch (kind) {
-    case EG_GATE_UP_FWD: return launch_gemm_dma<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, s);
-    case EG_DOWN_FWD: return launch_gemm_dma<Cfg, true, true, GM_ROWS, EPI_STORE>(p, s);
-    case EG_DOWN_DGRAD: return launch_gemm_dma<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, s);
-    case EG_DOWN_WGRAD: return launch_gemm_dma<Cfg, false, false, GM_RED, EPI_STORE>(p, s);
-    case EG_GATE_UP_DGRAD: return launch_gemm_dma<Cfg, true, false, GM_ROWS, EPI_STORE>(p, s);
-    case EG_GATE_UP_WGRAD: return launch_gemm_dma<Cfg, false, false, GM_RED, EPI_STORE>(p, s);
-  }
-  return hipErrorInvalidValue;
 }
 
 }  // namespace pmoe

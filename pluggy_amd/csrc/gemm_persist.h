@@ -170,7 +170,6 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   typedef PersistLayout<Cfg> L;
-  static_assert(!Cfg::SPLIT, "every wave issues its share of the DMAs");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");
@@ -184,11 +183,6 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
   const int groups = p.groups;
-#ifdef PMOE_PROBE
-  int probe_n = 0;
-#endif
-  PMOE_MARK(0);
-  PMOE_BTIME(0);
 
   // ---- tile list: GM_ROWS m-tiles follow the per-group row counts
   for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs[g];
@@ -233,11 +227,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
   // of stage g. With a double buffer (NS = 2) the next stage has only the
   // current one to land in, so its DMAs go out in the first substep.
-#ifdef PMOE_DMA_SPREAD
-  constexpr int SPREAD = PMOE_DMA_SPREAD < KS - 1 ? PMOE_DMA_SPREAD : KS - 1;
-#else
   constexpr int SPREAD = NS == 2 ? 1 : KS - 1;
-#endif
   constexpr int TOTM = SPREAD * MI * NI;  // MFMA slots the DMAs are spread over (several may share one)
   static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
@@ -413,40 +403,31 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       T.kd0 = in_next ? nxt.kd0 : cur.kd0;
       T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
       const int ls = in_next ? s - nk : s;
-      PMOE_MARK(10);
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
         load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
         substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1);
       });
-      PMOE_MARK(11);
       if (kt > 0) wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
-      PMOE_MARK(12);
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
-      PMOE_MARK(13);
       const char* na = smem + slot_of(g + 1);
       load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1);
     }
-    PMOE_MARK(20);
     // The next tile's first NS - 1 stages were issued during this tile's last
     // stages; wait for them before the epilogue issues its stores. The vector
     // memory counter also counts stores, so a wait placed after them (at the
     // next tile's stage 0) would hold every wave until its stores drained;
     // here the stores get a whole stage to drain before the next wait.
     wait_vmcnt<0>();
-    PMOE_MARK(24);
     store_slabs<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
-    PMOE_MARK(21);
     gs += nk;
     bi += nb;
     if (bi >= cnt) break;
     cur = nxt;
     setup(bi + nb, nxt);
-    PMOE_MARK(22);
   }
   wait_vmcnt<0>();  // the zero-reading DMAs past the last tile
-  PMOE_BTIME(1);
 }
 
 template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>

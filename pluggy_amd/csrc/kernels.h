@@ -80,6 +80,7 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
 template <typename TO>
 hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s);
 
+hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* count, hipStream_t s);
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
                          int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s);
 template <typename T>

@@ -869,6 +869,32 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   return hipGetLastError();
 }
 
+// Ids outside [0, E): one block of 1024 threads strides over all n ids and
+// writes the count (no atomics, no prior clearing of `count`).
+__global__ __launch_bounds__(1024) void count_invalid_ids_kernel(const int64_t* __restrict__ idx, int64_t n, int64_t E,
+                                                                 int32_t* __restrict__ count) {
+  __shared__ int s_w[16];
+  int c = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const int64_t e = idx[i];
+    c += (e < 0 || e >= E) ? 1 : 0;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  c = wave_incl_scan(c, lane);
+  if (lane == 63) s_w[wave] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+    for (int w = 0; w < 16; ++w) t += s_w[w];
+    count[0] = t;
+  }
+}
+
+hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* count, hipStream_t s) {
+  hipLaunchKernelGGL(count_invalid_ids_kernel, dim3(1), dim3(1024), 0, s, idx, n, E, count);
+  return hipGetLastError();
+}
+
 // Calls F with the compile-time top-k (the common values) or 0 (runtime K).
 template <class F>
 hipError_t with_kc(int K, F&& f) {

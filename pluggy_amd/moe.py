@@ -248,6 +248,20 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
 # -------------------------------------------------------------- expert FFN
 
 
+# Check caller-supplied expert ids before routing (moe_expert_ffn). The
+# reference raises on an id outside [0, E) (F.one_hot at moe.py:50, bincount at
+# moe.py:107); the kernels would clamp it into range instead. The check reads
+# one int32 back, i.e. it synchronises the host once per call, as the
+# reference's own bincount and .tolist() do; set False to skip it.
+VALIDATE_EXPERT_IDS = True
+
+
+def _check_expert_ids(top_indices: torch.Tensor, num_experts: int) -> None:
+    bad = int(ops.count_invalid_ids(top_indices, num_experts).item())
+    if bad:
+        raise RuntimeError(f"moe_expert_ffn: {bad} expert id(s) outside [0, {num_experts})")
+
+
 def _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj):
     """-> out and what the backward reads: offs, inv_pos, x_perm, gu, mid, y."""
     E = gate_up_proj.shape[0]
@@ -281,6 +295,8 @@ def _expert_ffn_fwd(hidden, top_indices, top_weights, gate_up_proj, down_proj, g
                     down_master=None):
     """The masters, when given, are the differentiable fp32 weights whose bf16
     copies gate_up_proj / down_proj are; the forward does not read them."""
+    if VALIDATE_EXPERT_IDS:
+        _check_expert_ids(top_indices, gate_up_proj.shape[0])
     return _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj)
 
 

@@ -68,6 +68,15 @@ def permute(top_indices, num_experts: int):
     return counts, offs, sorted_pair, inv_pos
 
 
+def count_invalid_ids(top_indices, num_experts: int) -> torch.Tensor:
+    """-> (1,) int32 device tensor: ids of top_indices outside [0, E)."""
+    require_gpu(top_indices)
+    count = torch.empty(1, dtype=torch.int32, device=top_indices.device)
+    call("pmoe_count_invalid_ids", ptr(top_indices), top_indices.numel(), num_experts, ptr(count),
+         stream_of(top_indices))
+    return count
+
+
 def dispatch(hidden, inv_pos, top_k: int):
     """x_perm[inv_pos[t*K + k]] = hidden[t] (the expert-sorted row gather)."""
     T, H = hidden.shape

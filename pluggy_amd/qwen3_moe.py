@@ -80,21 +80,3 @@ class Qwen3MoeSparseMLP(nn.Module):
         self.last_router_logits = logits
         return y.reshape(B, S, H)
 
-
-def load_balancing_loss_from_stats(stats: list[RouterStats], num_experts: int) -> torch.Tensor:
-    """Value of ``load_balancing_loss`` (qwen3_moe.py:285-308) from fused statistics.
-
-    ``E * sum_e (count_e / N) * (prob_sum_e / N)`` over the N rows of all layers;
-    equal to the reference value when selection agrees (no grad: use the
-    logits-based loss in training).
-    """
-    n = sum(s.tokens for s in stats)
-    counts = sum(s.expert_counts.double() for s in stats)
-    psum = sum(s.prob_sum.double() for s in stats)
-    return (counts / n * psum / n).sum() * num_experts
-
-
-def router_z_loss_from_stats(stats: list[RouterStats]) -> torch.Tensor:
-    """Value of ``router_z_loss`` (qwen3_moe.py:311-316): mean_t logsumexp(logits_t)^2."""
-    n = sum(s.tokens for s in stats)
-    return sum(s.lse_sq_sum.double() for s in stats).sum() / n

@@ -394,3 +394,30 @@ def test_argument_errors_raise():
         import pluggy_amd
         pluggy_amd.moe_expert_ffn(torch.zeros(4, 8), torch.zeros(4, 1, dtype=torch.int64), torch.ones(4, 1),
                                   torch.zeros(2, 16, 8), torch.zeros(2, 8, 8))
+
+
+@pytest.mark.parametrize("n,E", [(0, 4), (1, 1), (4096, 128), (100000, 33)])
+def test_count_invalid_ids(n, E):
+    """The id check counts exactly the ids outside [0, E) (negative and >= E)."""
+    g = gen(n + E)
+    ids = torch.randint(-3, E + 3, (n,), generator=g, dtype=torch.int64)
+    got = int(_ops().count_invalid_ids(ids.reshape(-1, 1).to(DEV), E).item())
+    assert got == int(((ids < 0) | (ids >= E)).sum())
+
+
+@pytest.mark.parametrize("bad", [-1, 8, 1 << 40])
+def test_moe_expert_ffn_rejects_out_of_range_ids(bad):
+    """moe_expert_ffn raises on an id outside [0, E), as the reference's F.one_hot /
+    bincount do (moe.py:50, :107), instead of routing the pair to a clamped expert."""
+    import pluggy_amd
+    T, H, I, E, K = 16, 64, 32, 8, 2
+    idx = torch.stack([torch.arange(T) % E, (torch.arange(T) + 1) % E], 1)
+    idx[5, 1] = bad
+    w = torch.full((T, K), 0.5)
+    args = (torch.randn(T, H).to(DEV), idx.to(DEV), w.to(DEV), torch.randn(E, 2 * I, H).to(DEV) * 0.02,
+            torch.randn(E, H, I).to(DEV) * 0.02)
+    with pytest.raises(RuntimeError, match="outside"):
+        pluggy_amd.moe_expert_ffn(*args)
+    idx[5, 1] = 3
+    out = pluggy_amd.moe_expert_ffn(args[0], idx.to(DEV), *args[2:])
+    assert torch.isfinite(out).all()
