@@ -216,6 +216,21 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      void* x_perm, void* gate_up_out, void* mid, void* y, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* pmoe_expert_ffn_forward without the workspace arguments. No counterpart in
+ * the reference: it is for callers that cannot allocate memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid allocation). The
+ * permutation's scratch lives in a 256 KiB static device array, one per
+ * device, so T*K <= 2048 * floor(65536 / E) pairs (PMOE_ERR_UNSUPPORTED
+ * beyond; e.g. 1 048 576 pairs at E = 128). Outputs and saved tensors are the
+ * caller's, as for pmoe_expert_ffn_forward. Calls that overlap on one device
+ * share that array and race; calls on different devices do not. */
+PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* top_indices, const void* top_weights,
+                                             int w_dtype, const void* gate_up_proj, const void* down_proj,
+                                             int dtype, int64_t T, int64_t K, int64_t E, int64_t H, int64_t I,
+                                             void* out, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
+                                             int32_t* inv_pos, void* x_perm, void* gate_up_out, void* mid, void* y,
+                                             void* stream);
+
 /* Autograd of pmoe_expert_ffn_forward. Any of grad_hidden, grad_top_weights,
  * grad_gate_up_proj, grad_down_proj may be NULL. grad_weight_dtype is the dtype of
  * the two weight gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master

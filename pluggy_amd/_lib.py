@@ -53,6 +53,8 @@ SIGNATURES = {
     "pmoe_expert_ffn_forward_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_expert_ffn_forward": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                                        _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_expert_ffn_forward_noalloc": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P,
+                                               _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "pmoe_expert_ffn_backward_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _INT]),
     "pmoe_expert_ffn_backward": (_INT, [_P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
                                         _P, _P, _P, _P, _P, _P, _P, _INT, _P, _SZ, _P]),

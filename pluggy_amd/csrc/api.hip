@@ -4,6 +4,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/pmoe.h"
@@ -504,6 +505,67 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
     return rc;
   if (int rc = pmoe_down_proj(mid, down_proj, offs, dtype, P, E, H, I, y, stream)) return rc;
   return pmoe_combine(y, top_weights, w_dtype, inv_pos, dtype, T, K, H, out, stream);
+}
+
+// ---- the whole-FFN forward without a workspace argument
+//
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops, harnesses that forbid allocation): the permutation's chunk
+// histograms, the only scratch memory of pmoe_expert_ffn_forward, live in a
+// file-scope device array of kStaticScratchBytes. Each device holds its own
+// copy until the process ends; its address is looked up once per device, with
+// that device current, on the entry point's first call there. Every call on a
+// device shares the array, so calls that overlap on one device race.
+// Nothing in it has to start at zero: the histogram kernel writes every
+// (chunk, expert) entry before the scan reads it.
+constexpr size_t kStaticScratchBytes = 256 * 1024;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+void* g_scratch_ptr[kMaxScratchDevices];
+hipError_t g_scratch_err[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device (the host-side name is
+// only a stand-in and must never reach a kernel).
+hipError_t static_scratch(void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
+  if (g_scratch_ptr[dev] == nullptr) return hipErrorInvalidSymbol;
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* top_indices, const void* top_weights,
+                                             int w_dtype, const void* gate_up_proj, const void* down_proj,
+                                             int dtype, int64_t T, int64_t K, int64_t E, int64_t H, int64_t I,
+                                             void* out, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
+                                             int32_t* inv_pos, void* x_perm, void* gate_up_out, void* mid, void* y,
+                                             void* stream) {
+  if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
+  const size_t need = pmoe_expert_ffn_forward_workspace_size(T, K, E);
+  if (need > kStaticScratchBytes)
+    return fail(PMOE_ERR_UNSUPPORTED,
+                "expert_ffn_forward_noalloc: T*K = %lld pairs over %lld experts need %zu bytes of scratch; the "
+                "static maximum is %zu (ceil(T*K / %d) * E * 4 bytes)",
+                (long long)(T * K), (long long)E, need, kStaticScratchBytes, kPermuteChunk);
+  void* ws = nullptr;
+  PMOE_TRY(static_scratch(&ws), "expert_ffn_forward_noalloc: static scratch address");
+  return pmoe_expert_ffn_forward(hidden, top_indices, top_weights, w_dtype, gate_up_proj, down_proj, dtype, T, K, E,
+                                 H, I, out, counts, offs, sorted_pair, inv_pos, x_perm, gate_up_out, mid, y, ws,
+                                 kStaticScratchBytes, stream);
 }
 
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype) {

@@ -113,3 +113,14 @@ def test_weight_gradient_dtype_is_checked(lib, entry):
     rc = getattr(lib, entry)(*nulls, _lib.PMOE_F32, P, E, H, I, None, None, _lib.PMOE_BF16, None)
     assert rc == -1 and b"dtype must be the operands' or fp32" in lib.pmoe_last_error_string()
 
+
+
+def test_noalloc_forward_rejects_sizes_beyond_its_static_scratch(lib):
+    """The allocation-free forward refuses, before any HIP call, a pair count
+    whose permutation histograms exceed its 256 KiB static scratch."""
+    from pluggy_amd import _lib
+
+    T, K, E, H, I = 131073, 8, 128, 64, 32  # 513 chunks x 128 experts x 4 bytes > 256 KiB
+    with pytest.raises(RuntimeError, match="static maximum"):
+        _lib.call("pmoe_expert_ffn_forward_noalloc", *([None] * 3), _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
+                  T, K, E, H, I, *([None] * 9), None)
