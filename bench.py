@@ -49,8 +49,10 @@ def parse_args():
     ap.add_argument("--neighbours-only", action="store_true",
                     help="time only the MoE half-block in the trainer's regime and print its JSON object "
                          "(for profiling that regime on its own)")
-    ap.add_argument("--cpu-tokens", type=int, default=512,
+    ap.add_argument("--cpu-tokens", type=int, default=256,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-5 (decode, 64 tokens) forward leg")
     ap.add_argument("--copy-mib", type=int, default=256,
                     help="size of the device-to-device copy timed as the measured HBM reference (0: skip)")
     return ap.parse_args()
@@ -67,8 +69,12 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(cfg, tokens: int | None):
-    """The reference CPU path (router + per-expert loop, autograd backward), restated in oracle/."""
+def cpu_baseline(cfg, tokens: int | None, iters: int = 3):
+    """The reference CPU path (router + per-expert loop, autograd backward), restated in oracle/.
+
+    One warm-up step, then ``iters`` timed steps; the median is reported. The
+    sample is the first ``tokens`` tokens' worth of the workload (a fresh
+    seeded draw of that size, same layer shape)."""
     import torch
 
     from oracle import moe_oracle as O
@@ -86,17 +92,21 @@ def cpu_baseline(cfg, tokens: int | None):
         if cfg.backward:
             y.reshape(T, H).backward(inp["grad_out"])
 
-    t0 = time.perf_counter()
-    step()
-    dt = time.perf_counter() - t0
+    step()  # warm-up
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    dt = statistics.median(times)
     return {
-        "value": T / dt,
+        "value": round(T / dt, 2),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"one {'fwd+bwd' if cfg.backward else 'fwd'} step of the restated reference CPU path "
-                   f"(fp32 router + per-expert loop, moe.py:38-65, torch autograd) at T={T} of the "
-                   f"{cfg.name} layer, {cfg.dtype}, no warm-up; {dt:.2f} s"),
+        "sample": (f"{'fwd+bwd' if cfg.backward else 'fwd'} steps of the restated reference CPU path (fp32 router + "
+                   f"per-expert loop, moe.py:38-65, torch autograd) at T={T} of the {cfg.name} layer, {cfg.dtype}: "
+                   f"1 warm-up + {iters} timed, median {dt:.2f} s (runs {', '.join(f'{t:.2f}' for t in times)} s)"),
         "cpu_model": cpu_model(),
         "os_cpu_count": os.cpu_count(),
         "torch": torch.__version__,
@@ -216,6 +226,58 @@ def neighbours(cfg, inp, steps: int, warmup: int, dev):
     return res
 
 
+def decode_leg(dev, steps: int = 50, warmup: int = 5):
+    """Config 5: a 64-token forward of the config-2
+    layer, where most experts get 0-4 rows and the expert weights stream from
+    HBM. Reports ms per forward and the weight-stream GB/s of the two expert
+    GEMMs (each hit expert's gate_up and down weights read once) against the
+    HBM peak."""
+    import torch
+
+    import pluggy_amd
+    from pluggy_amd.moe import stage_timer
+    from pluggy_amd.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS[5]
+    T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    inp = make_inputs(cfg, device=dev)
+    mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
+    with torch.no_grad():
+        mlp.router.weight.copy_(inp["router_weight"])
+    mlp.experts.gate_up_proj.data = inp["gate_up_proj"]
+    mlp.experts.down_proj.data = inp["down_proj"]
+    x = inp["x"].reshape(1, T, H)
+    with torch.no_grad():
+        for _ in range(warmup):
+            mlp(x)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            mlp(x)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        with stage_timer() as timer:
+            for _ in range(steps):
+                mlp(x)
+            torch.cuda.synchronize()
+    st = timer.summary()
+    hit = int((mlp.router.last_stats.expert_counts > 0).sum().item())
+    es = 2
+    gu_b, dn_b = hit * 2 * I * H * es, hit * H * I * es
+    gemm_ms = st["gate_up_fwd"]["mean_ms"] + st["down_fwd"]["mean_ms"]
+    gbs = (gu_b + dn_b) / (gemm_ms * 1e-3) / 1e9
+    return {"workload": f"{cfg.name} fwd (T={T}, layer as config 2)", "ms_per_forward": round(ms, 4),
+            "tokens/s": round(T / (ms * 1e-3), 1), "experts_hit": hit,
+            "weight_bytes": gu_b + dn_b, "expert_gemms_ms": round(gemm_ms, 4),
+            "weight_stream_GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "gate_up_fwd_GB/s": round(gu_b / (st["gate_up_fwd"]["mean_ms"] * 1e-3) / 1e9, 1),
+            "down_fwd_GB/s": round(dn_b / (st["down_fwd"]["mean_ms"] * 1e-3) / 1e9, 1),
+            "stages_ms": {n: round(v["mean_ms"], 4) for n, v in sorted(st.items(), key=lambda kv: -kv[1]["total_ms"])}}
+
+
 def copy_bandwidth(mib: int, dev, reps: int = 5):
     """HIP-event time of a plain device-to-device copy of `mib` MiB (read + write counted).
 
@@ -275,7 +337,7 @@ def main() -> int:
 
     import pluggy_amd
     from pluggy_amd.moe import stage_timer
-    from pluggy_amd.workloads import CONFIGS, combine_bytes, dispatch_bytes, make_inputs
+    from pluggy_amd.workloads import CONFIGS, combine_bytes, make_inputs
 
     cfg = CONFIGS[args.config]
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
@@ -345,16 +407,20 @@ def main() -> int:
     dom = max(gemm, key=lambda n: gemm[n]["total_ms"])
     # algorithmic FLOPs and HBM bytes per launch of each expert GEMM: every
     # operand read once and every output written once; an expert's weights are
-    # read only when it has rows (the last step's routing counts)
+    # read only when it has rows (the last step's routing counts). The
+    # token-major operands the GEMMs gather (hidden in gate_up fwd / wgrad, the
+    # output gradient in down dgrad / wgrad) count once per token (T*H); each
+    # gathered GEMM also reads its P sorted-row indices (and weights).
     active = int((mlp.router.last_stats.expert_counts > 0).sum().item())
     w_gu, w_dn = active * 2 * I * H * es, active * H * I * es
+    tok = T * H * es
     gemm_work = {
-        "gate_up_fwd": (2.0 * P * H * 2 * I, w_gu + P * H * es + P * 2 * I * es + P * I * es),
+        "gate_up_fwd": (2.0 * P * H * 2 * I, w_gu + tok + P * 8 + P * 2 * I * es + P * I * es),
         "down_fwd": (2.0 * P * I * H, w_dn + P * I * es + P * H * es),
-        "down_dgrad": (2.0 * P * H * I, P * H * es + w_dn + 2 * P * 2 * I * es),
-        "down_wgrad": (2.0 * P * H * I, P * H * es + P * I * es + w_dn),
+        "down_dgrad": (2.0 * P * H * I, tok + P * 8 + w_dn + 2 * P * 2 * I * es + P * ((I + 63) // 64) * 4),
+        "down_wgrad": (2.0 * P * H * I, tok + P * 4 + P * I * es + w_dn),
         "gate_up_dgrad": (2.0 * P * 2 * I * H, P * 2 * I * es + w_gu + P * H * es),
-        "gate_up_wgrad": (2.0 * P * 2 * I * H, P * 2 * I * es + P * H * es + w_gu),
+        "gate_up_wgrad": (2.0 * P * 2 * I * H, P * 2 * I * es + tok + P * 4 + w_gu),
     }
     dom_flops, dom_bytes = gemm_work[dom]
     dom_s = gemm[dom]["mean_ms"] * 1e-3
@@ -368,11 +434,14 @@ def main() -> int:
                 "frac": round(dom_gbs / PEAK_HBM_GBS, 4)}
     bound = "mfma" if intensity >= ridge else "hbm"
     hbm = {}
-    for name, nbytes in (("dispatch", dispatch_bytes(cfg)), ("combine", combine_bytes(cfg)),
+    for name, nbytes in (("combine", combine_bytes(cfg)),
                          # the block's backward hands the router's input gradient to
                          # the dispatch backward as its addend: one more (T, H) read
                          ("dispatch_bwd", P * H * es + P * 4 + 2 * T * H * es),
-                         ("combine_bwd", T * H * es + 2 * P * H * es + P * (4 + 2 * es))):
+                         # x, W (fp32), fp32 logits out, top-k ids / weights out
+                         ("router_fwd", T * H * es + E * H * 4 + T * E * 4 + T * K * (es + 8 + 4)),
+                         # x, W, logits, ids, fp32 weights and their gradient in; dx, dW out
+                         ("router_bwd", 2 * T * H * es + 2 * E * H * 4 + T * E * 4 + T * K * (8 + 4 + 4))):
         if name in stages:
             gbs = nbytes / (stages[name]["mean_ms"] * 1e-3) / 1e9
             hbm[name] = {"bytes": nbytes, "mean_ms": round(stages[name]["mean_ms"], 4), "GB/s": round(gbs, 1),
@@ -419,8 +488,13 @@ def main() -> int:
         ref = reference_gpu(cfg, inp, min(args.steps, 10), 2, dev)
         ref["speedup"] = round(result["value"] / ref["value"], 2)
         result["reference_gpu"] = ref
+    if not args.no_decode and args.config == 2:
+        result["decode"] = decode_leg(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
+        if args.config == 2:
+            # the reference's own CPU-runnable case: fp32 forward, whole workload
+            result["cpu_baseline_config1"] = cpu_baseline(CONFIGS[1], 0)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -106,12 +106,26 @@ PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64
 PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
                            void* x_perm, void* stream);
 
-/* Grouped gate_up GEMM + SwiGLU (moe.py:113-118, swiglu.py:14-16):
- * gate_up_out[p] = x_perm[p] . gate_up_proj[e(p)]^T  (P, 2I), rounded to dtype;
- * mid[p] = silu(gate) * up  (P, I). gate_up_proj: (E, 2I, H). */
-PMOE_API int pmoe_gate_up_swiglu(const void* x_perm, const void* gate_up_proj, const int32_t* offs, int dtype,
-                                 int64_t P, int64_t E, int64_t H, int64_t I, void* gate_up_out, void* mid,
-                                 void* stream);
+/* Per sorted row p of the permutation (pair q = sorted_pair[p]):
+ * sorted_token[p] = q / K, the token whose row the expert GEMMs gather (the
+ * reference's sorted_token, moe.py:90-101), and sorted_w[p] = top_weights[q]
+ * as fp32 (its sorted_w, moe.py:103). top_weights / sorted_w may be NULL
+ * together (no weights). sorted_pair, sorted_token, sorted_w: (T*K,). */
+PMOE_API int pmoe_sort_rows(const int32_t* sorted_pair, const void* top_weights, int w_dtype, int64_t T, int64_t K,
+                            int32_t* sorted_token, float* sorted_w, void* stream);
+
+/* Grouped gate_up GEMM + SwiGLU (moe.py:104, :113-118, :120; swiglu.py:14-16):
+ * with A_p = x[row_index[p]] (the row gather hidden[sorted_token] done inside
+ * the GEMM's operand loads; x holds x_rows rows) or A_p = x[p] when row_index
+ * is NULL (x_rows = P),
+ *   gate_up_out[p] = A_p . gate_up_proj[e(p)]^T  (P, 2I), rounded to dtype;
+ *   mid[p] = row_weight[p] * silu(gate) * up  (P, I)  (row_weight NULL: 1),
+ * i.e. the routing weight of moe.py:120 applied to the activation, so that
+ * the down projection's rows come out weighted. gate_up_proj: (E, 2I, H).
+ * A gathered x must stay below 2 GiB (PMOE_ERR_UNSUPPORTED beyond). */
+PMOE_API int pmoe_gate_up_swiglu(const void* x, const int32_t* row_index, const float* row_weight, int64_t x_rows,
+                                 const void* gate_up_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
+                                 int64_t H, int64_t I, void* gate_up_out, void* mid, void* stream);
 
 /* Grouped down GEMM (moe.py:119): y[p] = mid[p] . down_proj[e(p)]^T  (P, H);
  * down_proj: (E, H, I). y is the unweighted expert output. */
@@ -119,7 +133,8 @@ PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_
                             int64_t E, int64_t H, int64_t I, void* y, void* stream);
 
 /* Weighted combine (moe.py:120-123, in gather form, fp32 accumulation, k ascending):
- * out[t] = sum_k top_weights[t,k] * y[inv_pos[t*K+k]]. */
+ * out[t] = sum_k top_weights[t,k] * y[inv_pos[t*K+k]]; top_weights NULL: unit
+ * weights (rows that already carry their routing weight). */
 PMOE_API int pmoe_combine(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
                           int64_t T, int64_t K, int64_t H, void* out, void* stream);
 
@@ -129,23 +144,44 @@ PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const vo
                                    const int32_t* inv_pos, int dtype, int64_t T, int64_t K, int64_t H,
                                    void* grad_y, void* grad_top_weights, void* stream);
 
-/* Backward of pmoe_down_proj and the SwiGLU: grad_gate_up_out = SwiGLU'(gate_up_out) *
- * (grad_y . down_proj[e]) and grad_down_proj[e] = grad_y_e^T . mid_e (zeros for
- * an empty expert). Either output may be NULL. grad_weight_dtype is grad_down_proj's
- * dtype: `dtype`, or PMOE_F32 with bf16 operands (the gradient of an fp32 master
+/* Backward of pmoe_down_proj and the SwiGLU. G_p = grad[row_index[p]] (grad
+ * holds grad_rows rows: the layer's output gradient, gathered as the
+ * reference's grad of hidden[sorted_token] flows, moe.py:104/123) or
+ * G_p = grad[p] when row_index is NULL (grad_rows = P). acc_p = G_p .
+ * down_proj[e(p)].
+ *   Without row_weight, G is the gradient of y and acc of mid:
+ *     grad_gate_up_out = SwiGLU'(gate_up_out) * acc.
+ *   With row_weight (mid = w * silu(g) * up from pmoe_gate_up_swiglu), acc is
+ *   the gradient of that weighted mid:
+ *     grad_gate_up_out = SwiGLU'(gate_up_out) * (w * acc), and when part is not
+ *     NULL, part[p * part_ld + c] = sum over the 64 columns of block c of
+ *     acc * silu(g) * up (part_ld >= ceil(I / 64)); row p's partials sum to the
+ *     gradient of its routing weight (pmoe_pair_weight_grad).
+ *   grad_down_proj[e] = G_e^T . mid_e (zeros for an empty expert).
+ * Either output may be NULL. grad_weight_dtype is grad_down_proj's dtype:
+ * `dtype`, or PMOE_F32 with bf16 operands (the gradient of an fp32 master
  * weight that the forward cast to bf16, written without a separate cast). */
-PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
+PMOE_API int pmoe_down_proj_backward(const void* grad, const int32_t* row_index, const float* row_weight,
+                                     int64_t grad_rows, const void* mid, const void* gate_up_out,
                                      const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
                                      int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
-                                     int grad_weight_dtype, void* stream);
+                                     int grad_weight_dtype, float* part, int64_t part_ld, void* stream);
 
-/* Backward of the gate_up GEMM: grad_x_perm = grad_gate_up_out . gate_up_proj[e];
- * grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e. Either output may be NULL.
- * grad_weight_dtype is grad_gate_up_proj's dtype, as for pmoe_down_proj_backward. */
-PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
-                                   const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
-                                   void* grad_x_perm, void* grad_gate_up_proj, int grad_weight_dtype,
-                                   void* stream);
+/* Backward of the gate_up GEMM: grad_x_perm = grad_gate_up_out . gate_up_proj[e]
+ * (the sorted rows' input gradient; pmoe_dispatch_backward sums a token's K
+ * rows); grad_gate_up_proj[e] = grad_gate_up_out_e^T . X_e with X_p =
+ * x[row_index[p]] (x holds x_rows rows) or x[p] when row_index is NULL.
+ * Either output may be NULL. grad_weight_dtype as for pmoe_down_proj_backward. */
+PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x, const int32_t* row_index,
+                                   int64_t x_rows, const void* gate_up_proj, const int32_t* offs, int dtype, int64_t P,
+                                   int64_t E, int64_t H, int64_t I, void* grad_x_perm, void* grad_gate_up_proj,
+                                   int grad_weight_dtype, void* stream);
+
+/* Gradient of the routing weights (the autograd of moe.py:120, and of
+ * index_add_'s input there): grad_top_weights[q] = sum_j part[inv_pos[q] *
+ * part_ld + j] over j < nparts (fp32, j ascending), in gw_dtype; q = t*K + k. */
+PMOE_API int pmoe_pair_weight_grad(const float* part, int64_t part_ld, int64_t nparts, const int32_t* inv_pos,
+                                   int64_t T, int64_t K, void* grad_top_weights, int gw_dtype, void* stream);
 
 /* Backward of pmoe_dispatch: grad_hidden[t] = grad_hidden_add[t] + sum_k
  * grad_x_perm[inv_pos[t*K+k]] (fp32 sum, k ascending; grad_hidden_add (T,H)
@@ -202,19 +238,22 @@ PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32
 
 /* ------------------------------------------------------ whole expert FFN ---
  * Replaces moe_expert_ffn / _expert_ffn_grouped (pluggy/kernels/moe.py:68-168):
- * permute, dispatch, gate_up+SwiGLU, down, combine. The saved tensors
- * (counts, offs, sorted_pair, inv_pos, x_perm, gate_up_out, mid, y) are
- * caller-owned outputs that pmoe_expert_ffn_backward consumes.
+ * permute, sort_rows, gate_up+SwiGLU over the gathered hidden rows with the
+ * routing weight in the activation, down, and an unweighted combine. The
+ * expert-sorted copy of hidden (moe.py:104) is never materialised. The saved
+ * tensors (counts, offs, sorted_pair, inv_pos, sorted_token, sorted_w,
+ * gate_up_out, mid) are caller-owned outputs that pmoe_expert_ffn_backward
+ * consumes; y (P, H), the weighted expert rows, is only needed by the combine.
  * hidden (T,H), top_indices (T,K) int64, top_weights (T,K) w_dtype,
- * gate_up_proj (E,2I,H), down_proj (E,H,I), out (T,H); all but the
- * weights/indices in `dtype`. */
+ * gate_up_proj (E,2I,H), down_proj (E,H,I), out (T,H); sorted_token (P,)
+ * int32; sorted_w (P,) fp32; gate_up_out (P,2I), mid (P,I), y (P,H) dtype. */
 PMOE_API size_t pmoe_expert_ffn_forward_workspace_size(int64_t T, int64_t K, int64_t E);
 PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indices, const void* top_weights,
                                      int w_dtype, const void* gate_up_proj, const void* down_proj, int dtype,
                                      int64_t T, int64_t K, int64_t E, int64_t H, int64_t I, void* out,
                                      int32_t* counts, int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos,
-                                     void* x_perm, void* gate_up_out, void* mid, void* y, void* workspace,
-                                     size_t workspace_bytes, void* stream);
+                                     int32_t* sorted_token, float* sorted_w, void* gate_up_out, void* mid, void* y,
+                                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* pmoe_expert_ffn_forward without the workspace arguments. No counterpart in
  * the reference: it is for callers that cannot allocate memory (code under HIP
@@ -228,22 +267,23 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
                                              int w_dtype, const void* gate_up_proj, const void* down_proj,
                                              int dtype, int64_t T, int64_t K, int64_t E, int64_t H, int64_t I,
                                              void* out, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
-                                             int32_t* inv_pos, void* x_perm, void* gate_up_out, void* mid, void* y,
-                                             void* stream);
+                                             int32_t* inv_pos, int32_t* sorted_token, float* sorted_w,
+                                             void* gate_up_out, void* mid, void* y, void* stream);
 
-/* Autograd of pmoe_expert_ffn_forward. Any of grad_hidden, grad_top_weights,
- * grad_gate_up_proj, grad_down_proj may be NULL. grad_weight_dtype is the dtype of
- * the two weight gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master
- * weights). Workspace holds grad_y, grad_gate_up_out and grad_x_perm. */
+/* Autograd of pmoe_expert_ffn_forward from grad_out (T,H) dtype. Any of
+ * grad_hidden, grad_top_weights (T,K) w_dtype, grad_gate_up_proj,
+ * grad_down_proj may be NULL. grad_weight_dtype is the dtype of the two weight
+ * gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master weights).
+ * Workspace holds grad_gate_up_out, the sorted rows' input gradient and the
+ * routing-weight partials. */
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype);
-PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weights, int w_dtype,
-                                      const void* gate_up_proj, const void* down_proj, int dtype, int64_t T,
-                                      int64_t K, int64_t E, int64_t H, int64_t I, const int32_t* offs,
-                                      const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
-                                      const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
-                                      void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
-                                      int grad_weight_dtype, void* workspace, size_t workspace_bytes,
-                                      void* stream);
+PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, int w_dtype, const void* gate_up_proj,
+                                      const void* down_proj, int dtype, int64_t T, int64_t K, int64_t E, int64_t H,
+                                      int64_t I, const int32_t* offs, const int32_t* inv_pos,
+                                      const int32_t* sorted_token, const float* sorted_w, const void* gate_up_out,
+                                      const void* mid, void* grad_hidden, void* grad_top_weights,
+                                      void* grad_gate_up_proj, void* grad_down_proj, int grad_weight_dtype,
+                                      void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,12 +37,15 @@ SIGNATURES = {
     "pmoe_permute": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P]),
     "pmoe_count_invalid_ids": (_INT, [_P, _I64, _I64, _P, _P]),
     "pmoe_dispatch": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P]),
-    "pmoe_gate_up_swiglu": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "pmoe_sort_rows": (_INT, [_P, _P, _INT, _I64, _I64, _P, _P, _P]),
+    "pmoe_gate_up_swiglu": (_INT, [_P, _P, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_down_proj": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P]),
     "pmoe_combine": (_INT, [_P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),
     "pmoe_combine_backward": (_INT, [_P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P]),
-    "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _INT, _P]),
-    "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _INT, _P]),
+    "pmoe_down_proj_backward": (_INT, [_P, _P, _P, _I64, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P,
+                                       _INT, _P, _I64, _P]),
+    "pmoe_gate_up_backward": (_INT, [_P, _P, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _INT, _P]),
+    "pmoe_pair_weight_grad": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _INT, _P]),
     "pmoe_dispatch_backward": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P]),
     "pmoe_rmsnorm_forward": (_INT, [_P, _INT, _P, _F32, _I64, _I64, _P, _INT, _P, _P]),
     "pmoe_combine_residual": (_INT, [_P, _P, _INT, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),
@@ -52,12 +55,12 @@ SIGNATURES = {
                                               _INT, _P, _SZ, _P]),
     "pmoe_expert_ffn_forward_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "pmoe_expert_ffn_forward": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
-                                       _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+                                       _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "pmoe_expert_ffn_forward_noalloc": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P,
-                                               _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                               _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "pmoe_expert_ffn_backward_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _INT]),
     "pmoe_expert_ffn_backward": (_INT, [_P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
-                                        _P, _P, _P, _P, _P, _P, _P, _INT, _P, _SZ, _P]),
+                                        _P, _P, _P, _P, _P, _P, _INT, _P, _SZ, _P]),
 }
 
 _lock = threading.Lock()

@@ -330,20 +330,76 @@ PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_
 
 // ------------------------------------------------------------ expert GEMMs
 
-PMOE_API int pmoe_gate_up_swiglu(const void* x_perm, const void* gate_up_proj, const int32_t* offs, int dtype,
-                                 int64_t P, int64_t E, int64_t H, int64_t I, void* gate_up_out, void* mid,
-                                 void* stream) {
+extern "C++" {
+namespace {
+
+// A gathered operand is addressed through one buffer descriptor, whose byte
+// offsets are 32-bit: its storage must stay below 2 GiB.
+int check_gather(const int32_t* index, int64_t rows, int64_t cols, int dtype, int64_t P, const char* what) {
+  if (index == nullptr) {
+    PMOE_REQUIRE(rows == P, "%s: without a row index the operand has the P = %lld sorted rows (got %lld)", what,
+                 (long long)P, (long long)rows);
+    return PMOE_OK;
+  }
+  PMOE_REQUIRE(rows > 0, "%s: a gathered operand needs rows > 0", what);
+  const int64_t bytes = rows * cols * (dtype == PMOE_BF16 ? 2 : 4);
+  if (bytes >= ((int64_t)1 << 31) - 16)
+    return fail(PMOE_ERR_UNSUPPORTED, "%s: gathered operand of %lld bytes exceeds the 2 GiB a descriptor addresses",
+                what, (long long)bytes);
+  return PMOE_OK;
+}
+
+template <typename T, typename Tw>
+hipError_t run_expert(int kind, const void* A, const void* B, const void* aux, void* C, void* C2, void* Cw,
+                      const int32_t* offs, int64_t P, int64_t E, int64_t H, int64_t I, const ExpertGather& xg,
+                      hipStream_t s) {
+  return expert_gemm_run<T, Tw>(kind, (const T*)A, (const T*)B, (const T*)aux, (T*)C, (T*)C2, (Tw*)Cw, offs, (int)P,
+                                (int)E, (int)H, (int)I, xg, s);
+}
+
+// dtype: the operands'; wdt: the weight gradient's (wgrad kinds).
+hipError_t dispatch_expert(int kind, int dtype, int wdt, const void* A, const void* B, const void* aux, void* C,
+                           void* C2, void* Cw, const int32_t* offs, int64_t P, int64_t E, int64_t H, int64_t I,
+                           const ExpertGather& xg, hipStream_t s) {
+  if (dtype == PMOE_F32) return run_expert<float, float>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+  if (wdt == PMOE_F32) return run_expert<bf16_t, float>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+  return run_expert<bf16_t, bf16_t>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+}
+
+}  // namespace
+}  // extern "C++"
+
+PMOE_API int pmoe_sort_rows(const int32_t* sorted_pair, const void* top_weights, int w_dtype, int64_t T, int64_t K,
+                            int32_t* sorted_token, float* sorted_w, void* stream) {
+  PMOE_REQUIRE(T >= 0 && K > 0 && T * K <= kMaxIndex, "sort_rows: bad sizes");
+  PMOE_REQUIRE(dtype_ok(w_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(sorted_pair && sorted_token && (sorted_w == nullptr || top_weights), "sort_rows: null tensor");
+  const int P = (int)(T * K);
+  hipError_t st = w_dtype == PMOE_BF16
+                      ? sort_rows<bf16_t>(sorted_pair, (const bf16_t*)top_weights, P, (int)K, sorted_token, sorted_w,
+                                          as_stream(stream))
+                      : sort_rows<float>(sorted_pair, (const float*)top_weights, P, (int)K, sorted_token, sorted_w,
+                                         as_stream(stream));
+  return hip_status(st, "sort_rows");
+}
+
+PMOE_API int pmoe_gate_up_swiglu(const void* x, const int32_t* row_index, const float* row_weight, int64_t x_rows,
+                                 const void* gate_up_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
+                                 int64_t H, int64_t I, void* gate_up_out, void* mid, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_swiglu: bad dtype or I");
+  if (int rc = check_gather(row_index, x_rows, H, dtype, P, "gate_up_swiglu")) return rc;
   if (P == 0) return PMOE_OK;
-  PMOE_REQUIRE(x_perm && gate_up_proj && offs && gate_up_out && mid, "gate_up_swiglu: null tensor");
-  hipStream_t s = as_stream(stream);
-  hipError_t st = dtype == PMOE_BF16
-                      ? gate_up_swiglu_fwd<bf16_t>((const bf16_t*)x_perm, (const bf16_t*)gate_up_proj, offs, (int)P,
-                                                   (int)E, (int)H, (int)I, (bf16_t*)gate_up_out, (bf16_t*)mid, s)
-                      : gate_up_swiglu_fwd<float>((const float*)x_perm, (const float*)gate_up_proj, offs, (int)P,
-                                                  (int)E, (int)H, (int)I, (float*)gate_up_out, (float*)mid, s);
-  return hip_status(st, "gate_up_swiglu");
+  PMOE_REQUIRE(x && gate_up_proj && offs && gate_up_out && mid, "gate_up_swiglu: null tensor");
+  ExpertGather xg;
+  xg.index = row_index;
+  xg.rows = x_rows;
+  xg.row_w = row_weight;
+  PMOE_TRY(dispatch_expert(EG_GATE_UP_FWD, dtype, dtype, x, gate_up_proj, nullptr, gate_up_out, mid, nullptr, offs, P,
+                           E, H, I, xg, as_stream(stream)),
+           "gate_up_swiglu");
+  return PMOE_OK;
 }
 
 PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_t* offs, int dtype, int64_t P,
@@ -352,81 +408,93 @@ PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj: bad dtype or I");
   if (P == 0) return PMOE_OK;
   PMOE_REQUIRE(mid && down_proj && offs && y, "down_proj: null tensor");
-  hipStream_t s = as_stream(stream);
-  hipError_t st = dtype == PMOE_BF16 ? down_fwd<bf16_t>((const bf16_t*)mid, (const bf16_t*)down_proj, offs, (int)P,
-                                                        (int)E, (int)H, (int)I, (bf16_t*)y, s)
-                                     : down_fwd<float>((const float*)mid, (const float*)down_proj, offs, (int)P,
-                                                       (int)E, (int)H, (int)I, (float*)y, s);
-  return hip_status(st, "down_proj");
+  PMOE_TRY(dispatch_expert(EG_DOWN_FWD, dtype, dtype, mid, down_proj, nullptr, y, nullptr, nullptr, offs, P, E, H, I,
+                           ExpertGather(), as_stream(stream)),
+           "down_proj");
+  return PMOE_OK;
 }
 
-PMOE_API int pmoe_down_proj_backward(const void* grad_y, const void* mid, const void* gate_up_out,
+PMOE_API int pmoe_down_proj_backward(const void* grad, const int32_t* row_index, const float* row_weight,
+                                     int64_t grad_rows, const void* mid, const void* gate_up_out,
                                      const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
                                      int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
-                                     int grad_weight_dtype, void* stream) {
+                                     int grad_weight_dtype, float* part, int64_t part_ld, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj_backward: bad dtype or I");
   PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
                "down_proj_backward: grad_down_proj dtype must be the operands' or fp32");
-  PMOE_REQUIRE(offs && (P == 0 || grad_y), "down_proj_backward: null tensor");
+  if (int rc = check_gather(row_index, grad_rows, H, dtype, P, "down_proj_backward")) return rc;
+  PMOE_REQUIRE(part == nullptr || (row_weight != nullptr && part_ld >= (I + 63) / 64),
+               "down_proj_backward: routing-weight partials need row_weight and part_ld >= ceil(I / 64)");
+  PMOE_REQUIRE(offs && (P == 0 || grad), "down_proj_backward: null tensor");
   hipStream_t s = as_stream(stream);
-  const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
+  ExpertGather xg;
+  xg.index = row_index;
+  xg.rows = grad_rows;
   if (grad_gate_up_out && P > 0) {
     PMOE_REQUIRE(down_proj && gate_up_out, "down_proj_backward: null tensor");
-    hipError_t st =
-        dtype == PMOE_BF16
-            ? down_dgrad_swiglu_bwd<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)down_proj,
-                                            (const bf16_t*)gate_up_out, offs, p, e, h, i, (bf16_t*)grad_gate_up_out, s)
-            : down_dgrad_swiglu_bwd<float>((const float*)grad_y, (const float*)down_proj, (const float*)gate_up_out,
-                                           offs, p, e, h, i, (float*)grad_gate_up_out, s);
-    PMOE_TRY(st, "down dgrad");
+    ExpertGather xd = xg;
+    xd.row_w = row_weight;
+    xd.part = part;
+    xd.part_ld = (int)part_ld;
+    PMOE_TRY(dispatch_expert(EG_DOWN_DGRAD, dtype, dtype, grad, down_proj, gate_up_out, grad_gate_up_out, nullptr,
+                             nullptr, offs, P, E, H, I, xd, s),
+             "down dgrad");
+  } else {
+    PMOE_REQUIRE(part == nullptr, "down_proj_backward: routing-weight partials come with grad_gate_up_out");
   }
   if (grad_down_proj) {
     PMOE_REQUIRE(P == 0 || mid, "down_proj_backward: null mid");
-    hipError_t st =
-        dtype == PMOE_F32
-            ? down_wgrad<float>((const float*)grad_y, (const float*)mid, offs, p, e, h, i, (float*)grad_down_proj, s)
-        : grad_weight_dtype == PMOE_F32
-            ? down_wgrad_f32((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h, i, (float*)grad_down_proj, s)
-            : down_wgrad<bf16_t>((const bf16_t*)grad_y, (const bf16_t*)mid, offs, p, e, h, i,
-                                 (bf16_t*)grad_down_proj, s);
-    PMOE_TRY(st, "down wgrad");
+    PMOE_TRY(dispatch_expert(EG_DOWN_WGRAD, dtype, grad_weight_dtype, grad, mid, nullptr, nullptr, nullptr,
+                             grad_down_proj, offs, P, E, H, I, xg, s),
+             "down wgrad");
   }
   return PMOE_OK;
 }
 
-PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x_perm, const void* gate_up_proj,
-                                   const int32_t* offs, int dtype, int64_t P, int64_t E, int64_t H, int64_t I,
-                                   void* grad_x_perm, void* grad_gate_up_proj, int grad_weight_dtype,
-                                   void* stream) {
+PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x, const int32_t* row_index,
+                                   int64_t x_rows, const void* gate_up_proj, const int32_t* offs, int dtype, int64_t P,
+                                   int64_t E, int64_t H, int64_t I, void* grad_x_perm, void* grad_gate_up_proj,
+                                   int grad_weight_dtype, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_backward: bad dtype or I");
   PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
                "gate_up_backward: grad_gate_up_proj dtype must be the operands' or fp32");
+  if (int rc = check_gather(row_index, x_rows, H, dtype, P, "gate_up_backward")) return rc;
   PMOE_REQUIRE(offs && (P == 0 || grad_gate_up_out), "gate_up_backward: null tensor");
   hipStream_t s = as_stream(stream);
-  const int p = (int)P, e = (int)E, h = (int)H, i = (int)I;
   if (grad_x_perm && P > 0) {
     PMOE_REQUIRE(gate_up_proj, "gate_up_backward: null weight");
-    hipError_t st = dtype == PMOE_BF16
-                        ? gate_up_dgrad<bf16_t>((const bf16_t*)grad_gate_up_out, (const bf16_t*)gate_up_proj, offs, p,
-                                                e, h, i, (bf16_t*)grad_x_perm, s)
-                        : gate_up_dgrad<float>((const float*)grad_gate_up_out, (const float*)gate_up_proj, offs, p, e,
-                                               h, i, (float*)grad_x_perm, s);
-    PMOE_TRY(st, "gate_up dgrad");
+    PMOE_TRY(dispatch_expert(EG_GATE_UP_DGRAD, dtype, dtype, grad_gate_up_out, gate_up_proj, nullptr, grad_x_perm,
+                             nullptr, nullptr, offs, P, E, H, I, ExpertGather(), s),
+             "gate_up dgrad");
   }
   if (grad_gate_up_proj) {
-    PMOE_REQUIRE(P == 0 || x_perm, "gate_up_backward: null x_perm");
-    const bf16_t* gb = (const bf16_t*)grad_gate_up_out;
-    const bf16_t* xb = (const bf16_t*)x_perm;
-    hipError_t st = dtype == PMOE_F32 ? gate_up_wgrad<float>((const float*)grad_gate_up_out, (const float*)x_perm,
-                                                             offs, p, e, h, i, (float*)grad_gate_up_proj, s)
-                    : grad_weight_dtype == PMOE_F32
-                        ? gate_up_wgrad_f32(gb, xb, offs, p, e, h, i, (float*)grad_gate_up_proj, s)
-                        : gate_up_wgrad<bf16_t>(gb, xb, offs, p, e, h, i, (bf16_t*)grad_gate_up_proj, s);
-    PMOE_TRY(st, "gate_up wgrad");
+    PMOE_REQUIRE(P == 0 || x, "gate_up_backward: null x");
+    ExpertGather xg;
+    xg.index = row_index;
+    xg.rows = x_rows;
+    PMOE_TRY(dispatch_expert(EG_GATE_UP_WGRAD, dtype, grad_weight_dtype, grad_gate_up_out, x, nullptr, nullptr,
+                             nullptr, grad_gate_up_proj, offs, P, E, H, I, xg, s),
+             "gate_up wgrad");
   }
   return PMOE_OK;
+}
+
+PMOE_API int pmoe_pair_weight_grad(const float* part, int64_t part_ld, int64_t nparts, const int32_t* inv_pos,
+                                   int64_t T, int64_t K, void* grad_top_weights, int gw_dtype, void* stream) {
+  PMOE_REQUIRE(T >= 0 && K > 0 && T * K <= kMaxIndex && nparts >= 0 && part_ld >= nparts && part_ld < (1 << 20),
+               "pair_weight_grad: bad sizes");
+  PMOE_REQUIRE(dtype_ok(gw_dtype), "unknown dtype code");
+  if (T == 0) return PMOE_OK;
+  PMOE_REQUIRE(part && inv_pos && grad_top_weights, "pair_weight_grad: null tensor");
+  const int P = (int)(T * K);
+  hipError_t st = gw_dtype == PMOE_BF16
+                      ? pair_weight_grad<bf16_t>(part, (int)part_ld, (int)nparts, inv_pos, P, (bf16_t*)grad_top_weights,
+                                                 as_stream(stream))
+                      : pair_weight_grad<float>(part, (int)part_ld, (int)nparts, inv_pos, P, (float*)grad_top_weights,
+                                                as_stream(stream));
+  return hip_status(st, "pair_weight_grad");
 }
 
 // ---------------------------------------------------------------- combine
@@ -436,7 +504,7 @@ PMOE_API int pmoe_combine(const void* y, const void* top_weights, int w_dtype, c
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
-  PMOE_REQUIRE(y && top_weights && inv_pos && out, "combine: null tensor");
+  PMOE_REQUIRE(y && inv_pos && out, "combine: null tensor");  // top_weights NULL: unit weights
   hipStream_t s = as_stream(stream);
   const int t = (int)T, k = (int)K, h = (int)H;
   hipError_t st;
@@ -491,20 +559,21 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      int w_dtype, const void* gate_up_proj, const void* down_proj, int dtype,
                                      int64_t T, int64_t K, int64_t E, int64_t H, int64_t I, void* out,
                                      int32_t* counts, int32_t* offs, int32_t* sorted_pair, int32_t* inv_pos,
-                                     void* x_perm, void* gate_up_out, void* mid, void* y, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+                                     int32_t* sorted_token, float* sorted_w, void* gate_up_out, void* mid, void* y,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
-  PMOE_REQUIRE(I > 0, "expert_ffn_forward: I must be positive");
+  PMOE_REQUIRE(I > 0 && dtype_ok(dtype) && dtype_ok(w_dtype), "expert_ffn_forward: bad dtype or I");
   if (int rc = pmoe_permute(top_indices, T, K, E, counts, offs, sorted_pair, inv_pos, workspace, workspace_bytes,
                             stream))
     return rc;
   if (T == 0) return PMOE_OK;
   const int64_t P = T * K;
-  if (int rc = pmoe_dispatch(hidden, dtype, inv_pos, T, K, H, x_perm, stream)) return rc;
-  if (int rc = pmoe_gate_up_swiglu(x_perm, gate_up_proj, offs, dtype, P, E, H, I, gate_up_out, mid, stream))
+  if (int rc = pmoe_sort_rows(sorted_pair, top_weights, w_dtype, T, K, sorted_token, sorted_w, stream)) return rc;
+  if (int rc = pmoe_gate_up_swiglu(hidden, sorted_token, sorted_w, T, gate_up_proj, offs, dtype, P, E, H, I,
+                                   gate_up_out, mid, stream))
     return rc;
   if (int rc = pmoe_down_proj(mid, down_proj, offs, dtype, P, E, H, I, y, stream)) return rc;
-  return pmoe_combine(y, top_weights, w_dtype, inv_pos, dtype, T, K, H, out, stream);
+  return pmoe_combine(y, nullptr, w_dtype, inv_pos, dtype, T, K, H, out, stream);
 }
 
 // ---- the whole-FFN forward without a workspace argument
@@ -552,8 +621,8 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
                                              int w_dtype, const void* gate_up_proj, const void* down_proj,
                                              int dtype, int64_t T, int64_t K, int64_t E, int64_t H, int64_t I,
                                              void* out, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
-                                             int32_t* inv_pos, void* x_perm, void* gate_up_out, void* mid, void* y,
-                                             void* stream) {
+                                             int32_t* inv_pos, int32_t* sorted_token, float* sorted_w,
+                                             void* gate_up_out, void* mid, void* y, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
   const size_t need = pmoe_expert_ffn_forward_workspace_size(T, K, E);
   if (need > kStaticScratchBytes)
@@ -564,64 +633,68 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
   void* ws = nullptr;
   PMOE_TRY(static_scratch(&ws), "expert_ffn_forward_noalloc: static scratch address");
   return pmoe_expert_ffn_forward(hidden, top_indices, top_weights, w_dtype, gate_up_proj, down_proj, dtype, T, K, E,
-                                 H, I, out, counts, offs, sorted_pair, inv_pos, x_perm, gate_up_out, mid, y, ws,
-                                 kStaticScratchBytes, stream);
+                                 H, I, out, counts, offs, sorted_pair, inv_pos, sorted_token, sorted_w, gate_up_out,
+                                 mid, y, ws, kStaticScratchBytes, stream);
 }
 
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype) {
   const size_t es = dtype == PMOE_BF16 ? 2 : 4;
   const int64_t P = T * K;
-  return align_up((size_t)P * H * es) + align_up((size_t)P * 2 * I * es);
+  return align_up((size_t)P * 2 * I * es) + align_up((size_t)P * H * es) +
+         align_up((size_t)P * ((I + 63) / 64) * sizeof(float));
 }
 
-PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* top_weights, int w_dtype,
-                                      const void* gate_up_proj, const void* down_proj, int dtype, int64_t T,
-                                      int64_t K, int64_t E, int64_t H, int64_t I, const int32_t* offs,
-                                      const int32_t* sorted_pair, const int32_t* inv_pos, const void* x_perm,
-                                      const void* gate_up_out, const void* mid, const void* y, void* grad_hidden,
-                                      void* grad_top_weights, void* grad_gate_up_proj, void* grad_down_proj,
-                                      int grad_weight_dtype, void* workspace, size_t workspace_bytes,
-                                      void* stream) {
+PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, int w_dtype, const void* gate_up_proj,
+                                      const void* down_proj, int dtype, int64_t T, int64_t K, int64_t E, int64_t H,
+                                      int64_t I, const int32_t* offs, const int32_t* inv_pos,
+                                      const int32_t* sorted_token, const float* sorted_w, const void* gate_up_out,
+                                      const void* mid, void* grad_hidden, void* grad_top_weights,
+                                      void* grad_gate_up_proj, void* grad_down_proj, int grad_weight_dtype,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
   PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
                "expert_ffn_backward: weight gradient dtype must be the operands' or fp32");
-  (void)sorted_pair;
   const size_t need = pmoe_expert_ffn_backward_workspace_size(T, K, H, I, dtype);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(PMOE_ERR_WORKSPACE, "expert_ffn_backward: workspace %zu < %zu bytes", workspace_bytes, need);
   const int64_t P = T * K;
   const size_t es = dtype == PMOE_BF16 ? 2 : 4;
-  Carver cv(workspace);
-  char* grad_y = cv.take<char>((size_t)P * H * es);
-  char* grad_gu = cv.take<char>((size_t)P * 2 * I * es);
-  hipStream_t s = as_stream(stream);
-  if (T == 0) {
-    const size_t gs = grad_weight_dtype == PMOE_BF16 ? 2 : 4;
-    if (grad_gate_up_proj) PMOE_TRY(hipMemsetAsync(grad_gate_up_proj, 0, (size_t)E * 2 * I * H * gs, s), "zero");
-    if (grad_down_proj) PMOE_TRY(hipMemsetAsync(grad_down_proj, 0, (size_t)E * H * I * gs, s), "zero");
-    return PMOE_OK;
+  Carver c(workspace);
+  void* g_gu = c.take<char>((size_t)P * 2 * I * es);
+  void* g_xp = c.take<char>((size_t)P * H * es);
+  const int64_t part_ld = (I + 63) / 64;
+  float* part = c.take<float>((size_t)P * part_ld);
+  const bool need_rows = grad_hidden != nullptr;
+  const bool need_tw = grad_top_weights != nullptr;
+  const bool need_dgu = need_rows || need_tw || grad_gate_up_proj != nullptr;
+  if (T > 0 && need_dgu) {
+    if (int rc = pmoe_down_proj_backward(grad_out, sorted_token, sorted_w, T, mid, gate_up_out, down_proj, offs, dtype,
+                                         P, E, H, I, g_gu, nullptr, grad_weight_dtype, need_tw ? part : nullptr,
+                                         part_ld, stream))
+      return rc;
   }
-  // 1. combine backward: grad_y and grad_top_weights. grad_y is needed for any
-  //    other output; grad_top_weights goes to a scratch slot when not requested.
-  void* gtw = grad_top_weights;
-  if (!gtw) gtw = grad_gu;  // grad_gu is written later; P weights fit in P*2I elements
-  if (int rc = pmoe_combine_backward(grad_out, y, top_weights, w_dtype, inv_pos, dtype, T, K, H, grad_y, gtw, stream))
-    return rc;
-  // 2. down GEMM backward (dgrad fused with SwiGLU backward, then wgrad)
-  void* ggu = (grad_hidden || grad_gate_up_proj) ? grad_gu : nullptr;
-  if (int rc = pmoe_down_proj_backward(grad_y, mid, gate_up_out, down_proj, offs, dtype, P, E, H, I, ggu,
-                                       grad_down_proj, grad_weight_dtype, stream))
-    return rc;
-  // 3. gate_up GEMM backward; grad_x_perm reuses grad_y (consumed above, same stream)
-  void* gxp = grad_hidden ? grad_y : nullptr;
-  if (ggu) {
-    if (int rc = pmoe_gate_up_backward(grad_gu, x_perm, gate_up_proj, offs, dtype, P, E, H, I, gxp,
+  if (need_tw && T > 0) {
+    if (int rc = pmoe_pair_weight_grad(part, part_ld, part_ld, inv_pos, T, K, grad_top_weights, w_dtype, stream))
+      return rc;
+  }
+  if (need_rows) {
+    if (int rc = pmoe_gate_up_backward(g_gu, hidden, sorted_token, T, gate_up_proj, offs, dtype, P, E, H, I, g_xp,
+                                       nullptr, grad_weight_dtype, stream))
+      return rc;
+    if (int rc = pmoe_dispatch_backward(g_xp, inv_pos, nullptr, dtype, T, K, H, grad_hidden, stream)) return rc;
+  }
+  if (grad_gate_up_proj) {
+    if (int rc = pmoe_gate_up_backward(g_gu, hidden, sorted_token, T, gate_up_proj, offs, dtype, P, E, H, I, nullptr,
                                        grad_gate_up_proj, grad_weight_dtype, stream))
       return rc;
   }
-  // 4. dispatch backward
-  if (grad_hidden) return pmoe_dispatch_backward(grad_y, inv_pos, nullptr, dtype, T, K, H, grad_hidden, stream);
+  if (grad_down_proj) {
+    if (int rc = pmoe_down_proj_backward(grad_out, sorted_token, sorted_w, T, mid, gate_up_out, down_proj, offs,
+                                         dtype, P, E, H, I, nullptr, grad_down_proj, grad_weight_dtype, nullptr, 0,
+                                         stream))
+      return rc;
+  }
   return PMOE_OK;
 }
 
@@ -651,7 +724,7 @@ PMOE_API int pmoe_combine_residual(const void* y, const void* top_weights, int w
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
   PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
-  PMOE_REQUIRE(y && top_weights && inv_pos && residual && out, "combine_residual: null tensor");
+  PMOE_REQUIRE(y && inv_pos && residual && out, "combine_residual: null tensor");  // top_weights NULL: unit weights
   hipError_t st = by_dtype(dtype, [&](auto yp) {
     return by_dtype(w_dtype, [&](auto wp) {
       return by_dtype(res_dtype, [&](auto rp) {

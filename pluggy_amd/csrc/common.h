@@ -15,6 +15,32 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// The six grouped GEMMs of the expert FFN (forward, dgrad, wgrad of gate_up and down).
+enum ExpertGemm {
+  EG_GATE_UP_FWD = 0,  // gu, mid <- x_perm . W_gu[e]^T, SwiGLU epilogue
+  EG_DOWN_FWD = 1,     // y <- mid . W_dn[e]^T
+  EG_DOWN_DGRAD = 2,   // dgu <- SwiGLU'(gu) * (dy . W_dn[e])
+  EG_DOWN_WGRAD = 3,   // dW_dn[e] <- dy_e^T . mid_e
+  EG_GATE_UP_DGRAD = 4,  // dx_perm <- dgu . W_gu[e]
+  EG_GATE_UP_WGRAD = 5,  // dW_gu[e] <- dgu_e^T . x_perm_e
+};
+
+// The token-major side of an expert GEMM, when its expert-sorted rows are
+// gathered instead of materialised: the sorted row p of the operand that
+// holds tokens (x in EG_GATE_UP_FWD / EG_GATE_UP_WGRAD, the output gradient in
+// EG_DOWN_DGRAD / EG_DOWN_WGRAD) is row index[p] of a (rows, .) tensor.
+// row_w / part: the routing weight of each sorted row and the partials of its
+// gradient (EG_GATE_UP_FWD scales mid by row_w; EG_DOWN_DGRAD takes the
+// gradient of the scaled mid and writes the partials).
+struct ExpertGather {
+  const int32_t* index = nullptr;
+  int64_t rows = 0;
+  const float* row_w = nullptr;
+  float* part = nullptr;
+  int part_ld = 0;
+};
+
+
 // ---------------------------------------------------------------- bf16 ----
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t h) {

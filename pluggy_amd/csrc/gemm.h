@@ -200,10 +200,12 @@ struct TransStager {
   const Tg* base;
   int64_t ld;
   int r0, r_hi;
+  const int32_t* kidx;  // k-row k is row kidx[k] of base (nullptr: row k)
   u32x4 reg[PER_T][VEC];
 
-  __device__ __forceinline__ void init(const Tg* base_, int64_t ld_, int r0_, int r_hi_) {
-    base = base_; ld = ld_; r0 = r0_; r_hi = r_hi_;
+  __device__ __forceinline__ void init(const Tg* base_, int64_t ld_, int r0_, int r_hi_,
+                                       const int32_t* kidx_ = nullptr) {
+    base = base_; ld = ld_; r0 = r0_; r_hi = r_hi_; kidx = kidx_;
   }
   __device__ __forceinline__ void load(int k0, int k_hi, int tid) {
 #pragma unroll
@@ -217,7 +219,7 @@ struct TransStager {
         int k = k0 + kb * VEC + j;
         u32x4 v = {0u, 0u, 0u, 0u};
         if (ok_r && k < k_hi) {
-          const Tg* src = base + (int64_t)k * ld + r;
+          const Tg* src = base + (int64_t)(kidx != nullptr ? kidx[k] : k) * ld + r;
           if (r + VEC <= r_hi) v = *reinterpret_cast<const u32x4*>(src);
           else v = load_partial16(src, r_hi - r);
         }
@@ -254,6 +256,20 @@ struct GemmParams {
   uint64_t b_bytes;
   int planes;           // GM_RED uniform split: groups = planes * splits, plane g / splits reads A + plane * strideA
   int64_t strideA;
+  // Row gathers of a token-major operand (the expert-sorted rows are never
+  // materialised): with a_index, row p of A (GM_ROWS) or k-row p of A (GM_RED)
+  // is row a_index[p] of A's storage, which holds a_rows rows; b_index / b_rows
+  // likewise for the k-rows of B (GM_RED). a_index / b_index hold P entries.
+  const int32_t* a_index; int64_t a_rows;
+  const int32_t* b_index; int64_t b_rows;
+  int64_t n_index;      // entries of a_index / b_index (P)
+  // Epilogue extras. row_w[p]: the routing weight of output row p; EPI_SWIGLU
+  // writes mid = row_w * silu(g) * u, EPI_SWIGLU_BWD takes the accumulators as
+  // the gradient of that scaled activation. part: with EPI_SWIGLU_BWD and
+  // row_w, part[p * part_ld + c / 64] = sum over the 64 columns c.. of the
+  // accumulators times silu(g) * u (the routing weight's gradient, by block).
+  const float* row_w;
+  float* part; int part_ld;
 };
 
 struct TileInfo {
@@ -337,11 +353,12 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Cfg::MI][Cfg::NI]
         const int row = row_base + r, col = col_base + c;
         if (row < ti.m_end && col < p.inter) {
           float g[8], u[8], m[8];
+          const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;
 #pragma unroll
           for (int t = 0; t < 8; ++t) {
             g[t] = round_to<Tout>(stage[r * Cfg::EPI_LD + c + t]);
             u[t] = round_to<Tout>(stage[r * Cfg::EPI_LD + H2 + c + t]);
-            m[t] = g[t] * sigmoidf_(g[t]) * u[t];
+            m[t] = g[t] * sigmoidf_(g[t]) * u[t] * ws;
           }
           Vec8<Tout>::store(C + (int64_t)row * p.ldc + col, g);
           Vec8<Tout>::store(C + (int64_t)row * p.ldc + p.inter + col, u);
@@ -350,27 +367,32 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Cfg::MI][Cfg::NI]
       }
     } else {
       constexpr int CPR = WN / 8;
+      static_assert(EPI != EPI_SWIGLU_BWD || WN == 64, "routing-weight partials are per 64-column block");
       const int col_base = ti.n0 + wn * WN;
       for (int e = lane; e < 32 * CPR; e += 64) {
         const int r = e / CPR, c = (e % CPR) * 8;
         const int row = row_base + r, col = col_base + c;
+        float pd = 0.0f;  // this lane's share of <acc, silu(g) u> (EPI_SWIGLU_BWD with row_w)
         if (row < ti.m_end && col < p.N) {
           float v[8];
 #pragma unroll
           for (int t = 0; t < 8; ++t) v[t] = stage[r * Cfg::EPI_LD + c + t];
           if constexpr (EPI == EPI_SWIGLU_BWD) {
-            // v = d(mid); aux row holds [gate | up] pre-activations.
+            // v = d(mid), or with row_w d(w * mid); aux row holds [gate | up] pre-activations.
             const Tout* GU = reinterpret_cast<const Tout*>(p.aux) + (int64_t)row * p.ldaux;
             float g[8], u[8], dg[8], du[8];
             Vec8<Tout>::load(GU + col, g);
             Vec8<Tout>::load(GU + p.inter + col, u);
+            const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
               const float s = sigmoidf_(g[t]);
               const float silu = g[t] * s;
               const float dsilu = s * (1.0f + g[t] * (1.0f - s));
-              dg[t] = v[t] * u[t] * dsilu;
-              du[t] = v[t] * silu;
+              pd += v[t] * (silu * u[t]);
+              const float dm = v[t] * ws;
+              dg[t] = dm * u[t] * dsilu;
+              du[t] = dm * silu;
             }
             Vec8<Tout>::store(C + (int64_t)row * p.ldc + col, dg);
             Vec8<Tout>::store(C + (int64_t)row * p.ldc + p.inter + col, du);
@@ -378,6 +400,15 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Cfg::MI][Cfg::NI]
             Vec8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
           } else {
             for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+          }
+        }
+        if constexpr (EPI == EPI_SWIGLU_BWD) {
+          if (p.part != nullptr) {  // the CPR = 8 lanes of a row are consecutive: sum them in a fixed order
+            pd += __shfl_xor(pd, 1);
+            pd += __shfl_xor(pd, 2);
+            pd += __shfl_xor(pd, 4);
+            if ((e % CPR) == 0 && row < ti.m_end && col_base < p.N)
+              p.part[(int64_t)row * p.part_ld + col_base / 64] = pd;
           }
         }
       }
@@ -453,9 +484,12 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   if constexpr (A_KC) {
     const int m0 = ti.m0, me = ti.m_end;
     const int64_t lda = p.lda;
-    sa.init([&](int r) -> const TA* { return (m0 + r < me) ? A + (int64_t)(m0 + r) * lda : nullptr; }, tid);
+    const int32_t* ai = p.a_index;
+    sa.init([&](int r) -> const TA* {
+      return (m0 + r < me) ? A + (int64_t)(ai != nullptr ? ai[m0 + r] : m0 + r) * lda : nullptr;
+    }, tid);
   } else {
-    sa.init(A, p.lda, ti.m0, ti.m_end);
+    sa.init(A, p.lda, ti.m0, ti.m_end, p.a_index);
   }
   if constexpr (B_KC) {
     const int n0 = ti.n0, N = p.N, I = p.inter;
@@ -474,7 +508,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
       sb.init([&](int c) -> const TB* { return (n0 + c < N) ? B + (int64_t)(n0 + c) * ldb : nullptr; }, tid);
     }
   } else {
-    sb.init(B, p.ldb, ti.n0, p.N);
+    sb.init(B, p.ldb, ti.n0, p.N, p.b_index);
   }
 
   f32x16 acc[MI][NI];
@@ -542,6 +576,11 @@ inline GemmParams zero_params() {
   p.M = p.N = p.K = 0; p.split_chunk = 0; p.inter = 0;
   p.a_bytes = p.b_bytes = 0;
   p.planes = 1; p.strideA = 0;
+  p.a_index = nullptr; p.a_rows = 0;
+  p.b_index = nullptr; p.b_rows = 0;
+  p.n_index = 0;
+  p.row_w = nullptr;
+  p.part = nullptr; p.part_ld = 0;
   return p;
 }
 
@@ -560,21 +599,11 @@ hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The six grouped GEMMs of the expert FFN (forward, dgrad, wgrad of gate_up and down).
-enum ExpertGemm {
-  EG_GATE_UP_FWD = 0,  // gu, mid <- x_perm . W_gu[e]^T, SwiGLU epilogue
-  EG_DOWN_FWD = 1,     // y <- mid . W_dn[e]^T
-  EG_DOWN_DGRAD = 2,   // dgu <- SwiGLU'(gu) * (dy . W_dn[e])
-  EG_DOWN_WGRAD = 3,   // dW_dn[e] <- dy_e^T . mid_e
-  EG_GATE_UP_DGRAD = 4,  // dx_perm <- dgu . W_gu[e]
-  EG_GATE_UP_WGRAD = 5,  // dW_gu[e] <- dgu_e^T . x_perm_e
-};
-
 // Problem description of one expert GEMM. A, B: operands as listed above;
 // aux: gu for EG_DOWN_DGRAD; C2: mid for EG_GATE_UP_FWD.
 template <typename T>
 GemmParams expert_params(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P,
-                         int E, int H, int I) {
+                         int E, int H, int I, const ExpertGather& xg = ExpertGather()) {
   GemmParams p = zero_params();
   const uint64_t es = sizeof(T);
   p.offs = offs;
@@ -620,13 +649,23 @@ GemmParams expert_params(int kind, const T* A, const T* B, const T* aux, T* C, T
       p.a_bytes = (uint64_t)P * 2 * I * es; p.b_bytes = (uint64_t)P * H * es;
       break;
   }
+  if (xg.index != nullptr) {
+    p.n_index = P;
+    if (kind == EG_GATE_UP_WGRAD) {
+      p.b_index = xg.index; p.b_rows = xg.rows; p.b_bytes = (uint64_t)xg.rows * p.ldb * es;
+    } else if (kind == EG_GATE_UP_FWD || kind == EG_DOWN_DGRAD || kind == EG_DOWN_WGRAD) {
+      p.a_index = xg.index; p.a_rows = xg.rows; p.a_bytes = (uint64_t)xg.rows * p.lda * es;
+    }
+  }
+  if (kind == EG_GATE_UP_FWD || kind == EG_DOWN_DGRAD) p.row_w = xg.row_w;
+  if (kind == EG_DOWN_DGRAD) { p.part = xg.part; p.part_ld = xg.part_ld; }
   return p;
 }
 
 template <class Cfg, typename T>
 hipError_t expert_gemm(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P,
-                       int E, int H, int I, hipStream_t s) {
-  const GemmParams p = expert_params<T>(kind, A, B, aux, C, C2, offs, P, E, H, I);
+                       int E, int H, int I, const ExpertGather& xg, hipStream_t s) {
+  const GemmParams p = expert_params<T>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
   switch (kind) {
     case EG_GATE_UP_FWD: return launch_gemm<Cfg, T, T, T, true, true, GM_ROWS, EPI_SWIGLU>(p, s);
     case EG_DOWN_FWD: return launch_gemm<Cfg, T, T, T, true, true, GM_ROWS, EPI_STORE>(p, s);

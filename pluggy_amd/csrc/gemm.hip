@@ -50,66 +50,31 @@ int num_cus() {
   return g_cus[dev];
 }
 
-template <typename T>
-hipError_t run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, const int32_t* offs, int P, int E, int H,
-               int I, hipStream_t s) {
+}  // namespace
+
+template <typename T, typename Tw>
+hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, Tw* Cw, const int32_t* offs,
+                           int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s) {
+  const bool wgrad = kind == EG_DOWN_WGRAD || kind == EG_GATE_UP_WGRAD;
   if constexpr (sizeof(T) == 2) {
     if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
-      return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, num_cus(), s);
-    return expert_gemm_persist<DmaExpert>(kind, A, B, aux, C, C2, offs, P, E, H, I, num_cus(), s);
+      return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
+    return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {
-    return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, C, C2, offs, P, E, H, I, s);
+    static_assert(std::is_same<T, Tw>::value, "fp32 operands give fp32 weight gradients");
+    return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, wgrad ? Cw : C, C2, offs, P, E, H, I, xg, s);
   }
 }
 
-}  // namespace
-
-template <typename T>
-hipError_t gate_up_swiglu_fwd(const T* x_perm, const T* w_gu, const int32_t* offs, int P, int E, int H, int I,
-                              T* gu_out, T* mid, hipStream_t s) {
-  return run<T>(EG_GATE_UP_FWD, x_perm, w_gu, nullptr, gu_out, mid, offs, P, E, H, I, s);
-}
-
-template <typename T>
-hipError_t down_fwd(const T* mid, const T* w_dn, const int32_t* offs, int P, int E, int H, int I, T* y,
-                    hipStream_t s) {
-  return run<T>(EG_DOWN_FWD, mid, w_dn, nullptr, y, nullptr, offs, P, E, H, I, s);
-}
-
-template <typename T>
-hipError_t down_dgrad_swiglu_bwd(const T* dy, const T* w_dn, const T* gu_out, const int32_t* offs, int P, int E,
-                                 int H, int I, T* dgu, hipStream_t s) {
-  return run<T>(EG_DOWN_DGRAD, dy, w_dn, gu_out, dgu, nullptr, offs, P, E, H, I, s);
-}
-
-template <typename T>
-hipError_t down_wgrad(const T* dy, const T* mid, const int32_t* offs, int P, int E, int H, int I, T* dw_dn,
-                      hipStream_t s) {
-  return run<T>(EG_DOWN_WGRAD, dy, mid, nullptr, dw_dn, nullptr, offs, P, E, H, I, s);
-}
-
-template <typename T>
-hipError_t gate_up_dgrad(const T* dgu, const T* w_gu, const int32_t* offs, int P, int E, int H, int I, T* dx_perm,
-                         hipStream_t s) {
-  return run<T>(EG_GATE_UP_DGRAD, dgu, w_gu, nullptr, dx_perm, nullptr, offs, P, E, H, I, s);
-}
-
-template <typename T>
-hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int P, int E, int H, int I, T* dw_gu,
-                         hipStream_t s) {
-  return run<T>(EG_GATE_UP_WGRAD, dgu, x_perm, nullptr, dw_gu, nullptr, offs, P, E, H, I, s);
-}
-
-hipError_t down_wgrad_f32(const bf16_t* dy, const bf16_t* mid, const int32_t* offs, int P, int E, int H, int I,
-                          float* dw_dn, hipStream_t s) {
-  return expert_wgrad_persist_f32<DmaExpert>(EG_DOWN_WGRAD, dy, mid, dw_dn, offs, P, E, H, I, num_cus(), s);
-}
-
-hipError_t gate_up_wgrad_f32(const bf16_t* dgu, const bf16_t* x_perm, const int32_t* offs, int P, int E, int H,
-                             int I, float* dw_gu, hipStream_t s) {
-  return expert_wgrad_persist_f32<DmaExpert>(EG_GATE_UP_WGRAD, dgu, x_perm, dw_gu, offs, P, E, H, I,
-                                                          num_cus(), s);
-}
+template hipError_t expert_gemm_run<bf16_t, bf16_t>(int, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, bf16_t*,
+                                                    bf16_t*, const int32_t*, int, int, int, int, const ExpertGather&,
+                                                    hipStream_t);
+template hipError_t expert_gemm_run<bf16_t, float>(int, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, bf16_t*,
+                                                   float*, const int32_t*, int, int, int, int, const ExpertGather&,
+                                                   hipStream_t);
+template hipError_t expert_gemm_run<float, float>(int, const float*, const float*, const float*, float*, float*,
+                                                  float*, const int32_t*, int, int, int, int, const ExpertGather&,
+                                                  hipStream_t);
 
 template <typename TX, typename TW>
 hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, float* logits, hipStream_t s) {
@@ -197,19 +162,6 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
   p.M = E; p.N = H; p.K = T;
   return launch_gemm<CfgF32, float, TX, float, false, false, GM_RED, EPI_STORE>(p, s);
 }
-
-#define PMOE_INST_EXPERT(T)                                                                                      \
-  template hipError_t gate_up_swiglu_fwd<T>(const T*, const T*, const int32_t*, int, int, int, int, T*, T*,      \
-                                            hipStream_t);                                                       \
-  template hipError_t down_fwd<T>(const T*, const T*, const int32_t*, int, int, int, int, T*, hipStream_t);     \
-  template hipError_t down_dgrad_swiglu_bwd<T>(const T*, const T*, const T*, const int32_t*, int, int, int, int, \
-                                               T*, hipStream_t);                                                \
-  template hipError_t down_wgrad<T>(const T*, const T*, const int32_t*, int, int, int, int, T*, hipStream_t);   \
-  template hipError_t gate_up_dgrad<T>(const T*, const T*, const int32_t*, int, int, int, int, T*, hipStream_t); \
-  template hipError_t gate_up_wgrad<T>(const T*, const T*, const int32_t*, int, int, int, int, T*, hipStream_t);
-
-PMOE_INST_EXPERT(bf16_t)
-PMOE_INST_EXPERT(float)
 
 #define PMOE_INST_ROUTER(TX, TW)                                                                              \
   template hipError_t router_logits_gemm<TX, TW>(const TX*, const TW*, int, int, int, float*, hipStream_t);  \

@@ -163,6 +163,31 @@ struct KcDma {
       rowoff[i] = g < 0 ? kOOB : (uint32_t)(((int64_t)g * ld + 8 * c) * 2);
     }
   }
+  // Row gather: tile row r (< rows) is storage row idx[m0 + r] of the
+  // descriptor. The RPI rows of an instruction are consecutive, so their
+  // indices come through the scalar cache (uniform addresses, clamped into the
+  // table) and each lane picks its own; m0 must be wave-uniform.
+  __device__ __forceinline__ void init_gather(const int32_t* idx, int64_t n_idx, int m0, int rows, int64_t ld,
+                                              int wave, int lane) {
+    typedef const __attribute__((address_space(4))) int32_t cint;
+    cint* ci = (cint*)idx;  // wave-uniform reads through the scalar cache
+    const int64_t last = n_idx - 1;
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int rb = RPI * (wave + i * NW);
+      const int sel = lane / CPR;
+      int tok = 0;
+#pragma unroll
+      for (int j = 0; j < RPI; ++j) {
+        const int v = ci[min<int64_t>((int64_t)m0 + rb + j, last)];
+        tok = sel == j ? v : tok;
+      }
+      const int r = rb + sel;
+      const int c = (lane % CPR) ^ swz_kc<BK>(r);
+      kc[i] = 8 * c;
+      rowoff[i] = r < rows ? (uint32_t)(((int64_t)tok * ld + 8 * c) * 2) : kOOB;
+    }
+  }
   // this = second ? y : x, element by element (stays in registers)
   __device__ __forceinline__ void select(bool second, const KcDma& y, const KcDma& x) {
 #pragma unroll
@@ -221,6 +246,14 @@ struct TDma {
   template <int I>
   __device__ __forceinline__ void issue1(const BufRsrc& rs, uint32_t tile, int k0, int64_t ld, int wave) const {
     dma16(rs, tile + (wave + I * NW) * 1024, (uint32_t)((int64_t)(k0 + kk[I]) * ld * 2) + coloff[I]);
+  }
+  // k-row gather: this lane's k-row of instruction I is storage row tok (the
+  // caller's token of that k-row); k-rows at or past k_hi read zero.
+  template <int I>
+  __device__ __forceinline__ void issue1_rows(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, int tok,
+                                              int64_t ld, int wave) const {
+    const uint32_t v = k0 + kk[I] < k_hi ? (uint32_t)((int64_t)tok * ld * 2) + coloff[I] : kOOB;
+    dma16(rs, tile + (wave + I * NW) * 1024, v);
   }
 };
 

@@ -73,31 +73,39 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
             unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
             unpack8(uw, u);
+            const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;  // the routing weight
 #pragma unroll
-            for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
+            for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t] * ws;
             Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
           }
         }
       } else {
         constexpr int CPR = WN / 8;
+        static_assert(EPI != EPI_SWIGLU_BWD || WN == 64, "routing-weight partials are per 64-column block");
+        const int col_base = ti.n0 + wn * WN;
 #pragma unroll
         for (int e = lane; e < SLAB * CPR; e += 64) {
           const int r = e / CPR, c = (e % CPR) * 8;
-          const int row = row_base + r, col = ti.n0 + wn * WN + c;
+          const int row = row_base + r, col = col_base + c;
+          float pd = 0.0f;  // this lane's share of <acc, silu(g) u> (EPI_SWIGLU_BWD with row_w)
           if (row < ti.m_end && col < p.N) {
             float v[8];
             Vec8<float>::load(stage + r * LD + c, v);
             if constexpr (EPI == EPI_SWIGLU_BWD) {
+              // v = d(mid), or with row_w d(w * mid): then d(mid) = w v and d(w) += v . mid
               const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
               float g[8], u[8], dg[8], du[8];
               Vec8<bf16_t>::load(GU + col, g);
               Vec8<bf16_t>::load(GU + p.inter + col, u);
+              const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;
 #pragma unroll
               for (int t = 0; t < 8; ++t) {
                 const float sg = fast_sigmoid(g[t]);
                 const float silu = g[t] * sg;
-                dg[t] = v[t] * u[t] * (sg + silu * (1.0f - sg));
-                du[t] = v[t] * silu;
+                pd += v[t] * (silu * u[t]);
+                const float dm = v[t] * ws;
+                dg[t] = dm * u[t] * (sg + silu * (1.0f - sg));
+                du[t] = dm * silu;
               }
               Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
               Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
@@ -105,6 +113,15 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
               Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
             } else {
               for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+            }
+          }
+          if constexpr (EPI == EPI_SWIGLU_BWD) {
+            if (p.part != nullptr) {  // the CPR = 8 lanes of a row are consecutive: sum them in a fixed order
+              pd += __shfl_xor(pd, 1);
+              pd += __shfl_xor(pd, 2);
+              pd += __shfl_xor(pd, 4);
+              if ((e % CPR) == 0 && row < ti.m_end && col_base < p.N)
+                p.part[(int64_t)row * p.part_ld + col_base / 64] = pd;
             }
           }
         }
@@ -165,7 +182,29 @@ __device__ __forceinline__ int red_cost_tile(const int* s_cost, int groups, int 
 // tile's first NS - 1 stages have fully landed before its stage 0 (the
 // prologue, and each epilogue, waits for them), so stage 0 goes straight to
 // its barrier and every later stage waits for the same vmcnt.
-template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI>
+// The DMA instructions per stage of the operand whose k-rows are gathered
+// (one token per lane per instruction), and whether its tile shape has the
+// two k-rows per instruction (lanes 0-31, 32-63) the token reads assume.
+template <bool KG, class LdA, class LdB, bool ON_B>
+struct KGatherInfo {
+  static constexpr int INSTR = 1;
+  static constexpr bool ok = true;
+};
+template <class LdA, class LdB, bool ON_B>
+struct KGatherInfo<true, LdA, LdB, ON_B> {
+  typedef typename std::conditional<ON_B, LdB, LdA>::type L;
+  static constexpr int INSTR = L::INSTR;
+  static constexpr bool ok = L::KPI == 2 && L::CPR == 32;
+};
+
+// GATH: which operand's rows are gathered through an index table (see
+// GemmParams): 0 none, GA_ROWS (GM_ROWS: A's rows; indices once per tile),
+// GA_KROWS / GB_KROWS (GM_RED: A's / B's k-rows; the indices of the DMAs of
+// stage g + 1 are read through the scalar cache during stage g, and once per
+// tile for its first stage).
+enum GatherKind { G_NONE = 0, GA_ROWS = 1, GA_KROWS = 2, GB_KROWS = 3 };
+
+template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI, int GATH>
 __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
@@ -173,6 +212,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");
+  static_assert(GATH == G_NONE || (GATH == GA_ROWS && GM == GM_ROWS && A_KC) ||
+                    ((GATH == GA_KROWS || GATH == GB_KROWS) && GM == GM_RED),
+                "gathers: A's rows in GM_ROWS, A's or B's k-rows in GM_RED");
 
   __shared__ __attribute__((aligned(1024))) char smem[L::RING];
   __shared__ __attribute__((aligned(16))) float s_epi[L::EPI_FLOATS];
@@ -232,6 +274,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
 
+  // k-row gathers: the gathered [k][r] operand's DMA instructions per stage,
+  // each covering KPI = 2 k-rows (lanes 0-31 the first, 32-63 the second).
+  constexpr bool KGATH = GATH == GA_KROWS || GATH == GB_KROWS;
+  typedef KGatherInfo<KGATH, LdA, LdB, GATH == GB_KROWS> KGI;
+  constexpr int GI = KGI::INSTR;
+  static_assert(KGI::ok, "k-row gather expects 256-column [k][r] tiles");
+  const int32_t* gidx = GATH == GB_KROWS ? p.b_index : p.a_index;
+
   // What the DMAs of one tile need. nk is padded to at least NS - 1 stages
   // (the extra stages read zeros), so the DMAs of a tile's last NS - 1 stages
   // always fetch the following tile's first stages.
@@ -241,6 +291,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     LdA la;
     LdB lb;
     int nk, kd0, kd_hi;
+    int klo;  // first reduction index of the tile (wave-uniform; k-row gathers)
   };
   // Tile ordinal b of this block's share (b >= cnt: past the last tile; its
   // descriptors are empty, so every DMA reads zeros).
@@ -249,6 +300,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     T.nk = NS - 1;
     T.kd0 = 0;
     T.kd_hi = 0;
+    T.klo = 0;
     const bf16_t* a_base = A0;
     const bf16_t* b_base = B0;
     uint64_t a_bytes = 0, b_bytes = 0;
@@ -275,26 +327,40 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       }
       T.ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
       if constexpr (A_KC) {
-        a_base = A0 + (int64_t)T.ti.m0 * p.lda;
-        a_bytes = (uint64_t)(T.ti.m_end - T.ti.m0) * p.lda * 2;
+        if constexpr (GATH == GA_ROWS) {
+          a_bytes = p.a_bytes;  // the whole gathered storage
+        } else {
+          a_base = A0 + (int64_t)T.ti.m0 * p.lda;
+          a_bytes = (uint64_t)(T.ti.m_end - T.ti.m0) * p.lda * 2;
+        }
+      } else if constexpr (GATH == GA_KROWS) {
+        a_bytes = p.a_bytes;
       } else {
         a_base = A0 + (int64_t)T.ti.k_lo * p.lda;
         a_bytes = (uint64_t)(T.ti.k_hi - T.ti.k_lo) * p.lda * 2;
       }
       if constexpr (GM == GM_RED) {
-        b_base = B0 + (int64_t)T.ti.k_lo * p.ldb;
-        b_bytes = (uint64_t)(T.ti.k_hi - T.ti.k_lo) * p.ldb * 2;
+        if constexpr (GATH == GB_KROWS) {
+          b_bytes = p.b_bytes;
+        } else {
+          b_base = B0 + (int64_t)T.ti.k_lo * p.ldb;
+          b_bytes = (uint64_t)(T.ti.k_hi - T.ti.k_lo) * p.ldb * 2;
+        }
       }
       const int klen = T.ti.k_hi - T.ti.k_lo;
       T.nk = max((klen + BK - 1) / BK, NS - 1);
       T.kd0 = (GM == GM_RED) ? 0 : T.ti.k_lo;
       T.kd_hi = T.ti.k_hi - ((GM == GM_RED) ? T.ti.k_lo : 0);
+      T.klo = __builtin_amdgcn_readfirstlane(T.ti.k_lo);
     }
     T.rsA = make_rsrc(a_base, a_bytes);
     T.rsB = make_rsrc(b_base, b_bytes);
     if constexpr (A_KC) {
       const int rows = T.ti.m_end - T.ti.m0;
-      T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
+      if constexpr (GATH == GA_ROWS)
+        T.la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
+      else
+        T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
     } else {
       T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
     }
@@ -316,19 +382,44 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     }
   };
 
+  // Tokens of the gathered k-rows of tile-local stage ls of T: instruction i
+  // covers two k-rows, tok[i][0] for lanes 0-31 and tok[i][1] for 32-63. They
+  // are read through the scalar cache and stay wave-uniform (the per-lane
+  // pick happens at the DMA), so a read issued a stage ahead is not waited
+  // for until that stage.
+  auto tokens = [&](const LoadTile& T, int ls, int (&tok)[GI][2]) {
+    if constexpr (KGATH) {
+      typedef const __attribute__((address_space(4))) int32_t cint;
+      cint* ci = (cint*)gidx;
+      const int64_t last = p.n_index - 1;
+#pragma unroll
+      for (int i = 0; i < GI; ++i) {
+        const int64_t q = (int64_t)T.klo + ls * BK + (wave + i * NW) * 2;
+        tok[i][0] = ci[min<int64_t>(q, last)];
+        tok[i][1] = ci[min<int64_t>(q + 1, last)];
+      }
+    }
+  };
+
   int gs = 0;  // stream stage of the current tile's stage 0
   auto slot_of = [&](int g) { return (uint32_t)((g % NS) * Cfg::STAGE_BYTES); };
-  // DMA J of stage ls of tile T, into the ring slot of stream stage g.
-  auto dma_one = [&](const LoadTile& T, int ls, int g, auto jc) {
+  // DMA J of stage ls of tile T, into the ring slot of stream stage g; tok:
+  // the gathered k-rows' tokens of that stage.
+  auto dma_one = [&](const LoadTile& T, int ls, int g, const int (&tok)[GI][2], auto jc) {
     constexpr int J = decltype(jc)::value;
     const uint32_t st = lds0 + slot_of(g);
     const int k0 = T.kd0 + ls * BK;
     if constexpr (J < Cfg::A_INSTR) {
       if constexpr (A_KC) T.la.template issue1<J>(T.rsA, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+      else if constexpr (GATH == GA_KROWS)
+        T.la.template issue1_rows<J>(T.rsA, st, k0, T.kd_hi, lane < 32 ? tok[J][0] : tok[J][1], p.lda, wave);
       else T.la.template issue1<J>(T.rsA, st, k0, p.lda, wave);
     } else {
       constexpr int JB = J - Cfg::A_INSTR;
       if constexpr (B_KC) T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+      else if constexpr (GATH == GB_KROWS)
+        T.lb.template issue1_rows<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, lane < 32 ? tok[JB][0] : tok[JB][1],
+                                       p.ldb, wave);
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
@@ -346,9 +437,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   };
 
   f32x16 acc[MI][NI];
-  // One 16-k substep; with WITH_DMA the stage's D DMAs ride on its MFMAs.
+  // One 16-k substep; the stage's D DMAs ride on its MFMAs.
   auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], const LoadTile& T, int ls,
-                     int g) {
+                     int g, const int (&tok)[GI][2]) {
     constexpr int KSI = decltype(ksc)::value;
     static_for<0, MI * NI>([&](auto mc) {
       constexpr int M = decltype(mc)::value;
@@ -358,7 +449,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
         if constexpr ((DI * TOTM) / D == G) {
-          dma_one(T, ls, g, dc);
+          dma_one(T, ls, g, tok, dc);
           // keep the DMA between its MFMAs (MFMAs are not memory operations,
           // so the DMA's memory clobber alone would let them drift past it)
           __builtin_amdgcn_sched_barrier(0);
@@ -370,8 +461,12 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   LoadTile cur, nxt;
   setup(bi, cur);
   setup(bi + nb, nxt);
+  int tok[GI][2], tok_next[GI][2];
   // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
-  for (int s0 = 0; s0 < NS - 1; ++s0) static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, jc); });
+  for (int s0 = 0; s0 < NS - 1; ++s0) {
+    tokens(cur, s0, tok);
+    static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, tok, jc); });
+  }
   wait_vmcnt<0>();  // stages 0 .. NS-2 have landed: a tile's stage 0 never waits
   lds_barrier();
   bf16x8 af[2][MI], bfr[2][NI];
@@ -385,6 +480,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const int nk = cur.nk;
+    // tokens of stage 0's DMAs (stream stage gs + NS - 1: this tile's stage NS - 1, or the next tile's)
+    if constexpr (KGATH) tokens(NS - 1 >= nk ? nxt : cur, NS - 1 >= nk ? NS - 1 - nk : NS - 1, tok);
     for (int kt = 0; kt < nk; ++kt) {
       const int g = gs + kt;
       const char* sa = smem + slot_of(g);
@@ -406,13 +503,30 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
         load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
-        substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1);
+        substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok);
       });
       if (kt > 0) wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
+      if constexpr (KGATH) {
+        // the next stage's DMAs (stream stage g + NS: within this tile or the
+        // next, since the next tile has at least NS - 1 stages); read here so
+        // that the scalar reads run under this stage's last MFMAs rather than
+        // in front of a fragment wait (LDS and scalar reads share a counter)
+        if (kt + 1 < nk) {
+          const bool nn = s + 1 >= nk;
+          tokens(nn ? nxt : cur, nn ? s + 1 - nk : s + 1, tok_next);
+        }
+      }
       const char* na = smem + slot_of(g + 1);
       load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
-      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1);
+      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1, tok);
+      if constexpr (KGATH) {
+#pragma unroll
+        for (int i = 0; i < GI; ++i) {
+          tok[i][0] = tok_next[i][0];
+          tok[i][1] = tok_next[i][1];
+        }
+      }
     }
     // The next tile's first NS - 1 stages were issued during this tile's last
     // stages; wait for them before the epilogue issues its stores. The vector
@@ -430,12 +544,12 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   wait_vmcnt<0>();  // the zero-reading DMAs past the last tile
 }
 
-template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
+template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t, int GATH = G_NONE>
 hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) {
   if (p.groups > 1024) return hipErrorInvalidValue;
   const int grid = num_cus > 0 ? num_cus : 256;
-  hipLaunchKernelGGL((grouped_gemm_persist_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI>), dim3(grid), dim3(Cfg::NT), 0, s,
-                     p);
+  hipLaunchKernelGGL((grouped_gemm_persist_kernel<Cfg, Tout, A_KC, B_KC, GM, EPI, GATH>), dim3(grid), dim3(Cfg::NT), 0,
+                     s, p);
   return hipGetLastError();
 }
 
@@ -443,42 +557,45 @@ hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) 
 // for few-token batches serve the forward only).
 template <class Cfg>
 hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, bf16_t* C, bf16_t* C2,
-                                   const int32_t* offs, int P, int E, int H, int I, int num_cus, hipStream_t s) {
-  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, C, C2, offs, P, E, H, I);
+                                   const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
+                                   int num_cus, hipStream_t s) {
+  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, C, C2, offs, P, E, H, I, xg);
   switch (kind) {
-    case EG_GATE_UP_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_GATE_UP_FWD:
+      if (p.a_index != nullptr)
+        return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
     case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
   }
   return hipErrorInvalidValue;
 }
 
-// The two weight-gradient GEMMs with fp32 output (bf16 operands, gradients of
-// fp32 master weights): the accumulators are stored unrounded.
-template <class Cfg>
-hipError_t expert_wgrad_persist_f32(int kind, const bf16_t* A, const bf16_t* B, float* C, const int32_t* offs,
-                                    int P, int E, int H, int I, int num_cus, hipStream_t s) {
-  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, nullptr, nullptr, offs, P, E, H, I);
-  p.C = C;
+// The six expert GEMMs on the persistent kernel; Tw is the weight gradients'
+// type (bf16, or fp32 for fp32 master weights: the accumulators stored
+// unrounded). A gathered operand takes the GATH instance of its GEMM.
+template <class Cfg, typename Tw = bf16_t>
+hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C, bf16_t* C2,
+                               Tw* Cw, const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
+                               int num_cus, hipStream_t s) {
+  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
+  const bool gath = xg.index != nullptr;
   switch (kind) {
-    case EG_DOWN_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, float>(p, num_cus, s);
-    case EG_GATE_UP_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, float>(p, num_cus, s);
-  }
-  return hipErrorInvalidValue;
-}
-
-// The six expert GEMMs on the persistent kernel.
-template <class Cfg>
-hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
-                               bf16_t* C2, const int32_t* offs, int P, int E, int H, int I, int num_cus,
-                               hipStream_t s) {
-  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I);
-  switch (kind) {
-    case EG_GATE_UP_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_GATE_UP_FWD:
+      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
     case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
-    case EG_DOWN_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
-    case EG_DOWN_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+    case EG_DOWN_DGRAD:
+      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
     case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
-    case EG_GATE_UP_WGRAD: return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+    case EG_DOWN_WGRAD:
+    case EG_GATE_UP_WGRAD: {
+      p.C = Cw;
+      if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw>(p, num_cus, s);
+      if (kind == EG_DOWN_WGRAD)
+        return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GA_KROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GB_KROWS>(p, num_cus, s);
+    }
   }
   return hipErrorInvalidValue;
 }

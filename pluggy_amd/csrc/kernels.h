@@ -11,31 +11,15 @@
 
 namespace pmoe {
 
-// ---- grouped expert GEMMs (gemm.hip). T = bf16_t or float (activation dtype).
-// offs: (E,) int32 inclusive end row of each expert in the sorted order.
-template <typename T>
-hipError_t gate_up_swiglu_fwd(const T* x_perm, const T* w_gu, const int32_t* offs, int P, int E, int H, int I,
-                              T* gu_out, T* mid, hipStream_t s);
-template <typename T>
-hipError_t down_fwd(const T* mid, const T* w_dn, const int32_t* offs, int P, int E, int H, int I, T* y,
-                    hipStream_t s);
-template <typename T>
-hipError_t down_dgrad_swiglu_bwd(const T* dy, const T* w_dn, const T* gu_out, const int32_t* offs, int P, int E,
-                                 int H, int I, T* dgu, hipStream_t s);
-template <typename T>
-hipError_t down_wgrad(const T* dy, const T* mid, const int32_t* offs, int P, int E, int H, int I, T* dw_dn,
-                      hipStream_t s);
-template <typename T>
-hipError_t gate_up_dgrad(const T* dgu, const T* w_gu, const int32_t* offs, int P, int E, int H, int I, T* dx_perm,
-                         hipStream_t s);
-template <typename T>
-hipError_t gate_up_wgrad(const T* dgu, const T* x_perm, const int32_t* offs, int P, int E, int H, int I, T* dw_gu,
-                         hipStream_t s);
-// The two weight gradients from bf16 operands, stored as fp32 (fp32 master weights).
-hipError_t down_wgrad_f32(const bf16_t* dy, const bf16_t* mid, const int32_t* offs, int P, int E, int H, int I,
-                          float* dw_dn, hipStream_t s);
-hipError_t gate_up_wgrad_f32(const bf16_t* dgu, const bf16_t* x_perm, const int32_t* offs, int P, int E, int H,
-                             int I, float* dw_gu, hipStream_t s);
+// ---- grouped expert GEMMs (gemm.hip). T = bf16_t or float (activation
+// dtype); Tw: the weight gradients' type (EG_*_WGRAD; fp32 with bf16
+// operands for fp32 master weights). offs: (E,) int32 inclusive end row of each
+// expert in the sorted order. Operands per kind (see ExpertGemm): A, B, aux,
+// C, C2 (gate_up forward: mid), Cw (weight gradients); xg: gathers and
+// routing weights.
+template <typename T, typename Tw>
+hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, Tw* Cw, const int32_t* offs,
+                           int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s);
 
 // ---- router GEMMs in fp32 arithmetic (gemm.hip). TX: x dtype, TW: router weight dtype.
 template <typename TX, typename TW>
@@ -80,6 +64,12 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
 template <typename TO>
 hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s);
 
+template <typename TW>
+hipError_t sort_rows(const int32_t* sorted_pair, const TW* w, int P, int K, int32_t* sorted_token, float* sorted_w,
+                     hipStream_t s);
+template <typename TG>
+hipError_t pair_weight_grad(const float* part, int ld, int nparts, const int32_t* inv_pos, int P, TG* grad_w,
+                            hipStream_t s);
 hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* count, hipStream_t s);
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
                          int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s);

@@ -672,26 +672,26 @@ __device__ __forceinline__ void gather_sum_row(const T* __restrict__ y, const TW
   }
 }
 
-template <typename T, typename TW, int KC>
+template <typename T, typename TW, int KC, bool WEIGHTED = true>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ y, const TW* __restrict__ w,
                                                       const int32_t* __restrict__ inv_pos, int T_, int K, int H,
                                                       T* __restrict__ out) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  gather_sum_row<T, TW, KC, true, false>(y, w, inv_pos, static_cast<const T*>(nullptr), t, K, H, out,
-                                         threadIdx.x & 63);
+  gather_sum_row<T, TW, KC, WEIGHTED, false>(y, w, inv_pos, static_cast<const T*>(nullptr), t, K, H, out,
+                                             threadIdx.x & 63);
 }
 
 // out[t] = res[t] + sum_k w[t,k] * y[inv_pos[t*K + k]]: the combine with the
 // block's residual add (qwen3_moe.py:281) fused; res and out share dtype TR.
-template <typename T, typename TW, typename TR, int KC>
+template <typename T, typename TW, typename TR, int KC, bool WEIGHTED = true>
 __global__ __launch_bounds__(256) void combine_residual_kernel(const T* __restrict__ y, const TW* __restrict__ w,
                                                                const int32_t* __restrict__ inv_pos,
                                                                const TR* __restrict__ res, int T_, int K, int H,
                                                                TR* __restrict__ out) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  gather_sum_row<T, TW, KC, true, true, TR, TR>(y, w, inv_pos, res, t, K, H, out, threadIdx.x & 63);
+  gather_sum_row<T, TW, KC, WEIGHTED, true, TR, TR>(y, w, inv_pos, res, t, K, H, out, threadIdx.x & 63);
 }
 
 // grad_y[inv_pos[t*K+k]] = w[t,k] * dout[t]; dw[t,k] = <dout[t], y[inv_pos[t*K+k]]>.
@@ -895,6 +895,57 @@ hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* 
   return hipGetLastError();
 }
 
+// Per sorted row p (pair q = sorted_pair[p]): its token q / K and its routing
+// weight w[q] as fp32 (w may be null: no weights).
+template <typename TW>
+__global__ __launch_bounds__(256) void sort_rows_kernel(const int32_t* __restrict__ sorted_pair,
+                                                        const TW* __restrict__ w, int P, int K,
+                                                        int32_t* __restrict__ sorted_token, float* __restrict__ sorted_w) {
+  for (int p = blockIdx.x * 256 + threadIdx.x; p < P; p += gridDim.x * 256) {
+    const int q = sorted_pair[p];
+    sorted_token[p] = q / K;
+    if (sorted_w != nullptr) sorted_w[p] = load_scalar<TW>(w + q);
+  }
+}
+
+template <typename TW>
+hipError_t sort_rows(const int32_t* sorted_pair, const TW* w, int P, int K, int32_t* sorted_token, float* sorted_w,
+                     hipStream_t s) {
+  if (P == 0) return hipSuccess;
+  const int blocks = std::min((P + 255) / 256, 4096);
+  hipLaunchKernelGGL((sort_rows_kernel<TW>), dim3(blocks), dim3(256), 0, s, sorted_pair, w, P, K, sorted_token,
+                     sorted_w);
+  return hipGetLastError();
+}
+template hipError_t sort_rows<float>(const int32_t*, const float*, int, int, int32_t*, float*, hipStream_t);
+template hipError_t sort_rows<bf16_t>(const int32_t*, const bf16_t*, int, int, int32_t*, float*, hipStream_t);
+
+// The routing weights' gradient from the per-row partials of the down
+// backward: grad_w[q] = sum_j part[inv_pos[q] * ld + j] (j ascending, fp32).
+template <typename TG>
+__global__ __launch_bounds__(256) void pair_weight_grad_kernel(const float* __restrict__ part, int ld, int nparts,
+                                                               const int32_t* __restrict__ inv_pos, int P,
+                                                               TG* __restrict__ grad_w) {
+  for (int q = blockIdx.x * 256 + threadIdx.x; q < P; q += gridDim.x * 256) {
+    const float* r = part + (int64_t)inv_pos[q] * ld;
+    float acc = 0.0f;
+    for (int j = 0; j < nparts; ++j) acc += r[j];
+    store_scalar<TG>(grad_w + q, acc);
+  }
+}
+
+template <typename TG>
+hipError_t pair_weight_grad(const float* part, int ld, int nparts, const int32_t* inv_pos, int P, TG* grad_w,
+                            hipStream_t s) {
+  if (P == 0) return hipSuccess;
+  const int blocks = std::min((P + 255) / 256, 4096);
+  hipLaunchKernelGGL((pair_weight_grad_kernel<TG>), dim3(blocks), dim3(256), 0, s, part, ld, nparts, inv_pos, P,
+                     grad_w);
+  return hipGetLastError();
+}
+template hipError_t pair_weight_grad<float>(const float*, int, int, const int32_t*, int, float*, hipStream_t);
+template hipError_t pair_weight_grad<bf16_t>(const float*, int, int, const int32_t*, int, bf16_t*, hipStream_t);
+
 // Calls F with the compile-time top-k (the common values) or 0 (runtime K).
 template <class F>
 hipError_t with_kc(int K, F&& f) {
@@ -923,8 +974,12 @@ hipError_t combine_rows(const T* y, const TW* w, const int32_t* inv_pos, int T_,
                         hipStream_t s) {
   if (T_ == 0) return hipSuccess;
   return with_kc(K, [&](auto kc) {
-    hipLaunchKernelGGL((combine_kernel<T, TW, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, y, w,
-                       inv_pos, T_, K, H, out);
+    if (w != nullptr)
+      hipLaunchKernelGGL((combine_kernel<T, TW, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256), 0, s, y, w,
+                         inv_pos, T_, K, H, out);
+    else  // unit weights: the rows already carry their routing weight
+      hipLaunchKernelGGL((combine_kernel<T, TW, decltype(kc)::value, false>), dim3(blocks_for(T_, 4)), dim3(256), 0,
+                         s, y, w, inv_pos, T_, K, H, out);
     return hipGetLastError();
   });
 }
@@ -952,8 +1007,12 @@ hipError_t combine_rows_residual(const T* y, const TW* w, const int32_t* inv_pos
                                  TR* out, hipStream_t s) {
   if (T_ == 0) return hipSuccess;
   return with_kc8(K, [&](auto kc) {
-    hipLaunchKernelGGL((combine_residual_kernel<T, TW, TR, decltype(kc)::value>), dim3(blocks_for(T_, 4)), dim3(256),
-                       0, s, y, w, inv_pos, res, T_, K, H, out);
+    if (w != nullptr)
+      hipLaunchKernelGGL((combine_residual_kernel<T, TW, TR, decltype(kc)::value>), dim3(blocks_for(T_, 4)),
+                         dim3(256), 0, s, y, w, inv_pos, res, T_, K, H, out);
+    else
+      hipLaunchKernelGGL((combine_residual_kernel<T, TW, TR, decltype(kc)::value, false>), dim3(blocks_for(T_, 4)),
+                         dim3(256), 0, s, y, w, inv_pos, res, T_, K, H, out);
     return hipGetLastError();
   });
 }

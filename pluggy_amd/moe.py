@@ -248,6 +248,37 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
 # -------------------------------------------------------------- expert FFN
 
 
+def _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj):
+    """-> out and what the backward reads: offs, inv_pos, sorted_token, sorted_w, gu, mid.
+
+    The expert-sorted copy of the hidden rows (moe.py:104) is never built: the
+    gate_up GEMM gathers row sorted_token[p] of ``hidden`` in its operand loads,
+    and its SwiGLU epilogue multiplies the activation by the routing weight
+    (moe.py:120), so the down projection's rows come out weighted and the
+    combine is a plain sum of each token's K rows."""
+    E = gate_up_proj.shape[0]
+    K = top_indices.shape[1]
+    with _stage("permute"):
+        _, offs, sorted_pair, inv_pos = ops.permute(top_indices, E)
+    with _stage("sort_rows"):
+        sorted_token, sorted_w = ops.sort_rows(sorted_pair, top_weights, K)
+    with _stage("gate_up_fwd"):
+        gu, mid = ops.gate_up_swiglu(hidden, gate_up_proj, offs, sorted_token, sorted_w)
+    with _stage("down_fwd"):
+        y = ops.down_proj(mid, down_proj, offs)
+    with _stage("combine"):
+        out = ops.combine(y, None, inv_pos, K)
+    return out, offs, inv_pos, sorted_token, sorted_w, gu, mid
+
+
+def _ffn_fake_saved(hidden, K, E, I):
+    T, H = hidden.shape
+    P = T * K
+    i32 = torch.int32
+    return (hidden.new_empty(E, dtype=i32), hidden.new_empty(P, dtype=i32), hidden.new_empty(P, dtype=i32),
+            hidden.new_empty(P, dtype=torch.float32), hidden.new_empty(P, 2 * I), hidden.new_empty(P, I))
+
+
 # Check caller-supplied expert ids before routing (moe_expert_ffn). The
 # reference raises on an id outside [0, E) (F.one_hot at moe.py:50, bincount at
 # moe.py:107); the kernels would clamp it into range instead. The check reads
@@ -260,31 +291,6 @@ def _check_expert_ids(top_indices: torch.Tensor, num_experts: int) -> None:
     bad = int(ops.count_invalid_ids(top_indices, num_experts).item())
     if bad:
         raise RuntimeError(f"moe_expert_ffn: {bad} expert id(s) outside [0, {num_experts})")
-
-
-def _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj):
-    """-> out and what the backward reads: offs, inv_pos, x_perm, gu, mid, y."""
-    E = gate_up_proj.shape[0]
-    K = top_indices.shape[1]
-    with _stage("permute"):
-        _, offs, _, inv_pos = ops.permute(top_indices, E)
-    with _stage("dispatch"):
-        x_perm = ops.dispatch(hidden, inv_pos, K)
-    with _stage("gate_up_fwd"):
-        gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
-    with _stage("down_fwd"):
-        y = ops.down_proj(mid, down_proj, offs)
-    with _stage("combine"):
-        out = ops.combine(y, top_weights, inv_pos)
-    return out, offs, inv_pos, x_perm, gu, mid, y
-
-
-def _ffn_fake_saved(hidden, K, E, I):
-    T, H = hidden.shape
-    P = T * K
-    i32 = torch.int32
-    return (hidden.new_empty(E, dtype=i32), hidden.new_empty(P, dtype=i32), hidden.new_empty(P, H),
-            hidden.new_empty(P, 2 * I), hidden.new_empty(P, I), hidden.new_empty(P, H))
 
 
 @torch.library.custom_op("pmoe::expert_ffn_fwd", mutates_args=(),
@@ -306,36 +312,41 @@ def _(hidden, top_indices, top_weights, gate_up_proj, down_proj, gate_up_master=
     return (torch.empty_like(hidden),) + _ffn_fake_saved(hidden, top_indices.shape[1], E, I2 // 2)
 
 
-@torch.library.custom_op("pmoe::combine_bwd", mutates_args=(),
-                         schema="(Tensor grad_out, Tensor y, Tensor top_weights, Tensor inv_pos) -> (Tensor, Tensor)")
-def _combine_bwd(grad_out, y, top_weights, inv_pos):
-    """-> grad_y (P,H) = w * grad_out gathered, grad_top_weights (T,K)."""
-    with _stage("combine_bwd"):
-        return ops.combine_backward(grad_out, y, top_weights, inv_pos)
+@torch.library.custom_op("pmoe::expert_bwd_dgrad", mutates_args=(),
+                         schema="(Tensor grad_out, Tensor down_proj, Tensor offs, Tensor inv_pos, Tensor sorted_token, "
+                                "Tensor sorted_w, Tensor gu, int top_k, bool need_top_w) -> (Tensor, Tensor)")
+def _expert_bwd_dgrad(grad_out, down_proj, offs, inv_pos, sorted_token, sorted_w, gu, top_k, need_top_w):
+    """The down projection's input gradient through the SwiGLU: -> grad_gate_up_out
+    (P, 2I) and, with need_top_w, the routing weights' gradient (T, K) fp32
+    (an empty stand-in otherwise). grad_out (T, H) is the layer's output
+    gradient; its rows are gathered by sorted_token."""
+    with _stage("down_dgrad"):
+        g_gu, part = ops.down_proj_dgrad(grad_out, gu, down_proj, offs, sorted_token, sorted_w,
+                                         need_part=need_top_w)
+    if not need_top_w:
+        return g_gu, _empty_like_none(sorted_w)
+    with _stage("pair_wgrad"):
+        return g_gu, ops.pair_weight_grad(part, inv_pos, top_k)
 
 
-@_combine_bwd.register_fake
-def _(grad_out, y, top_weights, inv_pos):
-    return torch.empty_like(y), torch.empty_like(top_weights)
+@_expert_bwd_dgrad.register_fake
+def _(grad_out, down_proj, offs, inv_pos, sorted_token, sorted_w, gu, top_k, need_top_w):
+    P = sorted_token.shape[0]
+    return (gu.new_empty(P, gu.shape[1]),
+            grad_out.new_empty(P // top_k, top_k, dtype=torch.float32) if need_top_w else _empty_like_none(sorted_w))
 
 
-def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_rows, need_gu, need_dn, reduce_rows,
-                           f32_wgrads=(False, False)):
-    """The expert GEMMs' backward from grad_y. With need_rows, the (P, H) input
-    gradient of the dispatched rows goes to ``reduce_rows`` (which sums each
-    token's K rows) before the gate_up weight gradient is computed, so it is
-    freed early. f32_wgrads (gate_up, down): write that weight gradient in fp32.
+def _expert_gemms_backward(g_gu, grad_out, hidden, gate_up, down, offs, sorted_token, mid, need_rows, need_gu,
+                           need_dn, reduce_rows, f32_wgrads=(False, False)):
+    """The expert GEMMs' backward after the down dgrad (g_gu = grad_gate_up_out).
+    With need_rows, the (P, H) input gradient of the sorted rows goes to
+    ``reduce_rows`` (which sums each token's K rows) before the weight
+    gradients are computed, so it is freed early. f32_wgrads (gate_up, down):
+    write that weight gradient in fp32.
     -> (reduce_rows result or None, grad_gate_up or None, grad_down or None)."""
     E = gate_up.shape[0]
     f32 = torch.float32
     reduced = g_gu_w = g_dn_w = None
-    g_gu = None
-    if need_rows or need_gu:
-        with _stage("down_dgrad"):
-            g_gu = ops.down_proj_dgrad(grad_y, gu, down, offs)
-    if need_dn:
-        with _stage("down_wgrad"):
-            g_dn_w = ops.down_proj_wgrad(grad_y, mid, offs, E, f32 if f32_wgrads[1] else None)
     if need_rows:
         with _stage("gate_up_dgrad"):
             g_xp = ops.gate_up_dgrad(g_gu, gate_up, offs)
@@ -343,28 +354,32 @@ def _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_ro
         del g_xp
     if need_gu:
         with _stage("gate_up_wgrad"):
-            g_gu_w = ops.gate_up_wgrad(g_gu, x_perm, offs, E, f32 if f32_wgrads[0] else None)
+            g_gu_w = ops.gate_up_wgrad(g_gu, hidden, offs, E, f32 if f32_wgrads[0] else None, row_index=sorted_token)
+    if need_dn:
+        with _stage("down_wgrad"):
+            g_dn_w = ops.down_proj_wgrad(grad_out, mid, offs, E, f32 if f32_wgrads[1] else None,
+                                         row_index=sorted_token)
     return reduced, g_gu_w, g_dn_w
 
 
 @torch.library.custom_op("pmoe::expert_bwd", mutates_args=(),
-                         schema="(Tensor grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
-                                "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_hidden_add, int tokens, int top_k, "
-                                "bool[] needs, bool[] f32_wgrads) -> (Tensor, Tensor, Tensor)")
-def _expert_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs,
-                f32_wgrads):
-    """The expert GEMMs' backward from grad_y: -> grad_hidden (+ grad_hidden_add),
-    grad_gate_up, grad_down; an empty tensor where needs[i] is false (needs:
-    hidden, gate_up, down). f32_wgrads (gate_up, down): that weight gradient
-    is fp32 (an fp32 master's) instead of the operands' dtype."""
+                         schema="(Tensor g_gu, Tensor grad_out, Tensor hidden, Tensor gate_up_proj, Tensor down_proj, "
+                                "Tensor offs, Tensor inv_pos, Tensor sorted_token, Tensor mid, Tensor? grad_hidden_add, "
+                                "int top_k, bool[] needs, bool[] f32_wgrads) -> (Tensor, Tensor, Tensor)")
+def _expert_bwd(g_gu, grad_out, hidden, gate_up, down, offs, inv_pos, sorted_token, mid, grad_hidden_add, top_k,
+                needs, f32_wgrads):
+    """The expert GEMMs' backward after the down dgrad: -> grad_hidden (+
+    grad_hidden_add), grad_gate_up, grad_down; an empty tensor where needs[i] is
+    false (needs: hidden, gate_up, down). f32_wgrads (gate_up, down): that weight
+    gradient is fp32 (an fp32 master's) instead of the operands' dtype."""
     def reduce_rows(g_xp):
         with _stage("dispatch_bwd"):
-            return ops.dispatch_backward(g_xp, inv_pos, tokens, top_k, add=grad_hidden_add)
+            return ops.dispatch_backward(g_xp, inv_pos, hidden.shape[0], top_k, add=grad_hidden_add)
 
-    g_hidden, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, needs[0],
-                                                      needs[1], needs[2], reduce_rows, f32_wgrads)
+    g_hidden, g_gu_w, g_dn_w = _expert_gemms_backward(g_gu, grad_out, hidden, gate_up, down, offs, sorted_token, mid,
+                                                      needs[0], needs[1], needs[2], reduce_rows, f32_wgrads)
     e = _empty_like_none
-    return (g_hidden if g_hidden is not None else e(grad_y), g_gu_w if g_gu_w is not None else e(gate_up),
+    return (g_hidden if g_hidden is not None else e(hidden), g_gu_w if g_gu_w is not None else e(gate_up),
             g_dn_w if g_dn_w is not None else e(down))
 
 
@@ -373,9 +388,10 @@ def _wgrad_fake(w, f32):
 
 
 @_expert_bwd.register_fake
-def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, tokens, top_k, needs, f32_wgrads):
+def _(g_gu, grad_out, hidden, gate_up, down, offs, inv_pos, sorted_token, mid, grad_hidden_add, top_k, needs,
+      f32_wgrads):
     e = _empty_like_none
-    return (grad_y.new_empty(tokens, grad_y.shape[1]) if needs[0] else e(grad_y),
+    return (torch.empty_like(hidden) if needs[0] else e(hidden),
             _wgrad_fake(gate_up, f32_wgrads[0]) if needs[1] else e(gate_up),
             _wgrad_fake(down, f32_wgrads[1]) if needs[2] else e(down))
 
@@ -383,33 +399,38 @@ def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_hidden_add, to
 def _ffn_setup(ctx, inputs, output):
     hidden, top_indices, top_weights, gate_up_proj, down_proj, gate_up_master, down_master = inputs
     ctx.f32_wgrads = _f32_wgrads(gate_up_master, down_master)
-    out, offs, inv_pos, x_perm, gu, mid, y = output
-    ctx.save_for_backward(top_weights, gate_up_proj, down_proj, offs, inv_pos, x_perm, gu, mid, y)
-    ctx.dims = (hidden.shape[0], top_indices.shape[1])
-    ctx.mark_non_differentiable(offs, inv_pos, x_perm, gu, mid, y)
+    out, offs, inv_pos, sorted_token, sorted_w, gu, mid = output
+    ctx.save_for_backward(hidden, gate_up_proj, down_proj, offs, inv_pos, sorted_token, sorted_w, gu, mid)
+    ctx.top_k = top_indices.shape[1]
+    ctx.tw_dtype = top_weights.dtype
+    ctx.mark_non_differentiable(offs, inv_pos, sorted_token, sorted_w, gu, mid)
     ctx.set_materialize_grads(False)
 
 
 def _ffn_backward(ctx, grad_out, *_saved_grads):
     if grad_out is None:
         return (None,) * 7
-    top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid, y = ctx.saved_tensors
-    T, K = ctx.dims
+    hidden, gate_up, down, offs, inv_pos, sorted_token, sorted_w, gu, mid = ctx.saved_tensors
+    K = ctx.top_k
     need = _needs(ctx, 7)  # hidden, indices, weights, gate_up, down, gate_up_master, down_master
     need_gu, need_dn = need[3] or need[5], need[4] or need[6]
+    if not (need[0] or need[2] or need_gu or need_dn):
+        return (None,) * 7
     grad_out = grad_out.contiguous()
-    if grad_out.dtype != x_perm.dtype:
-        grad_out = grad_out.to(x_perm.dtype)
-    g_y, g_w = torch.ops.pmoe.combine_bwd(grad_out, y, top_w, inv_pos)
+    if grad_out.dtype != hidden.dtype:
+        grad_out = grad_out.to(hidden.dtype)
+    g_gu, g_w = torch.ops.pmoe.expert_bwd_dgrad(grad_out, down, offs, inv_pos, sorted_token, sorted_w, gu, K,
+                                                bool(need[2]))
     g_hidden = g_gu_w = g_dn_w = None
     if need[0] or need_gu or need_dn:
-        g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid,
-                                                             None, T, K,
+        g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(g_gu, grad_out, hidden, gate_up, down, offs, inv_pos,
+                                                             sorted_token, mid, None, K,
                                                              [bool(need[0]), bool(need_gu), bool(need_dn)],
                                                              ctx.f32_wgrads)
         g_hidden, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_hidden, g_gu_w, g_dn_w))
-    return (g_hidden if need[0] else None, None, (g_w if need[2] else None), g_gu_w if need[3] else None,
-            g_dn_w if need[4] else None, g_gu_w if need[5] else None, g_dn_w if need[6] else None)
+    g_w = g_w.to(ctx.tw_dtype) if need[2] else None
+    return (g_hidden if need[0] else None, None, g_w, g_gu_w if need[3] else None, g_dn_w if need[4] else None,
+            g_gu_w if need[5] else None, g_dn_w if need[6] else None)
 
 
 _expert_ffn_fwd.register_autograd(_ffn_backward, setup_context=_ffn_setup)
@@ -428,15 +449,16 @@ def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_
     """Router + dropless experts (Qwen3MoeSparseMLP.forward) as one op.
 
     -> out, router_logits, counts, prob_sum, lse_sq_sum, then what the backward
-    reads: top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y. The
-    masters, when given, are the differentiable fp32 weights whose bf16 copies
-    gate_up_proj / down_proj are (their gradients are written in fp32).
+    reads: top_i, top_w32, top_w, offs, inv_pos, sorted_token, sorted_w, gu,
+    mid. The masters, when given, are the differentiable fp32 weights whose
+    bf16 copies gate_up_proj / down_proj are (their gradients are written in
+    fp32).
     """
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
             x, router_weight, top_k, norm_topk_prob, logit_bias)
-    out, offs, inv_pos, x_perm, gu, mid, y = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
-    return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y
+    out, offs, inv_pos, stok, sw, gu, mid = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
+    return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid
 
 
 @_sparse_moe_fwd.register_fake
@@ -453,22 +475,21 @@ def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bi
 
 def _sparse_setup(ctx, inputs, output):
     x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master, dn_master = inputs
-    (out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y) = output
+    (out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid) = output
     ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
-    ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, top_w, gate_up_proj, down_proj, offs, inv_pos,
-                          x_perm, gu, mid, y)
+    ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, gate_up_proj, down_proj, offs, inv_pos, stok,
+                          sw, gu, mid)
     ctx.norm_topk_prob = bool(norm_topk_prob)
     ctx.dims = (x.shape[0], int(top_k))
-    ctx.mark_non_differentiable(counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y)
+    ctx.mark_non_differentiable(counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid)
     ctx.set_materialize_grads(False)
 
 
 def _sparse_backward(ctx, g_out, g_logits, *_rest):
-    """The router's share of the input gradient is computed first and added
-    inside the dispatch backward, so the two input gradients are never summed
-    by a separate pass."""
-    (x, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
-     y) = ctx.saved_tensors
+    """The down dgrad comes first (it yields the routing weights' gradient), then
+    the router's backward, whose input gradient is added inside the dispatch
+    backward, so the two input gradients are never summed by a separate pass."""
+    (x, rw, logits, top_i, top_w32, gate_up, down, offs, inv_pos, stok, sw, gu, mid) = ctx.saved_tensors
     T, K = ctx.dims
     need = _needs(ctx, 9)  # x, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
     need_gu, need_dn = need[2] or need[7], need[3] or need[8]
@@ -477,19 +498,21 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     if g_logits is not None:
         g_logits = g_logits.float().contiguous()
     g_x = g_rw = g_gu_w = g_dn_w = None
-    g_y = g_tw = None
+    g_gu = g_tw = None
     if g_out is not None:
         g_out = g_out.contiguous()
-        if g_out.dtype != x_perm.dtype:
-            g_out = g_out.to(x_perm.dtype)
-        g_y, g_tw = torch.ops.pmoe.combine_bwd(g_out, y, top_w, inv_pos)
+        if g_out.dtype != gu.dtype:
+            g_out = g_out.to(gu.dtype)
+        g_gu, g_tw = torch.ops.pmoe.expert_bwd_dgrad(g_out, down, offs, inv_pos, stok, sw, gu, K,
+                                                     bool(need[0] or need[1]))
+        g_tw = _none_if_empty(g_tw)
     gx_router = None
     if need[0] or need[1]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(x, rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
-    if g_y is not None and (need[0] or need_gu or need_dn):
+    if g_gu is not None and (need[0] or need_gu or need_dn):
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
-            g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if need[0] else None, T, K,
+            g_gu, g_out, x, gate_up, down, offs, inv_pos, stok, mid, gx_router if need[0] else None, K,
             [bool(need[0]), bool(need_gu), bool(need_dn)], ctx.f32_wgrads)
         g_x = _none_if_empty(g_hidden)
         g_gu_w = _none_if_empty(g_gu_w)
@@ -581,8 +604,8 @@ def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_pro
     The kernels compute in gate_up_proj's dtype; x is the residual stream (its
     own dtype). -> out, router_logits, counts, prob_sum, lse_sq_sum, then what
     the backward reads: normed, rstd, top_i, top_w32, top_w, offs, inv_pos,
-    x_perm, gu, mid, y. The masters, when given, are the differentiable fp32
-    weights whose bf16 copies gate_up_proj / down_proj are.
+    sorted_token, sorted_w, gu, mid. The masters, when given, are the
+    differentiable fp32 weights whose bf16 copies gate_up_proj / down_proj are.
     """
     with _stage("rmsnorm"):
         normed, rstd = ops.rmsnorm_forward(x, norm_weight, eps, gate_up_proj.dtype)
@@ -590,16 +613,16 @@ def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_pro
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
             normed, router_weight, top_k, norm_topk_prob, logit_bias)
     with _stage("permute"):
-        _, offs, _, inv_pos = ops.permute(top_i, gate_up_proj.shape[0])
-    with _stage("dispatch"):
-        x_perm = ops.dispatch(normed, inv_pos, top_k)
+        _, offs, sorted_pair, inv_pos = ops.permute(top_i, gate_up_proj.shape[0])
+    with _stage("sort_rows"):
+        stok, sw = ops.sort_rows(sorted_pair, top_w, top_k)
     with _stage("gate_up_fwd"):
-        gu, mid = ops.gate_up_swiglu(x_perm, gate_up_proj, offs)
+        gu, mid = ops.gate_up_swiglu(normed, gate_up_proj, offs, stok, sw)
     with _stage("down_fwd"):
         y = ops.down_proj(mid, down_proj, offs)
     with _stage("combine"):
-        out = ops.combine_residual(y, top_w, inv_pos, x)
-    return out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid, y
+        out = ops.combine_residual(y, None, inv_pos, x, top_k)
+    return out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid
 
 
 @_moe_sublayer_fwd.register_fake
@@ -613,34 +636,24 @@ def _(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_t
     return (torch.empty_like(x), x.new_empty(T, E, dtype=f32), x.new_empty(E, dtype=i32), x.new_empty(E, dtype=f32),
             x.new_empty(1, dtype=f32), x.new_empty(T, H, dtype=cdt), x.new_empty(T, dtype=f32),
             x.new_empty(T, K, dtype=torch.int64), x.new_empty(T, K, dtype=f32), x.new_empty(T, K, dtype=cdt),
-            x.new_empty(E, dtype=i32), x.new_empty(P, dtype=i32), x.new_empty(P, H, dtype=cdt),
-            x.new_empty(P, 2 * I, dtype=cdt), x.new_empty(P, I, dtype=cdt), x.new_empty(P, H, dtype=cdt))
-
-
-@torch.library.custom_op("pmoe::combine_residual_bwd", mutates_args=(),
-                         schema="(Tensor grad_out, Tensor y, Tensor top_weights, Tensor inv_pos) -> (Tensor, Tensor)")
-def _combine_residual_bwd(grad_out, y, top_weights, inv_pos):
-    """-> grad_y (P,H) = w * grad_out gathered, grad_top_weights (T,K); grad_out in the stream's dtype."""
-    with _stage("combine_bwd"):
-        return ops.combine_residual_backward(grad_out, y, top_weights, inv_pos)
-
-
-@_combine_residual_bwd.register_fake
-def _(grad_out, y, top_weights, inv_pos):
-    return torch.empty_like(y), torch.empty_like(top_weights)
+            x.new_empty(E, dtype=i32), x.new_empty(P, dtype=i32), x.new_empty(P, dtype=i32),
+            x.new_empty(P, dtype=f32), x.new_empty(P, 2 * I, dtype=cdt), x.new_empty(P, I, dtype=cdt))
 
 
 @torch.library.custom_op("pmoe::sublayer_bwd", mutates_args=(),
-                         schema="(Tensor? grad_y, Tensor gate_up_proj, Tensor down_proj, Tensor offs, Tensor inv_pos, "
-                                "Tensor x_perm, Tensor gu, Tensor mid, Tensor? grad_normed_add, Tensor x, "
-                                "Tensor norm_weight, Tensor rstd, Tensor? grad_residual, int top_k, bool[] needs, "
-                                "bool[] f32_wgrads) -> (Tensor, Tensor, Tensor, Tensor)")
-def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd,
-                  grad_residual, top_k, needs, f32_wgrads):
-    """Expert GEMM backward, then the dispatch, RMSNorm and residual backward in
-    one row pass: -> grad_x, grad_norm_weight, grad_gate_up, grad_down (empty
-    where needs[i] is false; needs: x, norm_weight, gate_up, down). f32_wgrads
-    (gate_up, down): that weight gradient is fp32 (an fp32 master's)."""
+                         schema="(Tensor? g_gu, Tensor? grad_out_c, Tensor normed, Tensor gate_up_proj, "
+                                "Tensor down_proj, Tensor offs, Tensor inv_pos, Tensor sorted_token, Tensor mid, "
+                                "Tensor? grad_normed_add, Tensor x, Tensor norm_weight, Tensor rstd, "
+                                "Tensor? grad_residual, int top_k, bool[] needs, bool[] f32_wgrads) -> "
+                                "(Tensor, Tensor, Tensor, Tensor)")
+def _sublayer_bwd(g_gu, grad_out_c, normed, gate_up, down, offs, inv_pos, sorted_token, mid, grad_normed_add, x,
+                  norm_weight, rstd, grad_residual, top_k, needs, f32_wgrads):
+    """Expert GEMM backward after the down dgrad, then the dispatch, RMSNorm and
+    residual backward in one row pass: -> grad_x, grad_norm_weight,
+    grad_gate_up, grad_down (empty where needs[i] is false; needs: x,
+    norm_weight, gate_up, down). grad_out_c is the output gradient in the
+    compute dtype (the down wgrad gathers its rows). f32_wgrads (gate_up,
+    down): that weight gradient is fp32 (an fp32 master's)."""
     need_x = needs[0] or needs[1]
 
     def reduce_rows(g_xp):
@@ -649,9 +662,9 @@ def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_no
                                                  top_k, need_weight=needs[1])
 
     reduced = g_gu_w = g_dn_w = None
-    if grad_y is not None:
-        reduced, g_gu_w, g_dn_w = _expert_gemms_backward(grad_y, gate_up, down, offs, x_perm, gu, mid, need_x,
-                                                         needs[2], needs[3], reduce_rows, f32_wgrads)
+    if g_gu is not None:
+        reduced, g_gu_w, g_dn_w = _expert_gemms_backward(g_gu, grad_out_c, normed, gate_up, down, offs, sorted_token,
+                                                         mid, need_x, needs[2], needs[3], reduce_rows, f32_wgrads)
     elif need_x:
         reduced = reduce_rows(None)
     g_x, g_nw = reduced if reduced is not None else (None, None)
@@ -661,8 +674,8 @@ def _sublayer_bwd(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_no
 
 
 @_sublayer_bwd.register_fake
-def _(grad_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, grad_normed_add, x, norm_weight, rstd, grad_residual,
-      top_k, needs, f32_wgrads):
+def _(g_gu, grad_out_c, normed, gate_up, down, offs, inv_pos, sorted_token, mid, grad_normed_add, x, norm_weight,
+      rstd, grad_residual, top_k, needs, f32_wgrads):
     e = _empty_like_none
     return (torch.empty_like(x) if needs[0] else e(x), torch.empty_like(norm_weight) if needs[1] else e(norm_weight),
             _wgrad_fake(gate_up, f32_wgrads[0]) if needs[2] else e(gate_up),
@@ -673,14 +686,14 @@ def _sublayer_setup(ctx, inputs, output):
     (x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master,
      dn_master) = inputs
     ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
-    (out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu, mid,
-     y) = output
-    ctx.save_for_backward(x, norm_weight, rstd, normed, router_weight, logits, top_i, top_w32, top_w, gate_up_proj,
-                          down_proj, offs, inv_pos, x_perm, gu, mid, y)
+    (out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu,
+     mid) = output
+    ctx.save_for_backward(x, norm_weight, rstd, normed, router_weight, logits, top_i, top_w32, gate_up_proj,
+                          down_proj, offs, inv_pos, stok, sw, gu, mid)
     ctx.norm_topk_prob = bool(norm_topk_prob)
     ctx.top_k = int(top_k)
-    ctx.mark_non_differentiable(counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, x_perm, gu,
-                                mid, y)
+    ctx.mark_non_differentiable(counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu,
+                                mid)
     ctx.set_materialize_grads(False)
 
 
@@ -688,8 +701,8 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
     """d out / d x is the identity (the residual) plus the norm-and-MLP path;
     the residual term, the router's share and the K expert rows are all summed
     inside the one row pass of the dispatch backward."""
-    (x, nw, rstd, normed, rw, logits, top_i, top_w32, top_w, gate_up, down, offs, inv_pos, x_perm, gu, mid,
-     y) = ctx.saved_tensors
+    (x, nw, rstd, normed, rw, logits, top_i, top_w32, gate_up, down, offs, inv_pos, stok, sw, gu,
+     mid) = ctx.saved_tensors
     # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
     need = _needs(ctx, 11)
     need_gu, need_dn = need[4] or need[9], need[5] or need[10]
@@ -698,20 +711,25 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
         return nones
     if g_logits is not None:
         g_logits = g_logits.float().contiguous()
-    g_y = g_tw = None
+    g_gu = g_tw = g_out_c = None
     if g_out is not None:
         g_out = g_out.contiguous()
-        g_y, g_tw = torch.ops.pmoe.combine_residual_bwd(g_out, y, top_w, inv_pos)
+        # the expert GEMMs gather rows of the output gradient in the compute dtype
+        g_out_c = g_out if g_out.dtype == gu.dtype else g_out.to(gu.dtype)
+        g_gu, g_tw = torch.ops.pmoe.expert_bwd_dgrad(g_out_c, down, offs, inv_pos, stok, sw, gu, ctx.top_k,
+                                                     bool(need[0] or need[1] or need[3]))
+        g_tw = _none_if_empty(g_tw)
     gx_router = g_rw = None
     if need[0] or need[1] or need[3]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(normed, rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
-    needs = [bool(need[0]), bool(need[1]), bool(need_gu) and g_y is not None, bool(need_dn) and g_y is not None]
+    needs = [bool(need[0]), bool(need[1]), bool(need_gu) and g_gu is not None, bool(need_dn) and g_gu is not None]
     g_x = g_nw = g_gu_w = g_dn_w = None
     if any(needs):
         g_x, g_nw, g_gu_w, g_dn_w = torch.ops.pmoe.sublayer_bwd(
-            g_y, gate_up, down, offs, inv_pos, x_perm, gu, mid, gx_router if (need[0] or need[1]) else None, x, nw,
-            rstd, g_out if need[0] else None, ctx.top_k, needs, ctx.f32_wgrads)
+            g_gu, g_out_c, normed, gate_up, down, offs, inv_pos, stok, mid,
+            gx_router if (need[0] or need[1]) else None, x, nw, rstd, g_out if need[0] else None, ctx.top_k, needs,
+            ctx.f32_wgrads)
         g_x, g_nw, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_x, g_nw, g_gu_w, g_dn_w))
     return (g_x if need[0] else None, g_nw if need[1] else None, None, g_rw if need[3] else None,
             g_gu_w if need[4] else None, g_dn_w if need[5] else None, None, None, None, g_gu_w if need[9] else None,

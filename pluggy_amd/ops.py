@@ -86,13 +86,30 @@ def dispatch(hidden, inv_pos, top_k: int):
     return x_perm
 
 
-def gate_up_swiglu(x_perm, gate_up_proj, offs):
+def sort_rows(sorted_pair, top_weights, top_k: int):
+    """-> sorted_token (P,) int32 = sorted_pair / K, sorted_w (P,) fp32 = top_weights.flatten()[sorted_pair]
+    (sorted_w None when top_weights is None)."""
+    P = sorted_pair.shape[0]
+    dev = sorted_pair.device
+    tok = torch.empty(P, dtype=torch.int32, device=dev)
+    sw = torch.empty(P, dtype=torch.float32, device=dev) if top_weights is not None else None
+    wcode = dtype_code(top_weights.dtype) if top_weights is not None else 0
+    call("pmoe_sort_rows", ptr(sorted_pair), ptr(top_weights), wcode, P // top_k, top_k, ptr(tok), ptr(sw),
+         stream_of(sorted_pair))
+    return tok, sw
+
+
+def gate_up_swiglu(x, gate_up_proj, offs, row_index=None, row_weight=None):
+    """-> gate_up_out (P, 2I), mid (P, I) = row_weight * silu(gate) * up.
+
+    Row p of the GEMM's input is x[row_index[p]] (gathered) or x[p] when
+    row_index is None (x is then the expert-sorted (P, H) copy)."""
     E, H, I = _dims(gate_up_proj)
-    P = x_perm.shape[0]
-    gu = torch.empty(P, 2 * I, dtype=x_perm.dtype, device=x_perm.device)
-    mid = torch.empty(P, I, dtype=x_perm.dtype, device=x_perm.device)
-    call("pmoe_gate_up_swiglu", ptr(x_perm), ptr(gate_up_proj), ptr(offs), dtype_code(x_perm.dtype), P, E, H, I,
-         ptr(gu), ptr(mid), stream_of(x_perm))
+    P = row_index.shape[0] if row_index is not None else x.shape[0]
+    gu = torch.empty(P, 2 * I, dtype=x.dtype, device=x.device)
+    mid = torch.empty(P, I, dtype=x.dtype, device=x.device)
+    call("pmoe_gate_up_swiglu", ptr(x), ptr(row_index), ptr(row_weight), x.shape[0], ptr(gate_up_proj), ptr(offs),
+         dtype_code(x.dtype), P, E, H, I, ptr(gu), ptr(mid), stream_of(x))
     return gu, mid
 
 
@@ -105,12 +122,14 @@ def down_proj(mid, down_proj_w, offs):
     return y
 
 
-def combine(y, top_weights, inv_pos):
-    T, K = top_weights.shape
+def combine(y, top_weights, inv_pos, top_k: int | None = None):
+    """out[t] = sum_k w[t,k] * y[inv_pos[t*K + k]]; top_weights None: unit weights (then give top_k)."""
+    T, K = (top_weights.shape if top_weights is not None else (inv_pos.shape[0] // top_k, top_k))
     H = y.shape[1]
     out = torch.empty(T, H, dtype=y.dtype, device=y.device)
-    call("pmoe_combine", ptr(y), ptr(top_weights), dtype_code(top_weights.dtype), ptr(inv_pos), dtype_code(y.dtype),
-         T, K, H, ptr(out), stream_of(y))
+    wcode = dtype_code(top_weights.dtype) if top_weights is not None else 0
+    call("pmoe_combine", ptr(y), ptr(top_weights), wcode, ptr(inv_pos), dtype_code(y.dtype), T, K, H, ptr(out),
+         stream_of(y))
     return out
 
 
@@ -124,66 +143,94 @@ def combine_backward(grad_out, y, top_weights, inv_pos):
     return gy, gw
 
 
-def down_proj_backward(grad_y, mid, gate_up_out, down_proj_w, offs):
+def part_cols(inter: int) -> int:
+    """Routing-weight partials per sorted row: one per 64-column block of I."""
+    return (inter + 63) // 64
+
+
+def down_proj_backward(grad, mid, gate_up_out, down_proj_w, offs, row_index=None, row_weight=None,
+                       need_part=False):
+    """-> grad_gate_up_out (P, 2I), grad_down_proj, partials (P, ceil(I/64)) fp32 or None.
+
+    The GEMMs' rows of ``grad`` are grad[row_index[p]] (gathered) or grad[p];
+    with row_weight (mid = w * silu(g) * u), grad is the gradient of the
+    weighted rows and the partials sum to the routing weights' gradient."""
     E, H, I = down_proj_w.shape
-    P = grad_y.shape[0]
-    ggu = torch.empty(P, 2 * I, dtype=grad_y.dtype, device=grad_y.device)
+    P = row_index.shape[0] if row_index is not None else grad.shape[0]
+    ggu = torch.empty(P, 2 * I, dtype=grad.dtype, device=grad.device)
     gdn = torch.empty_like(down_proj_w)
-    call("pmoe_down_proj_backward", ptr(grad_y), ptr(mid), ptr(gate_up_out), ptr(down_proj_w), ptr(offs),
-         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), ptr(gdn), dtype_code(gdn.dtype), stream_of(grad_y))
-    return ggu, gdn
+    part = torch.empty(P, part_cols(I), dtype=torch.float32, device=grad.device) if need_part else None
+    call("pmoe_down_proj_backward", ptr(grad), ptr(row_index), ptr(row_weight), grad.shape[0], ptr(mid),
+         ptr(gate_up_out), ptr(down_proj_w), ptr(offs), dtype_code(grad.dtype), P, E, H, I, ptr(ggu), ptr(gdn),
+         dtype_code(gdn.dtype), ptr(part), part_cols(I), stream_of(grad))
+    return ggu, gdn, part
 
 
-def down_proj_dgrad(grad_y, gate_up_out, down_proj_w, offs):
-    """grad_gate_up_out = SwiGLU'(gate_up_out) * (grad_y . down_proj[e]) (one kernel)."""
+def down_proj_dgrad(grad, gate_up_out, down_proj_w, offs, row_index=None, row_weight=None, need_part=False):
+    """grad_gate_up_out = SwiGLU'(gate_up_out) * (w *) (G . down_proj[e]) (one kernel), and with
+    need_part the routing-weight partials (P, ceil(I/64)) fp32 (else None)."""
     E, H, I = down_proj_w.shape
-    P = grad_y.shape[0]
-    ggu = torch.empty(P, 2 * I, dtype=grad_y.dtype, device=grad_y.device)
-    call("pmoe_down_proj_backward", ptr(grad_y), None, ptr(gate_up_out), ptr(down_proj_w), ptr(offs),
-         dtype_code(grad_y.dtype), P, E, H, I, ptr(ggu), None, dtype_code(grad_y.dtype), stream_of(grad_y))
-    return ggu
+    P = row_index.shape[0] if row_index is not None else grad.shape[0]
+    ggu = torch.empty(P, 2 * I, dtype=grad.dtype, device=grad.device)
+    part = torch.empty(P, part_cols(I), dtype=torch.float32, device=grad.device) if need_part else None
+    call("pmoe_down_proj_backward", ptr(grad), ptr(row_index), ptr(row_weight), grad.shape[0], None,
+         ptr(gate_up_out), ptr(down_proj_w), ptr(offs), dtype_code(grad.dtype), P, E, H, I, ptr(ggu), None,
+         dtype_code(grad.dtype), ptr(part), part_cols(I), stream_of(grad))
+    return ggu, part
 
 
-def down_proj_wgrad(grad_y, mid, offs, num_experts: int, out_dtype=None):
-    """grad_down_proj[e] = grad_y_e^T . mid_e (one kernel), in `out_dtype`
-    (default the operands'; fp32 from bf16 operands for an fp32 master weight)."""
-    P, H = grad_y.shape
-    I = mid.shape[1]
-    gdn = torch.empty(num_experts, H, I, dtype=out_dtype or grad_y.dtype, device=grad_y.device)
-    call("pmoe_down_proj_backward", ptr(grad_y), ptr(mid), None, None, ptr(offs), dtype_code(grad_y.dtype), P,
-         num_experts, H, I, None, ptr(gdn), dtype_code(gdn.dtype), stream_of(grad_y))
+def down_proj_wgrad(grad, mid, offs, num_experts: int, out_dtype=None, row_index=None):
+    """grad_down_proj[e] = G_e^T . mid_e (one kernel), G_p = grad[row_index[p]] or grad[p], in
+    `out_dtype` (default the operands'; fp32 from bf16 operands for an fp32 master weight)."""
+    H = grad.shape[1]
+    P, I = mid.shape
+    gdn = torch.empty(num_experts, H, I, dtype=out_dtype or grad.dtype, device=grad.device)
+    call("pmoe_down_proj_backward", ptr(grad), ptr(row_index), None, grad.shape[0], ptr(mid), None, None, ptr(offs),
+         dtype_code(grad.dtype), P, num_experts, H, I, None, ptr(gdn), dtype_code(gdn.dtype), None, 0,
+         stream_of(grad))
     return gdn
 
 
 def gate_up_dgrad(grad_gate_up_out, gate_up_proj, offs):
-    """grad_x_perm = grad_gate_up_out . gate_up_proj[e] (one kernel)."""
+    """grad_x_perm = grad_gate_up_out . gate_up_proj[e] (one kernel; the sorted rows' input gradient)."""
     E, H, I = _dims(gate_up_proj)
     P = grad_gate_up_out.shape[0]
     gx = torch.empty(P, H, dtype=grad_gate_up_out.dtype, device=grad_gate_up_out.device)
-    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), None, ptr(gate_up_proj), ptr(offs),
+    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), None, None, P, ptr(gate_up_proj), ptr(offs),
          dtype_code(gx.dtype), P, E, H, I, ptr(gx), None, dtype_code(gx.dtype), stream_of(gx))
     return gx
 
 
-def gate_up_wgrad(grad_gate_up_out, x_perm, offs, num_experts: int, out_dtype=None):
-    """grad_gate_up_proj[e] = grad_gate_up_out_e^T . x_perm_e (one kernel), in
-    `out_dtype` (default the operands'; fp32 from bf16 operands for an fp32 master)."""
-    P, H = x_perm.shape
+def gate_up_wgrad(grad_gate_up_out, x, offs, num_experts: int, out_dtype=None, row_index=None):
+    """grad_gate_up_proj[e] = grad_gate_up_out_e^T . X_e, X_p = x[row_index[p]] or x[p] (one kernel),
+    in `out_dtype` (default the operands'; fp32 from bf16 operands for an fp32 master)."""
+    H = x.shape[1]
+    P = grad_gate_up_out.shape[0]
     I = grad_gate_up_out.shape[1] // 2
-    gw = torch.empty(num_experts, 2 * I, H, dtype=out_dtype or x_perm.dtype, device=x_perm.device)
-    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x_perm), None, ptr(offs), dtype_code(x_perm.dtype),
-         P, num_experts, H, I, None, ptr(gw), dtype_code(gw.dtype), stream_of(x_perm))
+    gw = torch.empty(num_experts, 2 * I, H, dtype=out_dtype or x.dtype, device=x.device)
+    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x), ptr(row_index), x.shape[0], None, ptr(offs),
+         dtype_code(x.dtype), P, num_experts, H, I, None, ptr(gw), dtype_code(gw.dtype), stream_of(x))
     return gw
 
 
-def gate_up_backward(grad_gate_up_out, x_perm, gate_up_proj, offs):
+def gate_up_backward(grad_gate_up_out, x, gate_up_proj, offs, row_index=None):
     E, H, I = _dims(gate_up_proj)
-    P = x_perm.shape[0]
-    gx = torch.empty_like(x_perm)
+    P = grad_gate_up_out.shape[0]
+    gx = torch.empty(P, H, dtype=x.dtype, device=x.device)
     gw = torch.empty_like(gate_up_proj)
-    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x_perm), ptr(gate_up_proj), ptr(offs),
-         dtype_code(x_perm.dtype), P, E, H, I, ptr(gx), ptr(gw), dtype_code(gw.dtype), stream_of(x_perm))
+    call("pmoe_gate_up_backward", ptr(grad_gate_up_out), ptr(x), ptr(row_index), x.shape[0], ptr(gate_up_proj),
+         ptr(offs), dtype_code(x.dtype), P, E, H, I, ptr(gx), ptr(gw), dtype_code(gw.dtype), stream_of(x))
     return gx, gw
+
+
+def pair_weight_grad(part, inv_pos, top_k: int, out_dtype=torch.float32):
+    """grad_top_weights (T, K) = the sum of each pair's row partials (from down_proj_backward)."""
+    P, ld = part.shape
+    T = P // top_k
+    gw = torch.empty(T, top_k, dtype=out_dtype, device=part.device)
+    call("pmoe_pair_weight_grad", ptr(part), ld, ld, ptr(inv_pos), T, top_k, ptr(gw), dtype_code(out_dtype),
+         stream_of(part))
+    return gw
 
 
 def dispatch_backward(grad_x_perm, inv_pos, tokens: int, top_k: int, add=None):
@@ -211,13 +258,15 @@ def rmsnorm_forward(x, weight, eps: float, out_dtype):
     return out, rstd
 
 
-def combine_residual(y, top_weights, inv_pos, residual):
-    """out (residual.dtype) = residual + the weighted K-sum of the expert rows."""
-    T, K = top_weights.shape
+def combine_residual(y, top_weights, inv_pos, residual, top_k: int | None = None):
+    """out (residual.dtype) = residual + the (weighted) K-sum of the expert rows; top_weights None: unit weights."""
+    T = residual.shape[0]
+    K = top_weights.shape[1] if top_weights is not None else top_k
     H = y.shape[1]
     out = torch.empty_like(residual)
-    call("pmoe_combine_residual", ptr(y), ptr(top_weights), dtype_code(top_weights.dtype), ptr(inv_pos),
-         dtype_code(y.dtype), ptr(residual), dtype_code(residual.dtype), T, K, H, ptr(out), stream_of(y))
+    wcode = dtype_code(top_weights.dtype) if top_weights is not None else 0
+    call("pmoe_combine_residual", ptr(y), ptr(top_weights), wcode, ptr(inv_pos), dtype_code(y.dtype), ptr(residual),
+         dtype_code(residual.dtype), T, K, H, ptr(out), stream_of(y))
     return out
 
 

@@ -102,9 +102,10 @@ def dispatch_bytes(cfg: MoEConfig) -> float:
 
 
 def combine_bytes(cfg: MoEConfig) -> float:
-    """Compulsory bytes of the weighted combine: read P*H + P weights, write T*H."""
+    """Compulsory bytes of the combine: read the P weighted rows (P*H) and their
+    positions (P int32), write T*H (the routing weight is already in the rows)."""
     es = 2 if cfg.dtype == torch.bfloat16 else 4
-    return cfg.pairs * cfg.hidden * es + cfg.pairs * (4 + es) + cfg.tokens * cfg.hidden * es
+    return cfg.pairs * cfg.hidden * es + cfg.pairs * 4 + cfg.tokens * cfg.hidden * es
 
 
 def log2_ceil(n: int) -> int:

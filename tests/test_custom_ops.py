@@ -45,9 +45,10 @@ def test_router_bwd_fake(pmoe_ops):
 def test_expert_ffn_fwd_fake(pmoe_ops):
     out = pmoe_ops.expert_ffn_fwd(_meta(T, H), _meta(T, K, dtype=torch.int64), _meta(T, K), _meta(E, 2 * I, H),
                                   _meta(E, H, I))
-    bf, i32 = torch.bfloat16, torch.int32
-    assert _sig(out) == [((T, H), bf), ((E,), i32), ((P,), i32), ((P, H), bf), ((P, 2 * I), bf), ((P, I), bf),
-                         ((P, H), bf)]
+    bf, i32, f32 = torch.bfloat16, torch.int32, torch.float32
+    # out, then what the backward reads: offs, inv_pos, sorted_token, sorted_w, gate_up_out, mid
+    assert _sig(out) == [((T, H), bf), ((E,), i32), ((P,), i32), ((P,), i32), ((P,), f32), ((P, 2 * I), bf),
+                         ((P, I), bf)]
 
 
 def test_sparse_moe_fwd_fake(pmoe_ops):
@@ -55,14 +56,22 @@ def test_sparse_moe_fwd_fake(pmoe_ops):
                                   K, False, None)
     bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
     assert _sig(out) == [((T, H), bf), ((T, E), f32), ((E,), i32), ((E,), f32), ((1,), f32), ((T, K), torch.int64),
-                         ((T, K), f32), ((T, K), bf), ((E,), i32), ((P,), i32), ((P, H), bf), ((P, 2 * I), bf),
-                         ((P, I), bf), ((P, H), bf)]
+                         ((T, K), f32), ((T, K), bf), ((E,), i32), ((P,), i32), ((P,), i32), ((P,), f32),
+                         ((P, 2 * I), bf), ((P, I), bf)]
 
 
 def test_backward_fakes_drop_unneeded_grads(pmoe_ops):
-    gy, gu, dn = _meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I)
-    i32 = torch.int32
-    args = (gy, gu, dn, _meta(E, dtype=i32), _meta(P, dtype=i32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), None, T, K)
+    gu, dn = _meta(E, 2 * I, H), _meta(E, H, I)
+    i32, f32 = torch.int32, torch.float32
+    # the down dgrad: grad_gate_up_out and, when asked, the routing weights' gradient (fp32)
+    g_gu, g_w = pmoe_ops.expert_bwd_dgrad(_meta(T, H), dn, _meta(E, dtype=i32), _meta(P, dtype=i32),
+                                          _meta(P, dtype=i32), _meta(P, dtype=f32), _meta(P, 2 * I), K, True)
+    assert _sig([g_gu, g_w]) == [((P, 2 * I), torch.bfloat16), ((T, K), f32)]
+    _, g_w = pmoe_ops.expert_bwd_dgrad(_meta(T, H), dn, _meta(E, dtype=i32), _meta(P, dtype=i32),
+                                       _meta(P, dtype=i32), _meta(P, dtype=f32), _meta(P, 2 * I), K, False)
+    assert g_w.numel() == 0
+    args = (_meta(P, 2 * I), _meta(T, H), _meta(T, H), gu, dn, _meta(E, dtype=i32), _meta(P, dtype=i32),
+            _meta(P, dtype=i32), _meta(P, I), None, K)
     gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [True, False, True], [False, False])
     assert _sig([gh, gdn]) == [((T, H), torch.bfloat16), ((E, H, I), torch.bfloat16)]
     assert ggu.numel() == 0  # absent gradient: empty stand-in
@@ -70,8 +79,6 @@ def test_backward_fakes_drop_unneeded_grads(pmoe_ops):
     gh, ggu, gdn = pmoe_ops.expert_bwd(*args, [False, True, True], [True, True])
     assert _sig([ggu, gdn]) == [((E, 2 * I, H), torch.float32), ((E, H, I), torch.float32)]
     assert gh.numel() == 0
-    g_y, g_w = pmoe_ops.combine_bwd(_meta(T, H), _meta(P, H), _meta(T, K), _meta(P, dtype=i32))
-    assert _sig([g_y, g_w]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]
 
 
 def test_forward_ops_take_optional_masters(pmoe_ops):
@@ -93,17 +100,15 @@ def test_moe_sublayer_fwd_fake(pmoe_ops):
     bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
     assert _sig(out) == [((T, H), f32), ((T, E), f32), ((E,), i32), ((E,), f32), ((1,), f32), ((T, H), bf),
                          ((T,), f32), ((T, K), torch.int64), ((T, K), f32), ((T, K), bf), ((E,), i32), ((P,), i32),
-                         ((P, H), bf), ((P, 2 * I), bf), ((P, I), bf), ((P, H), bf)]
+                         ((P,), i32), ((P,), f32), ((P, 2 * I), bf), ((P, I), bf)]
 
 
 def test_sublayer_backward_fakes(pmoe_ops):
-    gy, gw = pmoe_ops.combine_residual_bwd(_meta(T, H, dtype=torch.float32), _meta(P, H), _meta(T, K),
-                                           _meta(P, dtype=torch.int32))
-    assert _sig([gy, gw]) == [((P, H), torch.bfloat16), ((T, K), torch.bfloat16)]
     x, nw = _meta(T, H, dtype=torch.float32), _meta(H, dtype=torch.float32)
-    outs = pmoe_ops.sublayer_bwd(_meta(P, H), _meta(E, 2 * I, H), _meta(E, H, I), _meta(E, dtype=torch.int32),
-                                 _meta(P, dtype=torch.int32), _meta(P, H), _meta(P, 2 * I), _meta(P, I), _meta(T, H),
-                                 x, nw, _meta(T, dtype=torch.float32), x, K, [True, False, True, True],
+    i32 = torch.int32
+    outs = pmoe_ops.sublayer_bwd(_meta(P, 2 * I), _meta(T, H), _meta(T, H), _meta(E, 2 * I, H), _meta(E, H, I),
+                                 _meta(E, dtype=i32), _meta(P, dtype=i32), _meta(P, dtype=i32), _meta(P, I),
+                                 _meta(T, H), x, nw, _meta(T, dtype=torch.float32), x, K, [True, False, True, True],
                                  [False, True])
     assert _sig(outs) == [((T, H), torch.float32), ((0,), torch.float32), ((E, 2 * I, H), torch.bfloat16),
                           ((E, H, I), torch.float32)]

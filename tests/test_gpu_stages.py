@@ -170,7 +170,7 @@ def test_down_proj_backward(dtype, case):
     gy = torch.randn(P, H, generator=g).to(dtype)
     gu = torch.randn(P, 2 * I, generator=g).to(dtype)
     mid = torch.randn(P, I, generator=g).to(dtype)
-    ggu, gdn = ops.down_proj_backward(gy.to(DEV), mid.to(DEV), gu.to(DEV), wdn.to(DEV), offs)
+    ggu, gdn, _ = ops.down_proj_backward(gy.to(DEV), mid.to(DEV), gu.to(DEV), wdn.to(DEV), offs)
     o = offs.cpu()
     dmid = ref_grouped(gy, wdn, o, trans_w=False)          # (P, I) = gy_e @ W_dn[e]
     gate, up = gu.double()[:, :I], gu.double()[:, I:]
@@ -229,6 +229,65 @@ def test_weight_gradients_in_fp32(case):
         for e, (lo, hi) in enumerate(seg_bounds(o)):
             if hi == lo:
                 assert torch.count_nonzero(f32_out[e]).item() == 0, "an empty expert has a zero weight gradient"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_gathered_rows_and_routing_weights(dtype, case):
+    """The forward and backward GEMMs over rows gathered from token-major tensors
+    (hidden, the output gradient) with the routing weight in the activation:
+    against fp64 of the materialised form (x[sorted_token], w * mid, ...)."""
+    T, K, E, H, I, mode = case
+    say(f"gathered rows {case} {dtype}")
+    ops = _ops()
+    idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, dtype)
+    g = gen(13)
+    P = T * K
+    tw = torch.rand(T, K, generator=g).to(dtype)
+    gout = torch.randn(T, H, generator=g).to(dtype)
+    stok, sw = ops.sort_rows(sp, tw.to(DEV), K)
+    o = offs.cpu()
+    # sort_rows: token and weight of every sorted row, bit for bit
+    sp64 = sp.cpu().long()
+    assert torch.equal(stok.cpu(), (sp64 // K).int())
+    assert torch.equal(sw.cpu(), tw.reshape(-1)[sp64].float())
+    tok = stok.cpu().long()
+    w64 = sw.cpu().double().unsqueeze(1)
+    # forward: gate_up over gathered rows, weighted mid
+    gu, mid = ops.gate_up_swiglu(x.to(DEV), wgu.to(DEV), offs, stok, sw)
+    ref_gu = ref_grouped(x[tok], wgu, o, trans_w=True)
+    check_close("gate_up (gathered)", gu, ref_gu, TOL[dtype], MAX_ABS_FRAC[dtype])
+    gq = gu.cpu().double()
+    check_close("w * mid", mid, w64 * silu64(gq[:, :I]) * gq[:, I:], TOL[dtype], MAX_ABS_FRAC[dtype])
+    # down backward from the gathered output gradient
+    ggu, gdn, part = ops.down_proj_backward(gout.to(DEV), mid, gu, wdn.to(DEV), offs, stok, sw, need_part=True)
+    G = gout[tok]
+    acc = ref_grouped(G, wdn, o, trans_w=False)                     # d(w * mid)
+    gate, up = gq[:, :I], gq[:, I:]
+    s_ = torch.sigmoid(gate)
+    dm = w64 * acc
+    ref_ggu = torch.cat([dm * up * s_ * (1 + gate * (1 - s_)), dm * gate * s_], dim=1)
+    check_close("dgate_up (gathered, weighted)", ggu, ref_ggu, TOL[dtype], MAX_ABS_FRAC[dtype])
+    check_close("d down_proj (gathered)", gdn, ref_wgrad(G, mid.cpu(), o), TOL[dtype], MAX_ABS_FRAC[dtype])
+    # the routing weights' gradient: <acc, silu(g) u> per row, by 64-column block, then summed per pair
+    prod = acc * (gate * s_ * up)
+    nb = (I + 63) // 64
+    ref_part = torch.stack([prod[:, 64 * c:64 * (c + 1)].sum(1) for c in range(nb)], 1)
+    check_close("weight partials", part, ref_part, 1e-5, 1e-4)
+    gtw = ops.pair_weight_grad(part, inv, K)
+    ref_gtw = ref_part.sum(1)[inv.cpu().long()].reshape(T, K)
+    check_close("d top_weights", gtw, ref_gtw, 1e-5, 1e-4)
+    # gate_up backward: dgrad on the sorted rows, wgrad over gathered rows
+    g2 = torch.randn(P, 2 * I, generator=gen(17)).to(dtype)
+    gxp, gwgu = ops.gate_up_backward(g2.to(DEV), x.to(DEV), wgu.to(DEV), offs, row_index=stok)
+    check_close("d x_perm", gxp, ref_grouped(g2, wgu, o, trans_w=False), TOL[dtype], MAX_ABS_FRAC[dtype])
+    check_close("d gate_up_proj (gathered)", gwgu, ref_wgrad(g2, x[tok], o), TOL[dtype], MAX_ABS_FRAC[dtype])
+    if dtype == torch.bfloat16:
+        # fp32 weight gradients over gathered rows: the same tiles unrounded
+        f32 = torch.float32
+        gw32 = ops.gate_up_wgrad(g2.to(DEV), x.to(DEV), offs, E, f32, row_index=stok)
+        gd32 = ops.down_proj_wgrad(gout.to(DEV), mid, offs, E, f32, row_index=stok)
+        assert torch.equal(gw32.to(dtype), gwgu) and torch.equal(gd32.to(dtype), gdn)
 
 
 # ----------------------------------------------------------------- router
@@ -338,22 +397,24 @@ def test_fused_expert_ffn_entry_points(dtype):
     offs = torch.empty(E, dtype=torch.int32, device=DEV)
     sp = torch.empty(P, dtype=torch.int32, device=DEV)
     inv = torch.empty(P, dtype=torch.int32, device=DEV)
-    xp = torch.empty(P, H, dtype=dtype, device=DEV)
+    stok = torch.empty(P, dtype=torch.int32, device=DEV)
+    sw = torch.empty(P, dtype=torch.float32, device=DEV)
     gu = torch.empty(P, 2 * I, dtype=dtype, device=DEV)
     mid = torch.empty(P, I, dtype=dtype, device=DEV)
     y = torch.empty(P, H, dtype=dtype, device=DEV)
     wsp = workspace(size("pmoe_expert_ffn_forward_workspace_size", T, K, E), DEV)
     stream = torch.cuda.current_stream().cuda_stream
     call("pmoe_expert_ffn_forward", ptr(x), ptr(idx), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(out),
-         ptr(counts), ptr(offs), ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(wsp), wsp.numel(), stream)
+         ptr(counts), ptr(offs), ptr(sp), ptr(inv), ptr(stok), ptr(sw), ptr(gu), ptr(mid), ptr(y), ptr(wsp),
+         wsp.numel(), stream)
     gx = torch.empty_like(x)
     gw = torch.empty_like(w)
     ggu = torch.empty_like(wgu)
     gdn = torch.empty_like(wdn)
     wsb = workspace(size("pmoe_expert_ffn_backward_workspace_size", T, K, H, I, dt), DEV)
-    call("pmoe_expert_ffn_backward", ptr(gout), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
-         ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), ptr(gx), ptr(gw), ptr(ggu), ptr(gdn), dt,
-         ptr(wsb), wsb.numel(), stream)
+    call("pmoe_expert_ffn_backward", ptr(gout), ptr(x), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
+         ptr(inv), ptr(stok), ptr(sw), ptr(gu), ptr(mid), ptr(gx), ptr(gw), ptr(ggu), ptr(gdn), dt, ptr(wsb),
+         wsb.numel(), stream)
     torch.cuda.synchronize()
     assert torch.equal(out, out_s)
     assert torch.equal(gx, xs.grad) and torch.equal(gw, ws_.grad)
@@ -362,8 +423,8 @@ def test_fused_expert_ffn_entry_points(dtype):
         # weight gradients of fp32 masters: the unrounded accumulators of the same tiles
         ggu32 = torch.empty(wgu.shape, dtype=torch.float32, device=DEV)
         gdn32 = torch.empty(wdn.shape, dtype=torch.float32, device=DEV)
-        call("pmoe_expert_ffn_backward", ptr(gout), ptr(w), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
-             ptr(sp), ptr(inv), ptr(xp), ptr(gu), ptr(mid), ptr(y), None, None, ptr(ggu32), ptr(gdn32),
+        call("pmoe_expert_ffn_backward", ptr(gout), ptr(x), dt, ptr(wgu), ptr(wdn), dt, T, K, E, H, I, ptr(offs),
+             ptr(inv), ptr(stok), ptr(sw), ptr(gu), ptr(mid), None, None, ptr(ggu32), ptr(gdn32),
              dtype_code(torch.float32), ptr(wsb), wsb.numel(), stream)
         torch.cuda.synchronize()
         assert torch.equal(ggu32.to(dtype), ggu) and torch.equal(gdn32.to(dtype), gdn)

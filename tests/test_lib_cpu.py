@@ -109,8 +109,13 @@ def test_weight_gradient_dtype_is_checked(lib, entry):
     from pluggy_amd import _lib
 
     P, E, H, I = 64, 4, 64, 32
-    nulls = (None,) * (5 if entry == "pmoe_down_proj_backward" else 4)
-    rc = getattr(lib, entry)(*nulls, _lib.PMOE_F32, P, E, H, I, None, None, _lib.PMOE_BF16, None)
+    if entry == "pmoe_down_proj_backward":  # grad, row_index, row_weight, grad_rows, mid, gate_up_out, down, offs
+        lead = (None, None, None, P, None, None, None, None)
+        tail = (None, None, _lib.PMOE_BF16, None, 0, None)
+    else:  # grad_gate_up_out, x, row_index, x_rows, gate_up_proj, offs
+        lead = (None, None, None, P, None, None)
+        tail = (None, None, _lib.PMOE_BF16, None)
+    rc = getattr(lib, entry)(*lead, _lib.PMOE_F32, P, E, H, I, *tail)
     assert rc == -1 and b"dtype must be the operands' or fp32" in lib.pmoe_last_error_string()
 
 
@@ -123,4 +128,4 @@ def test_noalloc_forward_rejects_sizes_beyond_its_static_scratch(lib):
     T, K, E, H, I = 131073, 8, 128, 64, 32  # 513 chunks x 128 experts x 4 bytes > 256 KiB
     with pytest.raises(RuntimeError, match="static maximum"):
         _lib.call("pmoe_expert_ffn_forward_noalloc", *([None] * 3), _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
-                  T, K, E, H, I, *([None] * 9), None)
+                  T, K, E, H, I, *([None] * 10), None)

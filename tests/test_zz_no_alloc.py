@@ -29,13 +29,14 @@ def _inputs(T, K, E, H, I, seed):
 
 
 def _outputs(T, K, E, H, I):
+    """out, counts, offs, sorted_pair, inv_pos, sorted_token, sorted_w, gate_up_out, mid, y."""
     P = T * K
     bf, i32 = torch.bfloat16, torch.int32
     return [torch.empty(T, H, dtype=bf, device=DEV), torch.empty(E, dtype=i32, device=DEV),
             torch.empty(E, dtype=i32, device=DEV), torch.empty(P, dtype=i32, device=DEV),
-            torch.empty(P, dtype=i32, device=DEV), torch.empty(P, H, dtype=bf, device=DEV),
-            torch.empty(P, 2 * I, dtype=bf, device=DEV), torch.empty(P, I, dtype=bf, device=DEV),
-            torch.empty(P, H, dtype=bf, device=DEV)]
+            torch.empty(P, dtype=i32, device=DEV), torch.empty(P, dtype=i32, device=DEV),
+            torch.empty(P, dtype=torch.float32, device=DEV), torch.empty(P, 2 * I, dtype=bf, device=DEV),
+            torch.empty(P, I, dtype=bf, device=DEV), torch.empty(P, H, dtype=bf, device=DEV)]
 
 
 def _call(name, inp, outs, T, K, E, H, I, ws=None):
@@ -75,4 +76,4 @@ def test_noalloc_rejects_sizes_beyond_the_static_scratch():
     T, K, E, H, I = 131073, 8, 128, 64, 32  # one chunk more than 256 KiB of histograms hold
     with pytest.raises(RuntimeError, match="static maximum"):
         _lib.call("pmoe_expert_ffn_forward_noalloc", *([None] * 3), _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
-                  T, K, E, H, I, *([None] * 9), None)
+                  T, K, E, H, I, *([None] * 10), None)
