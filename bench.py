@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -72,7 +73,8 @@ def cpu_model() -> str:
 def cpu_baseline(cfg, tokens: int | None, iters: int = 3):
     """The reference CPU path (router + per-expert loop, autograd backward), restated in oracle/.
 
-    One warm-up step, then ``iters`` timed steps; the median is reported. The
+    One warm-up step, then ``iters`` timed runs (each of as many steps as
+    fill about a second); the median per step is reported. The
     sample is the first ``tokens`` tokens' worth of the workload (a fresh
     seeded draw of that size, same layer shape)."""
     import torch
@@ -92,12 +94,17 @@ def cpu_baseline(cfg, tokens: int | None, iters: int = 3):
         if cfg.backward:
             y.reshape(T, H).backward(inp["grad_out"])
 
+    t0 = time.perf_counter()
     step()  # warm-up
+    # a timed run repeats the step until it lasts about a second (config 1's
+    # forward takes milliseconds), so the median is not timer noise
+    reps = max(1, math.ceil(1.0 / max(time.perf_counter() - t0, 1e-3)))
     times = []
     for _ in range(iters):
         t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
+        for _ in range(reps):
+            step()
+        times.append((time.perf_counter() - t0) / reps)
     dt = statistics.median(times)
     return {
         "value": round(T / dt, 2),
@@ -106,7 +113,8 @@ def cpu_baseline(cfg, tokens: int | None, iters: int = 3):
         "kind": "port",
         "sample": (f"{'fwd+bwd' if cfg.backward else 'fwd'} steps of the restated reference CPU path (fp32 router + "
                    f"per-expert loop, moe.py:38-65, torch autograd) at T={T} of the {cfg.name} layer, {cfg.dtype}: "
-                   f"1 warm-up + {iters} timed, median {dt:.2f} s (runs {', '.join(f'{t:.2f}' for t in times)} s)"),
+                   f"1 warm-up + {iters} timed runs of {reps} step(s), median {dt:.4g} s per step "
+                   f"(runs {', '.join(f'{t:.4g}' for t in times)} s)"),
         "cpu_model": cpu_model(),
         "os_cpu_count": os.cpu_count(),
         "torch": torch.__version__,
