@@ -54,6 +54,12 @@ CONFIGS = {
 }
 
 
+# Not a BASELINE.json configuration: the MoE layer of pluggy's own MoE training
+# config (configs/qwen3_moe_climbmix.json:4-19; micro batch 2 x seq 4096).
+CLIMBMIX = MoEConfig("qwen3-moe-climbmix", 8192, 1024, 32, 4, 512, torch.bfloat16, True, batch=2,
+                     notes="pluggy's qwen3_moe_climbmix training shape")
+
+
 def zipf_logit_bias(num_experts: int, s: float, seed: int = 2) -> torch.Tensor:
     """b_e = ln q_e - mean(ln q), q_e ~ (r_e + 1)^-s, r a seeded permutation of ids."""
     g = torch.Generator().manual_seed(seed)

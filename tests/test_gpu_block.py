@@ -247,20 +247,20 @@ def _check_routing_vs_cpu(x, Wr, gpu_logits, K, bias=None):
     return len(bad)
 
 
-def _run_config(cfg_id: int, tokens: int | None = None):
+def _run_config(cfg_id, tokens: int | None = None):
     """One configuration at full size: routing, counts and permutation bit-exact;
     the router statistics against the oracle; every output row, the whole input
     gradient, every expert's weight gradients and the full router weight gradient
     against fp64 truth (``ref_layer_fp64``) with rel-L2 and max-abs bounds;
     bitwise run-to-run determinism."""
-    from pluggy_amd.workloads import CONFIGS, make_inputs
+    from pluggy_amd.workloads import CONFIGS, MoEConfig, make_inputs
 
     pa = _mod()
-    cfg = CONFIGS[cfg_id]
+    cfg = cfg_id if isinstance(cfg_id, MoEConfig) else CONFIGS[cfg_id]
     inp = make_inputs(cfg, tokens=tokens)
     T = inp["x"].shape[0]
     H, E, K, I = cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
-    say(f"config {cfg_id} ({cfg.name}) T={T} H={H} E={E} K={K} I={I} {cfg.dtype} backward={cfg.backward}")
+    say(f"config {cfg_id if isinstance(cfg_id, int) else '-'} ({cfg.name}) T={T} H={H} E={E} K={K} I={I} {cfg.dtype} backward={cfg.backward}")
     mlp = pa.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(DEV)
     with torch.no_grad():
         mlp.router.weight.copy_(inp["router_weight"])
@@ -352,6 +352,13 @@ def test_config2_qwen3_30b_a3b():
 
 def test_config4_skewed():
     _run_config(4)
+
+
+def test_config_climbmix():
+    """pluggy's own MoE training shape (H=1024, E=32, top-4, I=512, T=8192)."""
+    from pluggy_amd.workloads import CLIMBMIX
+
+    _run_config(CLIMBMIX)
 
 
 def test_config5_decode():

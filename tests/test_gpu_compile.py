@@ -3,15 +3,21 @@
 The reference compiles every transformer block (pluggy/training/trainer.py:
 292-293), so the drop-in must trace without graph breaks: the MoE half of a
 block (RMSNorm -> sparse MLP -> residual add, qwen3_moe.py:281) is compiled
-with ``fullgraph=True`` and must give the eager results bit for bit (the same
-kernels run), including the gradient of an aux loss through the router logits.
+with ``fullgraph=True``, including the gradient of an aux loss through the
+router logits. With ``backend="aot_eager"`` the same kernels run, so the
+results must equal eager bit for bit. With the trainer's own backend (inductor,
+``block.compile(mode="default")``) the RMSNorm, the residual add and the
+z-loss become generated kernels whose fp32 reductions may be ordered
+differently, so the bar is the dtype's (rel-L2 and max-abs as everywhere
+else), the routing must equal eager's, and a second call must reproduce the
+first bit for bit.
 """
 
 import pytest
 import torch
 from torch import nn
 
-from _gpu_helpers import DEV, gen, say
+from _gpu_helpers import DEV, MAX_ABS_FRAC, check_close, gen, say
 
 pytestmark = pytest.mark.gpu
 
@@ -59,10 +65,12 @@ class _MoEHalfBlock(nn.Module):
         return y, z
 
 
+@pytest.mark.timeout(600)  # inductor compiles its kernels on first use
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_compiled_block_matches_eager(dtype):
+def test_compiled_block_matches_eager(dtype, backend):
     B, S, H, E, K, I = 2, 128, 256, 16, 4, 128
-    say(f"compile B={B} S={S} H={H} E={E} K={K} I={I} {dtype}")
+    say(f"compile[{backend}] B={B} S={S} H={H} E={E} K={K} I={I} {dtype}")
     torch.manual_seed(0)
     block = _MoEHalfBlock(H, I, E, K).to(DEV)
     rw, gu, dn = _weights(E, H, I, seed=3)
@@ -80,15 +88,24 @@ def test_compiled_block_matches_eager(dtype):
         x = x0.clone().requires_grad_(True)
         y, z = mod(x)
         (y.float().pow(2).mean() + 1e-3 * z).backward()
-        return [y.detach(), z.detach(), x.grad] + [prm.grad.clone() for prm in block.parameters()]
+        ids = block.ffn.router.last_stats.expert_counts.clone()
+        return [y.detach(), z.detach(), x.grad] + [prm.grad.clone() for prm in block.parameters()], ids
 
-    eager = run(block)
+    eager, eager_counts = run(block)
     torch._dynamo.reset()
-    compiled = torch.compile(block, backend="aot_eager", fullgraph=True)
-    got = run(compiled)
-    got2 = run(compiled)  # a second call reuses the compiled graph
+    if backend == "inductor":
+        compiled = torch.compile(block, mode="default", fullgraph=True)  # trainer.py:291-293
+    else:
+        compiled = torch.compile(block, backend="aot_eager", fullgraph=True)
+    got, got_counts = run(compiled)
+    got2, _ = run(compiled)  # a second call reuses the compiled graph
+    assert torch.equal(got_counts, eager_counts)
     names = ["y", "z", "dx"] + [n for n, _ in block.named_parameters()]
     for n, a, b, c in zip(names, eager, got, got2):
         say(f"  {n}: max|compiled - eager| = {(a.float() - b.float()).abs().max().item():.3e}")
-        assert torch.equal(a, b), n
+        if backend == "aot_eager":
+            assert torch.equal(a, b), n
+        else:
+            check_close(f"{n} (inductor vs eager)", b, a, 1e-2 if dtype == torch.bfloat16 else 1e-5,
+                        MAX_ABS_FRAC[dtype])
         assert torch.equal(b, c), n

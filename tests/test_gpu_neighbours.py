@@ -222,9 +222,14 @@ class _FusedHalfBlock(nn.Module):
         return pa.moe_sublayer(x, self.norm2, self.ffn)
 
 
-def test_moe_sublayer_compiled_matches_eager():
+@pytest.mark.timeout(600)  # inductor compiles its kernels on first use
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
+def test_moe_sublayer_compiled_matches_eager(backend):
+    """aot_eager runs the eager kernels: bitwise equal. Inductor (the trainer's
+    ``block.compile(mode="default")``, trainer.py:291-293) generates the loss
+    terms around the fused custom op: the dtype's bar, and bitwise reproducible."""
     B, S, H, E, K, I = 2, 64, 256, 16, 4, 128
-    say(f"moe_sublayer compiled B={B} S={S} H={H} E={E} K={K} I={I} (autocast bf16, fp32 stream)")
+    say(f"moe_sublayer compiled[{backend}] B={B} S={S} H={H} E={E} K={K} I={I} (autocast bf16, fp32 stream)")
     torch.manual_seed(0)
     blk = _FusedHalfBlock(H, I, E, K).to(DEV)
     g = gen(55)
@@ -245,8 +250,15 @@ def test_moe_sublayer_compiled_matches_eager():
 
     eager = run(blk)
     torch._dynamo.reset()
-    compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
+    if backend == "inductor":
+        compiled = torch.compile(blk, mode="default", fullgraph=True)
+    else:
+        compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
     got = run(compiled)
     got2 = run(compiled)
     for i, (a, b, c) in enumerate(zip(eager, got, got2)):
-        assert torch.equal(a, b) and torch.equal(b, c), i
+        if backend == "aot_eager":
+            assert torch.equal(a, b), i
+        else:
+            check_close(f"record {i} (inductor vs eager)", b, a, 1e-2, MAX_ABS_FRAC[bf16])
+        assert torch.equal(b, c), i
