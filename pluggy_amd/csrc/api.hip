@@ -72,9 +72,12 @@ int64_t router_blocks(int64_t T) { return (T + router_rows(T) - 1) / router_rows
 // times three piece n-tiles fall short of the 256 CUs when tokens are few
 // (decode), so the reduction over H is split (chunks of at least 256) until
 // there are about 256 tiles; the top-k kernel sums the planes in order.
-int router_logit_splits(int64_t T, int64_t H) {
+// Split of the logits GEMM's reduction over H: enough blocks to cover the
+// GPU's 256 CUs. pieces: the three-piece tiles of an fp32 weight (128 x 128
+// outputs) rather than the 64 x 64 tiles of a bf16 weight.
+int router_logit_splits(int64_t T, int64_t H, int64_t E, bool pieces) {
   if (T <= 0) return 1;
-  const int64_t tiles = 3 * ((T + 63) / 64);
+  const int64_t tiles = pieces ? ((T + 127) / 128) * ((E + 127) / 128) : ((T + 63) / 64) * ((E + 63) / 64);
   int64_t s = (256 + tiles - 1) / tiles;
   s = std::min<int64_t>(s, std::min<int64_t>(kRouterMaxSplits, std::max<int64_t>(1, H / 256)));
   return (int)std::max<int64_t>(1, s);
@@ -115,7 +118,9 @@ PMOE_API const char* pmoe_last_error_string(void) { return g_err; }
 PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E) {
   const int64_t nb = router_blocks(T);
   return align_up(nb * E * sizeof(float)) + align_up(nb * E * sizeof(int)) + align_up(nb * sizeof(float)) +
-         align_up(3 * E * H * sizeof(bf16_t)) + align_up(3 * router_logit_splits(T, H) * T * E * sizeof(float));
+         align_up(3 * E * H * sizeof(bf16_t)) +
+         align_up(std::max(router_logit_splits(T, H, E, true), router_logit_splits(T, H, E, false)) * T * E *
+                  sizeof(float));
 }
 
 PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
@@ -139,30 +144,31 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   int* blk_cnt = cv.take<int>(nb * E);
   float* blk_lse2 = cv.take<float>(nb);
   bf16_t* w3 = cv.take<bf16_t>(3 * E * H);
-  const int splits = router_logit_splits(T, H);
-  float* parts = cv.take<float>(3 * splits * T * E);
+  const bool pieces = x_dtype == PMOE_BF16 && w_dtype == PMOE_F32;
+  const int splits = router_logit_splits(T, H, E, pieces);
+  float* parts = cv.take<float>(splits * T * E);
   // Logits in fp32 arithmetic. bf16 x: x is exact in bf16, so splitting an fp32
-  // weight into three bf16 pieces makes every MFMA product exact; the three
-  // fp32 partials are summed in a fixed order by the top-k kernel.
+  // weight into three bf16 pieces makes every MFMA product exact; the GEMM's
+  // epilogue adds the three pieces' fp32 accumulators in a fixed order, and the
+  // top-k kernel sums the split-K planes in order.
   const float* lparts = logits;
-  int nparts = 1, nsplit = 1;
-  int64_t pstride = 0, ldp = E, sstride = 0;
+  int nsplit = 1;
+  int64_t sstride = 0;
   if (T > 0) {
     if (x_dtype == PMOE_BF16) {
       const bf16_t* wb = (const bf16_t*)weight;
-      nparts = 1;
+      int npieces = 1;
       if (w_dtype == PMOE_F32) {
         PMOE_TRY(split_bf16x3((const float*)weight, E * H, w3, s), "router weight split");
         wb = w3;
-        nparts = 3;
+        npieces = 3;
       }
-      PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, nparts, t, h, e, splits, parts, s),
+      // the pieces are summed in the GEMM's epilogue: one (T, E) plane per split
+      PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, npieces, t, h, e, splits, parts, s),
                "router logits GEMM");
       lparts = parts;
-      pstride = E;
-      ldp = (int64_t)nparts * E;
       nsplit = splits;
-      sstride = (int64_t)T * nparts * E;
+      sstride = (int64_t)T * E;
     } else {
       hipError_t st = w_dtype == PMOE_F32
                           ? router_logits_gemm<float, float>((const float*)x, (const float*)weight, t, h, e, logits, s)
@@ -172,12 +178,12 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
     }
     hipError_t st =
         tw_dtype == PMOE_BF16
-            ? router_topk<bf16_t>(lparts, nparts, pstride, nsplit, sstride, ldp, logits, logit_bias, t, e, k,
-                                  norm_topk_prob, (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum,
-                                  blk_lse2, blk_cnt, router_rows(T), s)
-            : router_topk<float>(lparts, nparts, pstride, nsplit, sstride, ldp, logits, logit_bias, t, e, k,
-                                 norm_topk_prob, (float*)top_weights, top_indices, top_weights_f32, blk_psum,
-                                 blk_lse2, blk_cnt, router_rows(T), s);
+            ? router_topk<bf16_t>(lparts, nsplit, sstride, E, logits, logit_bias, t, e, k, norm_topk_prob,
+                                  (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
+                                  router_rows(T), s)
+            : router_topk<float>(lparts, nsplit, sstride, E, logits, logit_bias, t, e, k, norm_topk_prob,
+                                 (float*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
+                                 router_rows(T), s);
     PMOE_TRY(st, "router top-k");
   }
   if (expert_counts || prob_sum || lse_sq_sum)

@@ -25,7 +25,7 @@ namespace pmoe {
 // split_chunk > 0 group g instead reduces k in [g * split_chunk, ...), a
 // split-K whose partial products land in separate C planes.
 enum GroupMode { GM_NONE = 0, GM_ROWS = 1, GM_RED = 2, GM_BATCH = 3 };
-enum EpiKind { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2 };
+enum EpiKind { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_SUM3 = 3 };
 
 template <typename Tc> struct Mfma;
 

@@ -86,31 +86,41 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
   return launch_gemm<CfgF32, TX, TW, float, true, true, GM_NONE, EPI_STORE>(p, s);
 }
 
-// Router GEMM tile configurations: the logits GEMM on 64x64 blocks of four
-// 32x32 wave tiles (N = 3E is small), the two backward GEMMs on 128x128 blocks.
+// Router GEMM tile configurations. The logits GEMM from the three bf16 pieces
+// of an fp32 weight: 128 x 128 output blocks whose eight 64 x 96 wave tiles
+// hold the three pieces of the same 32 columns (the x stage is loaded once for
+// all three, and the epilogue sums them). From a bf16 weight (one piece):
+// 64 x 64 blocks of four 32 x 32 wave tiles. The two backward GEMMs: 128 x 128
+// blocks.
+typedef DmaCfg<128, 384, 64, 96, 2, 64> DmaRouterLogits3;
 typedef DmaCfg<64, 64, 32, 32, 2> DmaRouterLogits;
 typedef DmaCfg<128, 128, 64, 64, 2> DmaRouterBwd;
 
-// Router logits from bf16 pieces of the router weight on the DMA engine: the
-// pieces are stacked along N (npieces*E columns), so the n-tiles of one
-// m-tile share its x rows in L2 and x is read from HBM once; fp32 out,
-// (T, npieces*E) row-major (64x128 blocks, four 32x64 wave tiles). With
-// splits > 1 the reduction over H is split into that many chunks (a multiple
-// of the k tile), each writing its own (T, npieces*E) plane at parts + s * T *
-// npieces * E: few tokens give too few tiles to fill the GPU otherwise.
+// Router logits x . W^T in fp32 from bf16 x and npieces bf16 pieces of W
+// stacked along rows (w3 = [piece 0; piece 1; piece 2], each (E, H); npieces
+// is 1 or 3). Each piece is accumulated over the block's k range on its own;
+// the epilogue adds them as (piece 0 + piece 1) + piece 2. With splits > 1 the
+// reduction over H is split into that many chunks (a multiple of the k tile),
+// each writing its own (T, E) plane at parts + s * T * E, which the caller
+// sums in order; few tokens give too few blocks to fill the GPU otherwise.
 hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
                                      int splits, float* parts, hipStream_t s) {
   GemmParams p = zero_params();
   p.A = x; p.lda = H;
   p.B = w3; p.ldb = H;
-  p.C = parts; p.ldc = npieces * E;
-  p.M = T; p.N = npieces * E; p.K = H;
+  p.C = parts; p.ldc = E;
+  p.M = T; p.N = E; p.K = H;
   p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)npieces * E * H * 2;
-  if (splits <= 1) return launch_gemm_dma<DmaRouterLogits, true, true, GM_NONE, EPI_STORE, float>(p, s);
-  constexpr int BK = DmaRouterLogits::BK;
   p.groups = splits;
-  p.split_chunk = ((H + splits - 1) / splits + BK - 1) / BK * BK;
-  p.strideC = (int64_t)T * npieces * E;
+  p.strideC = (int64_t)T * E;
+  if (npieces == 3) {
+    constexpr int BK = DmaRouterLogits3::BK;
+    p.split_chunk = splits > 1 ? ((H + splits - 1) / splits + BK - 1) / BK * BK : 0;
+    return launch_gemm_dma<DmaRouterLogits3, true, true, GM_BATCH, EPI_SUM3, float>(p, s);
+  }
+  if (npieces != 1) return hipErrorInvalidValue;
+  constexpr int BK = DmaRouterLogits::BK;
+  p.split_chunk = splits > 1 ? ((H + splits - 1) / splits + BK - 1) / BK * BK : 0;
   return launch_gemm_dma<DmaRouterLogits, true, true, GM_BATCH, EPI_STORE, float>(p, s);
 }
 

@@ -300,81 +300,56 @@ __device__ __forceinline__ void unpack8(const u32x4& w, float* v) {
 // 32-row slab at a time through its own LDS region (no block barriers): lanes
 // write their MFMA columns as fp32, then read back 8 consecutive columns of a
 // row with 16-byte LDS reads, convert with v_cvt_pk_bf16_f32 and store 16-byte
-// vectors. The fused SwiGLU forward / backward run on those 8-wide rows.
+// vectors (or 16 bytes of fp32 per half row). The router's logits GEMM sums
+// its three weight pieces here (EPI_SUM3).
 template <class Cfg, typename Tout, int GM, int EPI>
 __device__ __forceinline__ void store_tile_dma(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* smem_f,
                                                const TileInfo& ti, const GemmParams& p, int wave, int wm, int wn,
                                                int lane) {
-  constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN, LD = Cfg::EPI_LD;
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, LD = Cfg::EPI_LD;
+  // EPI_SUM3: the wave's three 32-column blocks are the three weight pieces of
+  // the same 32 output columns; they are summed (piece 0 + piece 1) + piece 2.
+  constexpr int WN = EPI == EPI_SUM3 ? 32 : Cfg::WN;
   static_assert(LD % 4 == 0, "16-byte aligned staging rows");
-  static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
+  static_assert(EPI == EPI_STORE || EPI == EPI_SUM3, "the router GEMMs store plainly or sum weight pieces");
+  static_assert(EPI != EPI_SUM3 || NI == 3, "EPI_SUM3 takes three pieces per wave");
   float* stage = smem_f + wave * 32 * LD;
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED || GM == GM_BATCH) C += (int64_t)ti.group * p.strideC;
   const int half = lane >> 5, col_l = lane & 31;
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
+    if constexpr (EPI == EPI_SUM3) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) stage[(8 * q + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * q + r];
+        for (int r = 0; r < 4; ++r)
+          stage[(8 * q + 4 * half + r) * LD + col_l] =
+              (acc[i][0][4 * q + r] + acc[i][1][4 * q + r]) + acc[i][2][4 * q + r];
+    } else {
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) stage[(8 * q + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * q + r];
+    }
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
     asm volatile("" ::: "memory");
     const int row_base = ti.m0 + wm * Cfg::WM + i * 32;
-    if constexpr (EPI == EPI_SWIGLU) {
-      constexpr int H2 = WN / 2, CPR = H2 / 8;
-      bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
-      const int col_base = ti.n0 + wn * H2;
+    constexpr int CPR = WN / 8;
+    const int col_base = ti.n0 + wn * WN;
 #pragma unroll
-      for (int e = lane; e < 32 * CPR; e += 64) {
-        const int r = e / CPR, c = (e % CPR) * 8;
-        const int row = row_base + r, col = col_base + c;
-        if (row < ti.m_end && col < p.inter) {
-          float g[8], u[8], m[8];
-          Vec8<float>::load(stage + r * LD + c, g);
-          Vec8<float>::load(stage + r * LD + H2 + c, u);
-          const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
-          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
-          *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
-          unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
-          unpack8(uw, u);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t];
-          Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
-        }
-      }
-    } else {
-      constexpr int CPR = WN / 8;
-      const int col_base = ti.n0 + wn * WN;
-#pragma unroll
-      for (int e = lane; e < 32 * CPR; e += 64) {
-        const int r = e / CPR, c = (e % CPR) * 8;
-        const int row = row_base + r, col = col_base + c;
-        if (row < ti.m_end && col < p.N) {
-          float v[8];
-          Vec8<float>::load(stage + r * LD + c, v);
-          if constexpr (EPI == EPI_SWIGLU_BWD) {
-            // v = d(mid); the aux row holds the [gate | up] pre-activations
-            const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
-            float g[8], u[8], dg[8], du[8];
-            Vec8<bf16_t>::load(GU + col, g);
-            Vec8<bf16_t>::load(GU + p.inter + col, u);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const float sg = fast_sigmoid(g[t]);
-              const float silu = g[t] * sg;
-              dg[t] = v[t] * u[t] * (sg + silu * (1.0f - sg));
-              du[t] = v[t] * silu;
-            }
-            Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
-            Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
-          } else if (col + 8 <= p.N) {
-            Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
-          } else {
-            for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
-          }
+    for (int e = lane; e < 32 * CPR; e += 64) {
+      const int r = e / CPR, c = (e % CPR) * 8;
+      const int row = row_base + r, col = col_base + c;
+      if (row < ti.m_end && col < p.N) {
+        float v[8];
+        Vec8<float>::load(stage + r * LD + c, v);
+        if (col + 8 <= p.N) {
+          Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
+        } else {
+          for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
         }
       }
     }
@@ -451,7 +426,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
-  static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && NI % 2 == 0), "SwiGLU epilogue layout");
+  static_assert(EPI != EPI_SUM3 || (B_KC && Cfg::WN == 96), "EPI_SUM3: three 32-row pieces per wave");
 
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::SMEM_BYTES];
   __shared__ int s_scan[1025];
@@ -461,7 +436,9 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
 
   // ---- tile mapping (logical tile id, n fastest)
-  const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+  // EPI_SUM3 tiles cover BN / 3 output columns (three weight pieces each)
+  constexpr int TN = EPI == EPI_SUM3 ? BN / 3 : BN;
+  const int ntiles_n = (p.N + TN - 1) / TN;
   TileInfo ti;
   const bf16_t* A = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B = reinterpret_cast<const bf16_t*>(p.B);
@@ -511,7 +488,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
     ti.group = 0; ti.m0 = slot * BM; ti.m_end = p.M; ti.k_lo = 0; ti.k_hi = p.K;
     if (ti.m0 >= p.M) return;
   }
-  ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+  ti.n0 = tn * TN;
 
   // ---- operand DMA descriptors. k-contiguous A is based at the tile's first
   // row and bounded by the group's last row; the [k][r] operands of GM_RED are
@@ -546,13 +523,14 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   };
   auto init_b = [&](LdB& lb, int vw) {
     if constexpr (B_KC) {
-      const int n0 = ti.n0, N = p.N, I = p.inter;
-      if constexpr (EPI == EPI_SWIGLU) {
+      const int n0 = ti.n0, N = p.N;
+      if constexpr (EPI == EPI_SUM3) {
+        // B = [piece 0; piece 1; piece 2], each N rows; tile row c feeds wave
+        // c / 96, piece (c % 96) / 32, output column n0 + 32 * wave + c % 32
         lb.init([&](int c) {
-          const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
-          const int gcol = n0 + w * h + (cc % h);
-          if (gcol >= I) return -1;
-          return cc < h ? gcol : I + gcol;
+          const int w = c / Cfg::WN, cc = c % Cfg::WN;
+          const int col = n0 + 32 * w + (cc & 31);
+          return col < N ? (cc >> 5) * N + col : -1;
         }, p.ldb, vw, lane);
       } else {
         lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, vw, lane);
@@ -687,7 +665,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
 
 template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t>
 hipError_t launch_gemm_dma(const GemmParams& p, hipStream_t s) {
-  const int ntn = (EPI == EPI_SWIGLU) ? (p.inter + Cfg::BN / 2 - 1) / (Cfg::BN / 2) : (p.N + Cfg::BN - 1) / Cfg::BN;
+  constexpr int TN = EPI == EPI_SUM3 ? Cfg::BN / 3 : Cfg::BN;
+  const int ntn = (p.N + TN - 1) / TN;
   int64_t slots;
   if (GM == GM_ROWS) slots = (p.M + Cfg::BM - 1) / Cfg::BM + p.groups;
   else if (GM == GM_RED || GM == GM_BATCH) slots = (int64_t)p.groups * ((p.M + Cfg::BM - 1) / Cfg::BM);

@@ -33,15 +33,15 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
                           float* partial, hipStream_t s);
 
 // ---- routing, permutation and row movement (route.hip).
-// logits = sum of nparts fp32 partial products, each the fixed-order sum of
-// nsplit split-K planes (plane s of partial q of (t, e) at
-// parts[s*split_stride + t*ldp + q*part_stride + e]), then softmax / top-k /
-// renormalisation and the per-block statistics.
+// logits = the fixed-order sum of nsplit split-K planes (plane s of (t, e) at
+// parts[s*split_stride + t*ldp + e]) plus the optional bias, then softmax /
+// top-k / renormalisation and the per-block statistics; one wave per row,
+// rows_per_block (<= 16) rows per block.
 template <typename TW>
-hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int nsplit, int64_t split_stride,
-                       int64_t ldp, float* logits, const float* logit_bias,
-                       int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
-                       float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s);
+hipError_t router_topk(const float* parts, int nsplit, int64_t split_stride, int64_t ldp, float* logits,
+                       const float* logit_bias, int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx,
+                       float* top_w_f32, float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block,
+                       hipStream_t s);
 hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s);
 // parts (T, npieces*E) fp32 = x . [w3[0]; w3[1]; ...]^T: one GEMM over the stacked pieces, so x is
 // read once; x (T,H) bf16, w3 (npieces,E,H) bf16. splits > 1: split-K over H

@@ -73,81 +73,28 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16
   }
 }
 
-// Logits of row `row`: the fixed-order sum of the partial products
-// ((p0 + p1) + p2), plus the optional bias. Partial q of (row, e) is itself
-// the in-order sum of nsplit split-K planes, plane s at parts[s * split_stride
-// + row * ldp + q * part_stride + e]. parts may alias logits (nparts 1,
-// nsplit 1). fetch_parts issues the loads of a row (up to kMaxParts
-// partials), so the top-k kernel can fetch row r + 4 while it ranks row r;
-// finish_logits sums the partials in that fixed order and writes the logits.
-constexpr int kMaxParts = 3;
+// Router top-k, one wave per row (the block's waves take consecutive rows).
+// The logits of (row, e) are the in-order sum of nsplit split-K planes, plane
+// sp at parts[sp * split_stride + row * ldp + e], plus the optional bias;
+// parts may alias logits (nsplit 1, no bias: nothing is written back). Every
+// plane's loads of a row are issued before the first is used (addresses are
+// clamped into the row, so no lane branches), so a row costs one memory
+// latency whatever nsplit is.
 constexpr int kMaxSplits = kRouterMaxSplits;
-template <int EPL>
-struct RowParts {
-  float p[kMaxParts][EPL];
-};
-template <int EPL>
-__device__ __forceinline__ void fetch_parts(const float* parts, int nparts, int64_t part_stride, int nsplit,
-                                            int64_t split_stride, int64_t ldp, int row, int E, int lane,
-                                            RowParts<EPL>& rp) {
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    const int64_t op = (int64_t)row * ldp + e;
-#pragma unroll
-    for (int q = 0; q < kMaxParts; ++q) {
-      float v = 0.0f;
-      if (e < E && q < nparts && nsplit == 1) {
-        v = parts[q * part_stride + op];
-      } else if (e < E && q < nparts) {
-        // every plane's load is issued before the first add (nsplit is
-        // uniform, so the loads past it are skipped by scalar branches), so a
-        // row costs one memory latency whatever nsplit is
-        float pl[kMaxSplits];
-#pragma unroll
-        for (int sp = 0; sp < kMaxSplits; ++sp)
-          pl[sp] = sp < nsplit ? parts[sp * split_stride + q * part_stride + op] : 0.0f;
-        v = pl[0];
-#pragma unroll
-        for (int sp = 1; sp < kMaxSplits; ++sp)
-          if (sp < nsplit) v += pl[sp];
-      }
-      rp.p[q][j] = v;
-    }
-  }
-}
-template <int EPL>
-__device__ __forceinline__ void finish_logits(const RowParts<EPL>& rp, int nparts, bool write, float* logits,
-                                              const float* bias, int row, int E, int lane, float (&v)[EPL]) {
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    float x = -INFINITY;
-    if (e < E) {
-      x = rp.p[0][j];
-#pragma unroll
-      for (int q = 1; q < kMaxParts; ++q)
-        if (q < nparts) x += rp.p[q][j];
-      if (bias != nullptr) x += bias[e];
-      if (write) logits[(int64_t)row * E + e] = x;
-    }
-    v[j] = x;
-  }
-}
 template <int EPL, typename TW>
-__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ parts, int nparts,
-                                                          int64_t part_stride, int nsplit, int64_t split_stride,
-                                                          int64_t ldp, float* logits,
-                                                          const float* __restrict__ bias,
-                                                          int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
-                                                          int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
-                                                          float* __restrict__ blk_psum, float* __restrict__ blk_lse2,
-                                                          int* __restrict__ blk_counts, int rows_per_block) {
-  extern __shared__ float sh[];  // [4][E] psum partials, then [E] int counts, then [4] lse2
+__global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restrict__ parts, int nsplit,
+                                                           int64_t split_stride, int64_t ldp, float* logits,
+                                                           const float* __restrict__ bias,
+                                                           int T, int E, int K, int norm_topk, TW* __restrict__ top_w,
+                                                           int64_t* __restrict__ top_idx, float* __restrict__ top_w_f32,
+                                                           float* __restrict__ blk_psum, float* __restrict__ blk_lse2,
+                                                           int* __restrict__ blk_counts) {
+  extern __shared__ float sh[];  // [NW][E] psum partials, then [E] int counts, then [NW] lse2
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = blockDim.x >> 6;
   float* s_psum = sh;
-  int* s_cnt = reinterpret_cast<int*>(sh + 4 * E);
-  float* s_lse2 = sh + 5 * E;
+  int* s_cnt = reinterpret_cast<int*>(sh + nw * E);
+  float* s_lse2 = sh + (nw + 1) * E;
   for (int e = tid; e < E; e += blockDim.x) s_cnt[e] = 0;
   __syncthreads();
 
@@ -155,20 +102,36 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 #pragma unroll
   for (int j = 0; j < EPL; ++j) psum[j] = 0.0f;
   float lse2 = 0.0f;
-
-  const int row0 = blockIdx.x * rows_per_block;
-  const int row1 = min(T, row0 + rows_per_block);
-  const bool write_logits = nparts > 1 || nsplit > 1 || bias != nullptr || parts != logits;
-  RowParts<EPL> cur;
-  if (row0 + wave < row1)
-    fetch_parts<EPL>(parts, nparts, part_stride, nsplit, split_stride, ldp, row0 + wave, E, lane, cur);
-  for (int row = row0 + wave; row < row1; row += 4) {
-    RowParts<EPL> nxt;
-    if (row + 4 < row1)
-      fetch_parts<EPL>(parts, nparts, part_stride, nsplit, split_stride, ldp, row + 4, E, lane, nxt);
+  const int row = blockIdx.x * nw + wave;
+  if (row < T) {
+    // ---- logits of the row (the loads of up to 4 lane slots in one batch)
+    constexpr int JB = EPL < 4 ? EPL : 4;
+    const bool write_logits = nsplit > 1 || bias != nullptr || parts != logits;
     float v[EPL];
-    finish_logits<EPL>(cur, nparts, write_logits, logits, bias, row, E, lane, v);
-    cur = nxt;
+#pragma unroll
+    for (int j0 = 0; j0 < EPL; j0 += JB) {
+      float pl[kMaxSplits][JB];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) {
+        if (sp < nsplit) {  // uniform
+#pragma unroll
+          for (int jj = 0; jj < JB; ++jj)
+            pl[sp][jj] = parts[sp * split_stride + (int64_t)row * ldp + min(lane + 64 * (j0 + jj), E - 1)];
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const int e = lane + 64 * (j0 + jj);
+        float x = pl[0][jj];
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplits; ++sp)
+          if (sp < nsplit) x += pl[sp][jj];
+        if (bias != nullptr) x += bias[min(e, E - 1)];
+        if (e < E && write_logits) logits[(int64_t)row * E + e] = x;
+        v[j0 + jj] = e < E ? x : -INFINITY;
+      }
+    }
+    // ---- softmax statistics
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
@@ -183,18 +146,19 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     s = wave_sum(s);
     const float inv_s = 1.0f / s;
     const float lse = m + logf(s);
-    lse2 += lse * lse;  // every lane holds the same value; lane 0's copy is used
+    lse2 = lse * lse;  // every lane holds the same value; lane 0's copy is used
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) psum[j] += ex[j] * inv_s;
+    for (int j = 0; j < EPL; ++j) psum[j] = ex[j] * inv_s;
 
-    // top-k by (logit desc, id asc); NaN ranks as -inf so a valid id is always
-    // found. Each pick: the wave max of the unpicked keys, then the lowest id
-    // holding it (ballot over each lane slot in id order).
+    // ---- top-k by (logit desc, id asc); NaN ranks as -inf so a valid id is
+    // always found. Each pick: the wave max of the unpicked keys, then the
+    // lowest id holding it (ballot over each lane slot in id order). Lane k
+    // keeps pick k's logit; the probabilities follow the loop.
     int key[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; ++j) key[j] = rank_key(nan_to_neg_inf(v[j]));
     unsigned selmask = 0;
-    float p_sel = 0.0f, psum_sel = 0.0f;
+    float v_sel = -INFINITY;
     int e_sel = 0;
     for (int k = 0; k < K; ++k) {
       int lm = INT_MIN;
@@ -208,12 +172,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
         const unsigned long long hit = __ballot(lane + 64 * j < E && !((selmask >> j) & 1u) && key[j] == km);
         if (be < 0 && hit != 0ull) be = 64 * j + __builtin_ctzll(hit);
       }
-      const float bv = key_value(km);
       if ((be & 63) == lane) selmask |= 1u << (be >> 6);
-      const float pk = expf(bv - m) * inv_s;
-      psum_sel += pk;
-      if (lane == k) { p_sel = pk; e_sel = be; }
+      if (lane == k) { v_sel = key_value(km); e_sel = be; }
     }
+    // p of each pick on its own lane; their sum in pick order
+    const float p_sel = lane < K ? expf(v_sel - m) * inv_s : 0.0f;
+    float psum_sel = 0.0f;
+    for (int k = 0; k < K; ++k)
+      psum_sel += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p_sel), k));
     if (lane < K) {
       const float w = norm_topk ? p_sel / psum_sel : p_sel;
       const int64_t o = (int64_t)row * K + lane;
@@ -232,10 +198,16 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   if (lane == 0) s_lse2[wave] = lse2;
   __syncthreads();
   for (int e = tid; e < E; e += blockDim.x) {
-    blk_psum[(int64_t)blockIdx.x * E + e] = ((s_psum[e] + s_psum[E + e]) + s_psum[2 * E + e]) + s_psum[3 * E + e];
+    float t = s_psum[e];
+    for (int w = 1; w < nw; ++w) t += s_psum[w * E + e];
+    blk_psum[(int64_t)blockIdx.x * E + e] = t;
     blk_counts[(int64_t)blockIdx.x * E + e] = s_cnt[e];
   }
-  if (tid == 0) blk_lse2[blockIdx.x] = ((s_lse2[0] + s_lse2[1]) + s_lse2[2]) + s_lse2[3];
+  if (tid == 0) {
+    float t = s_lse2[0];
+    for (int w = 1; w < nw; ++w) t += s_lse2[w];
+    blk_lse2[blockIdx.x] = t;
+  }
 }
 
 // One wave per expert (and one more for the lse^2 total): lane l sums the
@@ -783,18 +755,21 @@ hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s) {
 }
 
 template <typename TW>
-hipError_t router_topk(const float* parts, int nparts, int64_t part_stride, int nsplit, int64_t split_stride,
-                       int64_t ldp, float* logits, const float* logit_bias,
-                       int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx, float* top_w_f32,
-                       float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block, hipStream_t s) {
+hipError_t router_topk(const float* parts, int nsplit, int64_t split_stride, int64_t ldp, float* logits,
+                       const float* logit_bias, int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx,
+                       float* top_w_f32, float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block,
+                       hipStream_t s) {
   if (T == 0) return hipSuccess;
-  if (nparts < 1 || nparts > kMaxParts || nsplit < 1 || nsplit > kMaxSplits) return hipErrorInvalidValue;
+  if (nsplit < 1 || nsplit > kMaxSplits) return hipErrorInvalidValue;
+  // one wave per row of the block
+  if (rows_per_block < 1 || rows_per_block > 16) return hipErrorInvalidValue;
   const unsigned grid = blocks_for(T, rows_per_block);
-  const size_t shmem = (size_t)(5 * E + 4) * sizeof(float);
+  const unsigned threads = 64u * (unsigned)rows_per_block;
+  const size_t shmem = (size_t)((rows_per_block + 1) * E + rows_per_block) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \
-  hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(256), shmem, s, parts, nparts, part_stride,   \
-                     nsplit, split_stride, ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, \
-                     blk_psum, blk_lse2, blk_counts, rows_per_block)
+  hipLaunchKernelGGL((router_topk_kernel<EPL, TW>), dim3(grid), dim3(threads), shmem, s, parts, nsplit,            \
+                     split_stride, ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, \
+                     blk_lse2, blk_counts)
   if (E <= 64) PMOE_TOPK_CASE(1);
   else if (E <= 128) PMOE_TOPK_CASE(2);
   else if (E <= 256) PMOE_TOPK_CASE(4);
@@ -1043,11 +1018,10 @@ hipError_t dispatch_rows_bwd(const T* dx_perm, const int32_t* inv_pos, const T* 
   });
 }
 
-template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int, int64_t, int64_t, float*, const float*, int,
-                                        int, int, int, bf16_t*, int64_t*, float*, float*, float*, int*, int,
-                                        hipStream_t);
-template hipError_t router_topk<float>(const float*, int, int64_t, int, int64_t, int64_t, float*, const float*, int,
-                                       int, int, int, float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
+                                        bf16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<float>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
+                                       float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
                                            int, int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
