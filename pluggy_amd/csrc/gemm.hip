@@ -91,10 +91,12 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
 // hold the three pieces of the same 32 columns (the x stage is loaded once for
 // all three, and the epilogue sums them). From a bf16 weight (one piece):
 // 64 x 64 blocks of four 32 x 32 wave tiles. The two backward GEMMs: 128 x 128
-// blocks.
+// blocks, the weight gradient's (a long reduction over tokens) with a 4-deep
+// ring.
 typedef DmaCfg<128, 384, 64, 96, 2, 64> DmaRouterLogits3;
 typedef DmaCfg<64, 64, 32, 32, 2> DmaRouterLogits;
 typedef DmaCfg<128, 128, 64, 64, 2> DmaRouterBwd;
+typedef DmaCfg<128, 128, 64, 64, 4> DmaRouterDw;
 
 // Router logits x . W^T in fp32 from bf16 x and npieces bf16 pieces of W
 // stacked along rows (w3 = [piece 0; piece 1; piece 2], each (E, H); npieces
@@ -148,7 +150,7 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
   p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
   p.M = E; p.N = H; p.K = T;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
-  return launch_gemm_dma<DmaRouterBwd, false, false, GM_RED, EPI_STORE, float>(p, s);
+  return launch_gemm_dma<DmaRouterDw, false, false, GM_RED, EPI_STORE, float>(p, s);
 }
 
 template <typename TX, typename TW>

@@ -254,22 +254,28 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
-  const int64_t* irow = top_idx + (int64_t)row * K;
-  const float* wrow = top_w_f32 + (int64_t)row * K;
+  // lane k < K holds slot k's expert, weight and upstream gradient (one load
+  // each, all lanes at once); the slot loops below read them with readlane
+  const bool slot = lane < K;
+  const int64_t so = (int64_t)row * K + lane;
+  const int e_l = slot ? (int)top_idx[so] : 0;
+  const float w_l = slot ? top_w_f32[so] : 0.0f;
+  const float g_l = (slot && grad_w != nullptr) ? load_scalar<TG>(grad_w + so) : 0.0f;
+  auto rd = [](float v, int k) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k)); };
   // inner = sum_k w_k G_k, in slot order
   float inner = 0.0f;
   if (grad_w != nullptr)
-    for (int k = 0; k < K; ++k) inner += wrow[k] * load_scalar<TG>(grad_w + (int64_t)row * K + k);
+    for (int k = 0; k < K; ++k) inner += rd(w_l, k) * rd(g_l, k);
   float d[EPL];
   if (norm_topk) {
 #pragma unroll
     for (int j = 0; j < EPL; ++j) d[j] = 0.0f;
     if (grad_w != nullptr) {
+      const float val_l = w_l * (g_l - inner);
       for (int k = 0; k < K; ++k) {
-        const int e = (int)irow[k];
+        const int e = __builtin_amdgcn_readlane(e_l, k);
+        const float val = rd(val_l, k);
         if ((e & 63) == lane) {
-          const float g = load_scalar<TG>(grad_w + (int64_t)row * K + k);
-          const float val = wrow[k] * (g - inner);
 #pragma unroll
           for (int j = 0; j < EPL; ++j)
             if ((e >> 6) == j) d[j] = val;
@@ -299,9 +305,9 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
     for (int j = 0; j < EPL; ++j) d[j] = -v[j] * inv_s * inner;
     if (grad_w != nullptr) {
       for (int k = 0; k < K; ++k) {
-        const int e = (int)irow[k];
+        const int e = __builtin_amdgcn_readlane(e_l, k);
+        const float g = rd(g_l, k);
         if ((e & 63) == lane) {
-          const float g = load_scalar<TG>(grad_w + (int64_t)row * K + k);
 #pragma unroll
           for (int j = 0; j < EPL; ++j)
             if ((e >> 6) == j) d[j] += v[j] * inv_s * g;
