@@ -135,13 +135,13 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
 // k-stages plus an epilogue worth about kRedEpiStages stages (measured: a
 // 256x256 bf16 tile drains in ~3 stage times). s_cost[g] = cost of one tile of
 // each group before g (inclusive scan to groups + 1 entries, computed by wave
-// 0); every thread gets s_cost[groups].
+// 0), *s_cmax = the largest cost of one tile; every thread gets s_cost[groups].
 constexpr int kRedEpiStages = 3;
 template <int BK, int NS>
-__device__ __forceinline__ int red_cost_scan(const int32_t* offs, int groups, int* s_cost) {
+__device__ __forceinline__ int red_cost_scan(const int32_t* offs, int groups, int* s_cost, int* s_cmax) {
   const int tid = threadIdx.x, lane = tid & 63;
   if (tid < 64) {
-    int carry = 0;
+    int carry = 0, cmax = 0;
     for (int base = 0; base < groups; base += 64) {
       const int g = base + lane;
       int c = 0;
@@ -149,11 +149,17 @@ __device__ __forceinline__ int red_cost_scan(const int32_t* offs, int groups, in
         const int rows = offs[g] - (g == 0 ? 0 : offs[g - 1]);
         c = max((rows + BK - 1) / BK, NS - 1) + kRedEpiStages;
       }
+      cmax = max(cmax, c);
       const int inc = wave_incl_scan(c, lane) + carry;
       if (g < groups) s_cost[g + 1] = inc;
       carry = __shfl(inc, 63, kWave);
     }
-    if (lane == 0) s_cost[0] = 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) cmax = max(cmax, __shfl_xor(cmax, o, kWave));
+    if (lane == 0) {
+      s_cost[0] = 0;
+      *s_cmax = cmax;
+    }
   }
   __syncthreads();
   return s_cost[groups];
@@ -220,6 +226,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   __shared__ __attribute__((aligned(16))) float s_epi[L::EPI_FLOATS];
   __shared__ int s_scan[1025];
   __shared__ int s_offs[1024];
+  __shared__ int s_order[1024];  // GM_RED under skew: groups by tile cost, descending
+  __shared__ int s_cmax;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -238,25 +246,58 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // and its blocks walk it in a stride of their count. GM_ROWS tiles all run
   // the full reduction, so the shares hold equal tile counts; a GM_RED tile
   // runs its group's reduction range, so there the shares hold equal cost.
+  // Under skewed routing (GM_RED, one tile costing more than half a block's
+  // mean share) the shares cannot balance: a heavy group's tiles crowd one
+  // XCD's blocks. Then the tiles are taken in order of descending cost and
+  // dealt to the blocks in a snake (round k gives tile k*NB + p to the block
+  // at position p, or k*NB + NB-1-p for odd k), positions XCD-major so that a
+  // group's tiles still run side by side on one XCD.
   const int xcd = blockIdx.x & 7;
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
-  int cnt, start;
+  const int bi = blockIdx.x >> 3;                  // this block's position on its XCD
+  int cnt = 0, start = 0, tpg = 1, spos = 0;
+  bool skew = false;
   if (total == 0) {
     return;
   } else if constexpr (GM == GM_RED) {
-    const int tpg = mt_red * ntiles_n;  // tiles per group
-    const int64_t c_all = red_cost_scan<BK, NS>(s_offs, groups, s_scan) * (int64_t)tpg;
-    const int b0 = red_cost_tile(s_scan, groups, tpg, c_all * xcd / 8);
-    const int b1 = xcd == 7 ? total : red_cost_tile(s_scan, groups, tpg, c_all * (xcd + 1) / 8);
-    start = b0;
-    cnt = b1 - b0;
+    tpg = mt_red * ntiles_n;  // tiles per group
+    const int64_t c_all = red_cost_scan<BK, NS>(s_offs, groups, s_scan, &s_cmax) * (int64_t)tpg;
+    skew = (int64_t)s_cmax * 2 * gridDim.x > c_all;
+    if (skew) {
+      for (int g = tid; g < groups; g += Cfg::NT) {
+        const int c = s_scan[g + 1] - s_scan[g];
+        int r = 0;
+        for (int h = 0; h < groups; ++h) {
+          const int ch = s_scan[h + 1] - s_scan[h];
+          r += (ch > c || (ch == c && h < g)) ? 1 : 0;
+        }
+        s_order[r] = g;
+      }
+      __syncthreads();
+      for (int x = 0; x < xcd; ++x) spos += ((int)gridDim.x - x + 7) >> 3;
+      spos += bi;
+    } else {
+      const int b0 = red_cost_tile(s_scan, groups, tpg, c_all * xcd / 8);
+      const int b1 = xcd == 7 ? total : red_cost_tile(s_scan, groups, tpg, c_all * (xcd + 1) / 8);
+      start = b0;
+      cnt = b1 - b0;
+    }
   } else {
     const int per = total >> 3, rem = total & 7;
     cnt = per + (xcd < rem ? 1 : 0);
     start = xcd * per + (xcd < rem ? xcd : rem);
   }
-  int bi = blockIdx.x >> 3;  // this block's position in the XCD share
-  if (bi >= cnt) return;
+  // The k-th tile of this block (k = 0, 1, ...) as a list index, or -1 past its last.
+  auto tile_at = [&](int k) -> int {
+    if (skew) {
+      const int NB = (int)gridDim.x;
+      const int j = k * NB + ((k & 1) ? NB - 1 - spos : spos);
+      return j < total ? s_order[j / tpg] * tpg + j % tpg : -1;
+    }
+    const int b = bi + k * nb;
+    return b < cnt ? start + b : -1;
+  };
+  if (tile_at(0) < 0) return;
 
   const uint32_t lds0 = lds_addr(smem);
   float* stage = s_epi + wave * L::SLAB * L::EPI_LD;
@@ -293,9 +334,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     int nk, kd0, kd_hi;
     int klo;  // first reduction index of the tile (wave-uniform; k-row gathers)
   };
-  // Tile ordinal b of this block's share (b >= cnt: past the last tile; its
-  // descriptors are empty, so every DMA reads zeros).
-  auto setup = [&](int b, LoadTile& T) {
+  // Tile t of the list (t < 0: past the block's last tile; its descriptors
+  // are empty, so every DMA reads zeros).
+  auto setup = [&](int t, LoadTile& T) {
     T.ti.group = 0; T.ti.m0 = 0; T.ti.m_end = 0; T.ti.n0 = 0; T.ti.k_lo = 0; T.ti.k_hi = 0;
     T.nk = NS - 1;
     T.kd0 = 0;
@@ -304,8 +345,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     const bf16_t* a_base = A0;
     const bf16_t* b_base = B0;
     uint64_t a_bytes = 0, b_bytes = 0;
-    if (b < cnt) {
-      const int t = start + b;
+    if (t >= 0) {
       int tn = t % ntiles_n, slot = t / ntiles_n;
       if constexpr (GM == GM_ROWS) {
         // An expert's tiles are ordered n-tile major, its m-tiles inner, so
@@ -459,8 +499,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   };
 
   LoadTile cur, nxt;
-  setup(bi, cur);
-  setup(bi + nb, nxt);
+  int kt_tile = 0;  // this block's tile counter
+  setup(tile_at(0), cur);
+  setup(tile_at(1), nxt);
   int tok[GI][2], tok_next[GI][2];
   // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
   for (int s0 = 0; s0 < NS - 1; ++s0) {
@@ -536,10 +577,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     wait_vmcnt<0>();
     store_slabs<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
     gs += nk;
-    bi += nb;
-    if (bi >= cnt) break;
+    ++kt_tile;
+    if (tile_at(kt_tile) < 0) break;
     cur = nxt;
-    setup(bi + nb, nxt);
+    setup(tile_at(kt_tile + 1), nxt);
   }
   wait_vmcnt<0>();  // the zero-reading DMAs past the last tile
 }
