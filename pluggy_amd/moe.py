@@ -27,6 +27,7 @@ from collections import defaultdict
 from dataclasses import dataclass
 
 import torch
+import torch.nn.functional as F
 
 from . import ops
 from ._lib import require_gpu
@@ -94,26 +95,68 @@ def _stage(name: str):
 
 
 def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
-    """The operand dtype CUDA autocast asks for (bf16), or None when it is off.
+    """The operand dtype for the kernels under CUDA autocast, or None when it is off.
 
     The reference trainer runs the model under ``torch.autocast(cuda, bf16)``
     with fp32 parameters (pluggy/training/trainer.py:469). There the router's
     linear runs in bf16 (qwen3_moe.py:172), and the expert weights are cast to
     the activation dtype with the stated intent "bf16 under autocast"
     (moe.py:110-112). The drop-in therefore hands the kernels bf16 operands
-    whenever autocast is on, whatever the residual stream's dtype, and returns
-    its outputs in the input's dtype as the reference does. (torch's
+    whenever bf16 autocast is on, whatever the residual stream's dtype, and
+    returns its outputs in the input's dtype as the reference does. (torch's
     ``F.grouped_mm`` is not on autocast's bf16 list, so with an fp32 residual
     stream the reference's expert GEMMs actually run in fp32; this build keeps
-    the stated bf16 intent.) The kernels compute in bf16 or fp32 only, so an
-    fp16 autocast region is rejected.
+    the stated bf16 intent.) The kernels compute in bf16 or fp32 only: under
+    fp16 autocast they take fp32 operands (at least fp16's precision), and the
+    outputs keep the input's dtype.
     """
     if t.is_cuda and torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
-        if dt != torch.bfloat16:
-            raise NotImplementedError(f"pluggy_amd computes in bf16 or fp32; autocast asks for {dt}")
-        return dt
+        return torch.bfloat16 if dt == torch.bfloat16 else torch.float32
     return None
+
+
+def _compute_dtype(t: torch.Tensor) -> torch.dtype:
+    """The dtype the kernels compute in for activations ``t``: autocast's (see
+    ``_amp_dtype``), else ``t``'s own when it is bf16 or fp32, else fp32 (an
+    fp16 tensor is computed in fp32 and the result cast back)."""
+    amp = _amp_dtype(t)
+    if amp is not None:
+        return amp
+    return t.dtype if t.dtype in (torch.bfloat16, torch.float32) else torch.float32
+
+
+def _router_operand(w: torch.Tensor, amp: torch.dtype | None) -> torch.Tensor:
+    """The router weight as the kernels take it: bf16 under bf16 autocast (as
+    the reference's ``F.linear`` there), else fp32 or bf16 as given (fp32 for
+    any other dtype)."""
+    if amp == torch.bfloat16:
+        w = w.to(torch.bfloat16)
+    elif w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.float()
+    return w.contiguous()
+
+
+# Hidden and intermediate sizes reach the kernels as multiples of 8 (16-byte
+# rows). Other sizes are zero-padded on the way in and sliced on the way out:
+# the zero columns add nothing to any product, the SwiGLU of a zero gate and
+# up column is zero, and autograd carries the gradients back through the pad.
+def _pad8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def _pad_last(t: torch.Tensor, n: int) -> torch.Tensor:
+    return t if t.shape[-1] == n else F.pad(t, (0, n - t.shape[-1]))
+
+
+def _pad_experts(gate_up_proj: torch.Tensor, down_proj: torch.Tensor, Hp: int, Ip: int):
+    """(E, 2I, H), (E, H, I) -> (E, 2Ip, Hp), (E, Hp, Ip), gate rows [0, I) then up rows at [Ip, Ip + I)."""
+    E, I2, H = gate_up_proj.shape
+    I = I2 // 2
+    gate, up = gate_up_proj[:, :I], gate_up_proj[:, I:]
+    gate = F.pad(gate, (0, Hp - H, 0, Ip - I))
+    up = F.pad(up, (0, Hp - H, 0, Ip - I))
+    return torch.cat([gate, up], dim=1), F.pad(down_proj, (0, Ip - I, 0, Hp - H))
 
 
 def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, torch.Tensor | None]:
@@ -231,10 +274,9 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     assert 1 <= top_k <= weight.shape[0]
     require_gpu(hidden, weight, logit_bias)
     amp = _amp_dtype(hidden)
-    x = (hidden if amp is None else hidden.to(amp)).contiguous()
-    w = (weight if amp is None else weight.to(amp)).contiguous()
-    if w.dtype not in (torch.float32, torch.bfloat16):
-        w = w.float()
+    H = hidden.shape[1]
+    x = _pad_last(hidden.to(_compute_dtype(hidden)), _pad8(H)).contiguous()
+    w = _pad_last(_router_operand(weight, amp), _pad8(H)).contiguous()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     logits, top_w, top_i, _w32, counts, psum, lse2 = torch.ops.pmoe.router_fwd(
@@ -541,18 +583,23 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     assert 1 <= top_k <= router_weight.shape[0]
     require_gpu(hidden, router_weight, gate_up_proj, down_proj, logit_bias)
     amp = _amp_dtype(hidden)
-    dt = hidden.dtype if amp is None else amp
-    x = hidden.to(dt).contiguous()
-    rw = (router_weight if amp is None else router_weight.to(amp)).contiguous()
-    if rw.dtype not in (torch.float32, torch.bfloat16):
-        rw = rw.float()
-    gu, gu_master = _compute_weight(gate_up_proj, dt)
-    dn, dn_master = _compute_weight(down_proj, dt)
+    dt = _compute_dtype(hidden)
+    T, H = hidden.shape
+    I = gate_up_proj.shape[1] // 2
+    Hp, Ip = _pad8(H), _pad8(I)
+    x = _pad_last(hidden.to(dt), Hp).contiguous()
+    rw = _pad_last(_router_operand(router_weight, amp), Hp).contiguous()
+    if (Hp, Ip) != (H, I):
+        gu, dn = _pad_experts(gate_up_proj.to(dt), down_proj.to(dt), Hp, Ip)
+        gu, gu_master, dn, dn_master = gu.contiguous(), None, dn.contiguous(), None
+    else:
+        gu, gu_master = _compute_weight(gate_up_proj, dt)
+        dn, dn_master = _compute_weight(down_proj, dt)
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
                                                                      logit_bias, gu_master, dn_master)[:5]
-    return out.to(hidden.dtype), logits, RouterStats(counts, psum, lse2, x.shape[0])
+    return out[:, :H].to(hidden.dtype), logits, RouterStats(counts, psum, lse2, T)
 
 
 def moe_expert_ffn(
@@ -578,14 +625,21 @@ def moe_expert_ffn(
     assert gate_up_proj.dim() == 3 and down_proj.dim() == 3
     del use_grouped_mm  # one code path: the HIP grouped kernels
     require_gpu(hidden, top_indices, top_weights, gate_up_proj, down_proj)
-    amp = _amp_dtype(hidden)
-    dt = hidden.dtype if amp is None else amp
-    gu, gu_master = _compute_weight(gate_up_proj, dt)
-    dn, dn_master = _compute_weight(down_proj, dt)
+    dt = _compute_dtype(hidden)
+    H = hidden.shape[1]
+    I = gate_up_proj.shape[1] // 2
+    Hp, Ip = _pad8(H), _pad8(I)
+    if (Hp, Ip) != (H, I):
+        gu, dn = _pad_experts(gate_up_proj.to(dt), down_proj.to(dt), Hp, Ip)
+        gu, gu_master, dn, dn_master = gu.contiguous(), None, dn.contiguous(), None
+    else:
+        gu, gu_master = _compute_weight(gate_up_proj, dt)
+        dn, dn_master = _compute_weight(down_proj, dt)
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
-    out = torch.ops.pmoe.expert_ffn_fwd(hidden.to(dt).contiguous(), top_indices.to(torch.int64).contiguous(),
-                                        tw.contiguous(), gu, dn, gu_master, dn_master)[0]
-    return out.to(hidden.dtype)
+    out = torch.ops.pmoe.expert_ffn_fwd(_pad_last(hidden.to(dt), Hp).contiguous(),
+                                        top_indices.to(torch.int64).contiguous(), tw.contiguous(), gu, dn,
+                                        gu_master, dn_master)[0]
+    return out[:, :H].to(hidden.dtype)
 
 
 # ------------------------------- MoE half of the block: RMSNorm -> MLP -> add
@@ -757,17 +811,18 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     B, S, H = x.shape
     require_gpu(x)
     assert isinstance(norm, torch.nn.RMSNorm) and tuple(norm.normalized_shape) == (H,) and norm.weight is not None
-    if H > 4096:  # the fused backward keeps a row in registers; wider rows take the unfused path
+    I = mlp.experts.gate_up_proj.shape[1] // 2
+    if H > 4096 or H % 8 or I % 8 or x.dtype not in (torch.float32, torch.bfloat16):
+        # the fused backward keeps a row in registers, and its row kernels take
+        # 16-byte rows of an fp32 or bf16 stream; other shapes take the unfused path
         return x + mlp(norm(x))
     r = mlp.router
     flat = x.reshape(B * S, H).contiguous()
     amp = _amp_dtype(flat)
-    cdt = flat.dtype if amp is None else amp
+    cdt = _compute_dtype(flat)
     eps = norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
     nw = norm.weight if norm.weight.dtype == torch.float32 else norm.weight.float()
-    rw = r.weight if amp is None else r.weight.to(amp)
-    if rw.dtype not in (torch.float32, torch.bfloat16):
-        rw = rw.float()
+    rw = _router_operand(r.weight, amp)
     gu, gu_master = _compute_weight(mlp.experts.gate_up_proj, cdt)
     dn, dn_master = _compute_weight(mlp.experts.down_proj, cdt)
     bias = r.logit_bias.float().contiguous() if r.logit_bias is not None else None

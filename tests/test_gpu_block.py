@@ -121,6 +121,57 @@ def test_sparse_mlp_module(dtype, norm):
     _check_routing_vs_cpu(x.reshape(B * S, H), Wr, logits.detach().cpu(), K)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sparse_mlp_module_any_size(dtype):
+    """Hidden and intermediate sizes that are not multiples of 8 (the reference
+    takes any): the host layer zero-pads them to the kernels' 16-byte rows and
+    slices the result; values and every gradient vs fp64 autograd as above,
+    and moe_expert_ffn on the same routing."""
+    pa = _mod()
+    B, S, H, E, K, I = 2, 96, 100, 8, 2, 52
+    say(f"sparse MLP any size H={H} I={I} E={E} K={K} {dtype}")
+    g = gen(23)
+    x = torch.randn(B, S, H, generator=g).to(dtype)
+    Wr = torch.randn(E, H, generator=g) * 0.05
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype)
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype)
+    gout = torch.randn(B * S, H, generator=g).to(dtype)
+    glog = torch.randn(B * S, E, generator=g) * 0.01
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        mlp.router.weight.copy_(Wr)
+        mlp.experts.gate_up_proj.data = Wgu.to(DEV)
+        mlp.experts.down_proj.data = Wdn.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    out = mlp(xg)
+    assert out.shape == (B, S, H) and out.dtype == dtype
+    logits = mlp.last_router_logits
+    loss = (out.reshape(B * S, H).float() * gout.to(DEV).float()).sum() + (logits * glog.to(DEV)).sum()
+    loss.backward()
+    idx = torch.from_numpy(O.select_topk(logits.detach().cpu(), K))
+    ref = _ref_block_fp64(x.reshape(B * S, H), Wr, Wgu, Wdn, idx, True, gout, glog)
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-4
+    names = ["out", "logits", "dx", "dWr", "dWgu", "dWdn"]
+    got = [out.reshape(B * S, H), logits, xg.grad.reshape(B * S, H), mlp.router.weight.grad,
+           mlp.experts.gate_up_proj.grad, mlp.experts.down_proj.grad]
+    for n, a, b in zip(names, got, ref):
+        check_close(n, a, b, tol, MAX_ABS_FRAC[dtype])
+    # the operator alone, on the module's routing
+    _, tw, ti = pa.router_topk(xg.detach().reshape(B * S, H), mlp.router.weight.detach(), K)
+    h = xg.detach().reshape(B * S, H).clone().requires_grad_(True)
+    gu = mlp.experts.gate_up_proj.detach().clone().requires_grad_(True)
+    dn = mlp.experts.down_proj.detach().clone().requires_grad_(True)
+    y = pa.moe_expert_ffn(h, ti, tw, gu, dn)
+    (y.float() * gout.to(DEV).float()).sum().backward()
+    hr = x.reshape(B * S, H).double().requires_grad_(True)
+    gur, dnr = Wgu.double().requires_grad_(True), Wdn.double().requires_grad_(True)
+    yr = O.expert_ffn_loop(hr, ti.cpu(), tw.cpu().double(), gur, dnr)
+    (yr * gout.double()).sum().backward()
+    for n, a, b in (("ffn out", y, yr), ("ffn dx", h.grad, hr.grad), ("ffn dWgu", gu.grad, gur.grad),
+                    ("ffn dWdn", dn.grad, dnr.grad)):
+        check_close(n, a, b, tol, MAX_ABS_FRAC[dtype])
+
+
 @pytest.mark.parametrize("E,K", [(4, 4), (1, 1)])
 def test_sparse_mlp_every_expert_and_single_expert(E, K):
     """K = E (every token uses every expert) and E = K = 1 (a dense SwiGLU MLP) vs fp64 autograd."""

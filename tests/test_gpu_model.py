@@ -88,11 +88,59 @@ def test_autocast_sparse_mlp(x_dtype):
     check_close("moe_expert_ffn out", y, ref[0], 1e-2, MAX_ABS_FRAC[torch.bfloat16])
 
 
-def test_fp16_autocast_is_rejected():
+def test_fp16_autocast_computes_in_fp32():
+    """Under fp16 autocast the kernels take fp32 operands (they compute in bf16
+    or fp32 only): the module's values and gradients equal the fp32 results
+    without autocast, bit for bit, in the input's dtype."""
     pa = _pa()
     mlp = pa.Qwen3MoeSparseMLP(64, 32, 8, 2).to(DEV)
-    with torch.autocast("cuda", dtype=torch.float16), pytest.raises(NotImplementedError, match="bf16 or fp32"):
-        mlp(torch.randn(1, 8, 64, device=DEV))
+    g = gen(51)
+    with torch.no_grad():
+        for prm in mlp.parameters():
+            prm.copy_(torch.randn(prm.shape, generator=g) * 0.05)
+    x0 = torch.randn(1, 40, 64, generator=g).to(DEV)
+
+    def run(autocast):
+        x = x0.clone().requires_grad_(True)
+        for prm in mlp.parameters():
+            prm.grad = None
+        with torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+            y = mlp(x)
+            lg = mlp.last_router_logits
+        (y.pow(2).sum() + lg.sum()).backward()
+        return [y.detach(), lg.detach(), x.grad] + [prm.grad.clone() for prm in mlp.parameters()]
+
+    plain, amp = run(False), run(True)
+    assert amp[0].dtype == torch.float32
+    for i, (a, b) in enumerate(zip(plain, amp)):
+        assert torch.equal(a, b), i
+
+
+def test_fp16_tensors_compute_in_fp32():
+    """fp16 activations and weights (the reference runs them in fp16): the
+    kernels compute in fp32 and return fp16; values and gradients vs fp64 on
+    the fp16 inputs within fp16's rounding."""
+    pa = _pa()
+    T, H, E, K, I = 96, 64, 8, 2, 32
+    g = gen(53)
+    x = torch.randn(T, H, generator=g).half()
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).half()
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).half()
+    lg = torch.randn(T, E, generator=g)
+    tw, ti = torch.softmax(lg, -1).topk(K, dim=-1)
+    tw = (tw / tw.sum(-1, keepdim=True)).half()
+    gout = torch.randn(T, H, generator=g)
+    h = x.to(DEV).requires_grad_(True)
+    gu, dn = Wgu.to(DEV).requires_grad_(True), Wdn.to(DEV).requires_grad_(True)
+    y = pa.moe_expert_ffn(h, ti.to(DEV), tw.to(DEV), gu, dn)
+    assert y.dtype == torch.float16
+    (y.float() * gout.to(DEV)).sum().backward()
+    hr = x.double().requires_grad_(True)
+    gur, dnr = Wgu.double().requires_grad_(True), Wdn.double().requires_grad_(True)
+    yr = O.expert_ffn_loop(hr, ti, tw.double(), gur, dnr)
+    (yr * gout.double()).sum().backward()
+    for n, a, b in (("out", y, yr), ("dx", h.grad, hr.grad), ("dWgu", gu.grad, gur.grad), ("dWdn", dn.grad, dnr.grad)):
+        check_close(n, a, b, 2e-3, 2e-3)
 
 
 class _Block(nn.Module):
