@@ -172,6 +172,45 @@ def test_sparse_mlp_module_any_size(dtype):
         check_close(n, a, b, tol, MAX_ABS_FRAC[dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sparse_mlp_largest_expert_count_and_top_k(dtype):
+    """E = 1024 and K = 64, the largest the kernels take (include/pmoe.h): the
+    router's widest rows, 1024 groups in every grouped GEMM's scan, most of
+    them empty or one-row; values and every gradient vs fp64 autograd."""
+    pa = _mod()
+    B, S, H, E, K, I = 1, 96, 128, 1024, 64, 64
+    say(f"sparse MLP E={E} K={K} H={H} I={I} {dtype}")
+    g = gen(29)
+    x = torch.randn(B, S, H, generator=g).to(dtype)
+    Wr = torch.randn(E, H, generator=g) * 0.05
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype)
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype)
+    gout = torch.randn(B * S, H, generator=g).to(dtype)
+    glog = torch.randn(B * S, E, generator=g) * 0.01
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        mlp.router.weight.copy_(Wr)
+        mlp.experts.gate_up_proj.data = Wgu.to(DEV)
+        mlp.experts.down_proj.data = Wdn.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    out = mlp(xg)
+    logits = mlp.last_router_logits
+    loss = (out.reshape(B * S, H).float() * gout.to(DEV).float()).sum() + (logits * glog.to(DEV)).sum()
+    loss.backward()
+    idx = torch.from_numpy(O.select_topk(logits.detach().cpu(), K))
+    counts = np.bincount(idx.reshape(-1).numpy(), minlength=E)
+    say(f"  experts hit {(counts > 0).sum()} of {E}, max rows {counts.max()}")
+    ref = _ref_block_fp64(x.reshape(B * S, H), Wr, Wgu, Wdn, idx, True, gout, glog)
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-4
+    names = ["out", "logits", "dx", "dWr", "dWgu", "dWdn"]
+    got = [out.reshape(B * S, H), logits, xg.grad.reshape(B * S, H), mlp.router.weight.grad,
+           mlp.experts.gate_up_proj.grad, mlp.experts.down_proj.grad]
+    for n, a, b in zip(names, got, ref):
+        check_close(n, a, b, tol, MAX_ABS_FRAC[dtype])
+    for e in np.nonzero(counts == 0)[0][:8]:
+        assert torch.count_nonzero(mlp.experts.gate_up_proj.grad[e]) == 0
+
+
 @pytest.mark.parametrize("E,K", [(4, 4), (1, 1)])
 def test_sparse_mlp_every_expert_and_single_expert(E, K):
     """K = E (every token uses every expert) and E = K = 1 (a dense SwiGLU MLP) vs fp64 autograd."""

@@ -295,7 +295,9 @@ def test_gathered_rows_and_routing_weights(dtype, case):
 
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("T,H,E,K,norm", [(2048, 512, 8, 2, True), (1000, 2048, 128, 8, True),
-                                          (300, 256, 60, 4, False), (64, 2048, 128, 8, True)])
+                                          (300, 256, 60, 4, False), (64, 2048, 128, 8, True),
+                                          # the largest expert count and top-k the kernels take
+                                          (256, 256, 1024, 64, True), (130, 264, 200, 13, False)])
 def test_router_forward(x_dtype, T, H, E, K, norm):
     say(f"router T={T} H={H} E={E} K={K} norm={norm} {x_dtype}")
     ops = _ops()
@@ -346,7 +348,9 @@ def test_router_ties_and_bias():
 @pytest.mark.parametrize("T,H,E,K", [(700, 512, 64, 6),
                                      # several 1024-token split-K chunks of the weight gradient and a
                                      # ragged last one; then the config-2 shape (8 chunks)
-                                     (3000, 512, 64, 6), (8192, 2048, 128, 8)])
+                                     (3000, 512, 64, 6), (8192, 2048, 128, 8),
+                                     # the largest expert count and top-k
+                                     (256, 256, 1024, 64)])
 def test_router_backward(norm, x_dtype, T, H, E, K):
     say(f"router backward T={T} H={H} E={E} K={K} norm={norm} {x_dtype}")
     ops = _ops()
