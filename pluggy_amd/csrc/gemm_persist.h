@@ -131,6 +131,14 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   }
 }
 
+// Of D DMAs placed after MFMA slots (i * TOTM) / D, those before slot PRE.
+template <int D, int TOTM, int PRE>
+constexpr int dmas_before() {
+  int c = 0;
+  for (int i = 0; i < D; ++i) c += (i * TOTM) / D < PRE ? 1 : 0;
+  return c;
+}
+
 // GM_RED cost model: a tile of group g runs max(ceil(rows_g / BK), NS - 1)
 // k-stages plus an epilogue worth about kRedEpiStages stages (measured: a
 // 256x256 bf16 tile drains in ~3 stage times). s_cost[g] = cost of one tile of
@@ -308,11 +316,22 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
-  // of stage g. With a double buffer (NS = 2) the next stage has only the
-  // current one to land in, so its DMAs go out in the first substep.
-  constexpr int SPREAD = NS == 2 ? 1 : KS - 1;
+  // of stage g. The gate_up forward at 32-deep stages spreads them over all
+  // KS substeps, the last of which runs after the stage's barrier (measured:
+  // -3 %); the other GEMMs keep them before the barrier (spread, the other
+  // row-grouped GEMMs lost 5-9 % and the weight gradients 3 %). With a double
+  // buffer (NS = 2) the next stage has only the current one to land in, so
+  // its DMAs go out in the first substep.
+  constexpr int SPREAD = NS == 2 ? 1 : ((EPI == EPI_SWIGLU && KS == 2) ? KS : KS - 1);
   constexpr int TOTM = SPREAD * MI * NI;  // MFMA slots the DMAs are spread over (several may share one)
   static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
+  // The stage's DMAs issued before its barrier. At that barrier stream stage
+  // g + 1 must have landed; issued after its last DMA are the full stages
+  // g + 2 .. g + NS - 2 and these D_PRE of stage g + NS - 1, so that many may
+  // stay outstanding.
+  constexpr int D_PRE = dmas_before<D, TOTM, (KS - 1) * MI * NI>();
+  constexpr int WAIT_N = (NS - 3) * D + D_PRE;
+  static_assert(WAIT_N >= 0 && D_PRE >= 1, "stage accounting");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
 
   // k-row gathers: the gathered [k][r] operand's DMA instructions per stage,
@@ -551,7 +570,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
         substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok);
       });
-      if (kt > 0) wait_stages<D, NS>(NS - 2);  // stream stage g + 1 has landed (this wave's share)
+      if (kt > 0) wait_vmcnt<WAIT_N>();  // stream stage g + 1 has landed (this wave's share)
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
       if constexpr (KGATH) {
         // the next stage's DMAs (stream stage g + NS: within this tile or the
