@@ -53,7 +53,7 @@ def parse_args():
     ap.add_argument("--cpu-tokens", type=int, default=256,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
     ap.add_argument("--no-decode", action="store_true",
-                    help="skip the config-5 (decode, 64 tokens) forward leg")
+                    help="skip the config-5 (decode, 64 tokens) forward leg and the EP=8 share leg")
     ap.add_argument("--copy-mib", type=int, default=256,
                     help="size of the device-to-device copy timed as the measured HBM reference (0: skip)")
     return ap.parse_args()
@@ -286,6 +286,57 @@ def decode_leg(dev, steps: int = 50, warmup: int = 5):
             "stages_ms": {n: round(v["mean_ms"], 4) for n, v in sorted(st.items(), key=lambda kv: -kv[1]["total_ms"])}}
 
 
+def ep_share_leg(dev, ep: int = 8, steps: int = 20, warmup: int = 5):
+    """One GPU's share of config 2 under expert parallelism over `ep` GPUs
+    (design only in this build: no all-to-all runs). GPU 0 owns experts
+    [0, E/ep); it receives the config-2 pairs routed to them (their token rows,
+    one row per pair, with the routing weight) and runs the expert FFN forward
+    and backward on those rows alone: `moe_expert_ffn` with K = 1 over E/ep
+    experts, the same kernels at the per-GPU shape."""
+    import torch
+
+    import pluggy_amd
+    from pluggy_amd.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS[2]
+    T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    El = E // ep
+    inp = make_inputs(cfg, device=dev)
+    _, tw, ti = pluggy_amd.router_topk(inp["x"], inp["router_weight"], K)
+    sel = ti.reshape(-1) < El
+    tok = torch.arange(T, device=dev).repeat_interleave(K)[sel]
+    rows = inp["x"][tok].contiguous()
+    idx = ti.reshape(-1)[sel].reshape(-1, 1).contiguous()
+    w = tw.reshape(-1)[sel].reshape(-1, 1).contiguous()
+    gu = inp["gate_up_proj"][:El].clone().requires_grad_(True)
+    dn = inp["down_proj"][:El].clone().requires_grad_(True)
+    g = torch.randn(rows.shape, generator=torch.Generator().manual_seed(3)).to(rows.dtype).to(dev)
+    P = rows.shape[0]
+
+    def step():
+        x = rows.detach().requires_grad_(True)
+        y = pluggy_amd.moe_expert_ffn(x, idx, w, gu, dn)
+        y.backward(g)
+        gu.grad = dn.grad = None
+
+    for _ in range(warmup):
+        step()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = 3.0 * (2.0 * P * H * 2 * I + 2.0 * P * I * H)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": f"expert FFN fwd+bwd of one GPU's share at EP={ep} of {cfg.name}: {El} experts, "
+                        f"{P} received rows (all-to-all not run)",
+            "experts": El, "rows": P, "ms_per_step": round(ms, 4), "TFLOP/s": round(tf, 1),
+            "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
 def copy_bandwidth(mib: int, dev, reps: int = 5):
     """HIP-event time of a plain device-to-device copy of `mib` MiB (read + write counted).
 
@@ -498,11 +549,14 @@ def main() -> int:
         result["reference_gpu"] = ref
     if not args.no_decode and args.config == 2:
         result["decode"] = decode_leg(dev)
+        result["ep8_share"] = ep_share_leg(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
         if args.config == 2:
-            # the reference's own CPU-runnable case: fp32 forward, whole workload
+            # the reference's own CPU-runnable case: fp32 forward, whole workload;
+            # and the decode forward, whole workload
             result["cpu_baseline_config1"] = cpu_baseline(CONFIGS[1], 0)
+            result["cpu_baseline_config5"] = cpu_baseline(CONFIGS[5], 0)
     print(json.dumps(result), flush=True)
     return 0
 
