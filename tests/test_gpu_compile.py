@@ -109,3 +109,42 @@ def test_compiled_block_matches_eager(dtype, backend):
             check_close(f"{n} (inductor vs eager)", b, a, 1e-2 if dtype == torch.bfloat16 else 1e-5,
                         MAX_ABS_FRAC[dtype])
         assert torch.equal(b, c), n
+
+
+@pytest.mark.timeout(600)  # inductor compiles its kernels on first use
+def test_compiled_block_dynamic_sequence_lengths():
+    """The trainer's compiled blocks see different sequence lengths; after the
+    first recompile torch.compile traces them with a symbolic length, through
+    the custom ops' fake implementations. Three lengths under inductor, each
+    against eager (bf16 bar) with the same routing."""
+    from _gpu_helpers import MAX_ABS_FRAC, check_close
+    H, E, K, I = 256, 16, 4, 128
+    torch.manual_seed(0)
+    block = _MoEHalfBlock(H, I, E, K).to(DEV)
+    rw, gu, dn = _weights(E, H, I, seed=7)
+    with torch.no_grad():
+        block.ffn.router.weight.copy_(rw)
+        block.ffn.experts.gate_up_proj.copy_(gu.float())
+        block.ffn.experts.down_proj.copy_(dn.float())
+    block = block.to(torch.bfloat16)
+    block.ffn.router.weight.data = block.ffn.router.weight.data.float()
+    torch._dynamo.reset()
+    compiled = torch.compile(block, mode="default", fullgraph=True)
+
+    def run(mod, x0):
+        for prm in block.parameters():
+            prm.grad = None
+        x = x0.clone().requires_grad_(True)
+        y, z = mod(x)
+        (y.float().pow(2).mean() + 1e-3 * z).backward()
+        counts = block.ffn.router.last_stats.expert_counts.clone()
+        return [y.detach(), x.grad] + [prm.grad.clone() for prm in block.parameters()], counts
+
+    for S in (128, 96, 160):
+        say(f"dynamic compile S={S}")
+        x0 = torch.randn(2, S, H, generator=gen(100 + S)).to(torch.bfloat16).to(DEV)
+        ref, ref_counts = run(block, x0)
+        got, got_counts = run(compiled, x0)
+        assert torch.equal(ref_counts, got_counts)
+        for i, (a, b) in enumerate(zip(ref, got)):
+            check_close(f"S={S} record {i}", b, a, 1e-2, MAX_ABS_FRAC[torch.bfloat16])
