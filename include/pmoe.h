@@ -106,6 +106,16 @@ PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64
 PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
                            void* x_perm, void* stream);
 
+/* pmoe_permute and pmoe_sort_rows in one pass (moe.py:89-108): the
+ * permutation, and for each sorted row p the expert GEMMs' row tables
+ * sorted_token[p] = sorted_pair[p] / K and sorted_w[p] = float(top_weights[
+ * sorted_pair[p]]) (sorted_w may be NULL, then top_weights too). Workspace as
+ * pmoe_permute_workspace_size. */
+PMOE_API int pmoe_permute_rows(const int64_t* top_indices, const void* top_weights, int w_dtype, int64_t T,
+                               int64_t K, int64_t E, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
+                               int32_t* inv_pos, int32_t* sorted_token, float* sorted_w, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* Per sorted row p of the permutation (pair q = sorted_pair[p]):
  * sorted_token[p] = q / K, the token whose row the expert GEMMs gather (the
  * reference's sorted_token, moe.py:90-101), and sorted_w[p] = top_weights[q]

@@ -38,6 +38,7 @@ SIGNATURES = {
     "pmoe_count_invalid_ids": (_INT, [_P, _I64, _I64, _P, _P]),
     "pmoe_dispatch": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P]),
     "pmoe_sort_rows": (_INT, [_P, _P, _INT, _I64, _I64, _P, _P, _P]),
+    "pmoe_permute_rows": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "pmoe_gate_up_swiglu": (_INT, [_P, _P, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "pmoe_down_proj": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P]),
     "pmoe_combine": (_INT, [_P, _P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P]),

@@ -298,6 +298,25 @@ PMOE_API int pmoe_permute(const int64_t* top_indices, int64_t T, int64_t K, int6
   return PMOE_OK;
 }
 
+PMOE_API int pmoe_permute_rows(const int64_t* top_indices, const void* top_weights, int w_dtype, int64_t T,
+                               int64_t K, int64_t E, int32_t* counts, int32_t* offs, int32_t* sorted_pair,
+                               int32_t* inv_pos, int32_t* sorted_token, float* sorted_w, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (int rc = check_moe_dims(T, K, E, 8, 0)) return rc;
+  PMOE_REQUIRE(dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(counts && offs &&
+                   (T == 0 || (top_indices && sorted_pair && inv_pos && sorted_token && (!sorted_w || top_weights))),
+               "permute_rows: null tensor");
+  const size_t need = pmoe_permute_workspace_size(T, K, E);
+  if (workspace_bytes < need || !workspace)
+    return fail(PMOE_ERR_WORKSPACE, "permute_rows: workspace %zu < %zu bytes", workspace_bytes, need);
+  PMOE_TRY(permute_pairs(top_indices, (int)T, (int)K, (int)E, counts, offs, sorted_pair, inv_pos,
+                         static_cast<int32_t*>(workspace), kPermuteChunk, as_stream(stream), sorted_token, sorted_w,
+                         top_weights, w_dtype == PMOE_BF16),
+           "permute_rows");
+  return PMOE_OK;
+}
+
 PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64_t E, int32_t* count,
                                     void* stream) {
   PMOE_REQUIRE(n >= 0 && E >= 1, "count_invalid_ids: n %lld, E %lld", (long long)n, (long long)E);
@@ -569,12 +588,11 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
   PMOE_REQUIRE(I > 0 && dtype_ok(dtype) && dtype_ok(w_dtype), "expert_ffn_forward: bad dtype or I");
-  if (int rc = pmoe_permute(top_indices, T, K, E, counts, offs, sorted_pair, inv_pos, workspace, workspace_bytes,
-                            stream))
+  if (int rc = pmoe_permute_rows(top_indices, top_weights, w_dtype, T, K, E, counts, offs, sorted_pair, inv_pos,
+                                 sorted_token, sorted_w, workspace, workspace_bytes, stream))
     return rc;
   if (T == 0) return PMOE_OK;
   const int64_t P = T * K;
-  if (int rc = pmoe_sort_rows(sorted_pair, top_weights, w_dtype, T, K, sorted_token, sorted_w, stream)) return rc;
   if (int rc = pmoe_gate_up_swiglu(hidden, sorted_token, sorted_w, T, gate_up_proj, offs, dtype, P, E, H, I,
                                    gate_up_out, mid, stream))
     return rc;

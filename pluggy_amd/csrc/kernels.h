@@ -71,8 +71,14 @@ template <typename TG>
 hipError_t pair_weight_grad(const float* part, int ld, int nparts, const int32_t* inv_pos, int P, TG* grad_w,
                             hipStream_t s);
 hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* count, hipStream_t s);
+// Stable counting-sort permutation of the T*K pairs by expert; with
+// sorted_token non-null it also writes the expert GEMMs' row tables
+// (sorted_token[p] = sorted_pair[p] / K, sorted_w[p] = float(w[sorted_pair[p]]),
+// w bf16 when w_bf16 else fp32; sorted_w may be null).
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
-                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s);
+                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s,
+                         int32_t* sorted_token = nullptr, float* sorted_w = nullptr, const void* w = nullptr,
+                         int w_bf16 = 0);
 template <typename T>
 hipError_t dispatch_rows(const T* x, const int32_t* inv_pos, int T_, int K, int H, T* x_perm, hipStream_t s);
 template <typename T, typename TW>

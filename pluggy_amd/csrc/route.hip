@@ -460,6 +460,26 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
   }
 }
 
+// The expert GEMMs' row tables of sorted row p (pair q): sorted_token[p] =
+// q / K and sorted_w[p] = float(w[q]) (w bf16 or fp32; sorted_w may be NULL).
+// With sorted_token NULL the permutation writes no tables.
+struct RowTables {
+  int32_t* sorted_token = nullptr;
+  float* sorted_w = nullptr;
+  const void* w = nullptr;
+  int w_bf16 = 0;
+  int K = 1;
+};
+
+__device__ __forceinline__ void write_row_tables(const RowTables& rt, int pos, int q) {
+  if (rt.sorted_token != nullptr) {
+    rt.sorted_token[pos] = q / rt.K;
+    if (rt.sorted_w != nullptr)
+      rt.sorted_w[pos] = rt.w_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(rt.w)[q])
+                                   : static_cast<const float*>(rt.w)[q];
+  }
+}
+
 // Stable scatter of pairs q0 .. q1-1 by one block of 256 threads: s_base[e]
 // holds the position of expert e's first pair of the range, s_wcnt ([4][E])
 // is zero. Within a round of 256 pairs, a pair's rank among the lower lanes
@@ -468,7 +488,7 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
 __device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict__ idx, int q0, int q1, int E,
                                                       int nbits, int* s_base, int* s_wcnt,
                                                       int32_t* __restrict__ sorted_pair,
-                                                      int32_t* __restrict__ inv_pos) {
+                                                      int32_t* __restrict__ inv_pos, const RowTables& rt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int qb = q0; qb < q1; qb += 256) {
@@ -489,6 +509,7 @@ __device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict_
       for (int w = 0; w < wave; ++w) pos += s_wcnt[w * E + e];
       sorted_pair[pos] = q;
       inv_pos[q] = pos;
+      write_row_tables(rt, pos, q);
     }
     __syncthreads();
     for (int x = tid; x < E; x += 256) {
@@ -502,7 +523,7 @@ __device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict_
 __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
                                                               int chunk, const int32_t* __restrict__ chunk_base,
                                                               int32_t* __restrict__ sorted_pair,
-                                                              int32_t* __restrict__ inv_pos) {
+                                                              int32_t* __restrict__ inv_pos, RowTables rt) {
   extern __shared__ int sm[];
   int* s_base = sm;       // [E]
   int* s_wcnt = sm + E;   // [4][E]
@@ -512,7 +533,71 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
   }
   __syncthreads();
   const int q0 = blockIdx.x * chunk;
-  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos);
+  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
+}
+
+// The scatter for at most kFusedScanChunks chunks, with the scan folded in:
+// every block reads the whole chunk histogram (nchunks x E counts, a few
+// KiB), sums each expert's column (its total, and the part before this
+// block's chunk), and scans the totals over the experts, so the bases need no
+// kernel of their own; block 0 also writes counts and offs. The sums run in
+// chunk order and the scan in expert order, so every block derives the same
+// bases as the separate scan would.
+constexpr int kFusedScanChunks = 64;
+__global__ __launch_bounds__(256) void permute_scatter_scan_kernel(const int64_t* __restrict__ idx, int P, int E,
+                                                                   int nbits, int chunk, int nchunks,
+                                                                   const int32_t* __restrict__ chunk_hist,
+                                                                   int32_t* __restrict__ counts,
+                                                                   int32_t* __restrict__ offs,
+                                                                   int32_t* __restrict__ sorted_pair,
+                                                                   int32_t* __restrict__ inv_pos, RowTables rt) {
+  extern __shared__ int sm[];
+  int* s_base = sm;       // [E]
+  int* s_wcnt = sm + E;   // [4][E]
+  __shared__ int s_wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x;
+  // thread t takes experts t*per .. t*per+per-1 (E <= 1024, per <= 4): their
+  // totals over all chunks and their sums over the chunks before c
+  const int per = (E + 255) / 256;
+  int tot[4], pre[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * per + j;
+    tot[j] = pre[j] = 0;
+    if (j < per && e < E) {
+      int v[kFusedScanChunks];
+#pragma unroll
+      for (int i = 0; i < kFusedScanChunks; ++i) v[i] = i < nchunks ? chunk_hist[(int64_t)i * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < kFusedScanChunks; ++i) {
+        if (i < c) pre[j] += v[i];
+        tot[j] += v[i];
+      }
+    }
+    sum += tot[j];
+  }
+  const int inc = wave_incl_scan(sum, lane);
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  int excl = inc - sum;
+  for (int w = 0; w < wave; ++w) excl += s_wsum[w];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * per + j;
+    if (j < per && e < E) {
+      if (c == 0) {
+        counts[e] = tot[j];
+        offs[e] = excl + tot[j];
+      }
+      s_base[e] = excl + pre[j];
+      excl += tot[j];
+    }
+  }
+  for (int e = tid; e < 4 * E; e += 256) s_wcnt[e] = 0;
+  __syncthreads();
+  const int q0 = c * chunk;
+  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
 }
 
 // The whole permutation of at most one chunk of pairs (decode) in one block:
@@ -521,7 +606,7 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
 __global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
                                                             int32_t* __restrict__ counts, int32_t* __restrict__ offs,
                                                             int32_t* __restrict__ sorted_pair,
-                                                            int32_t* __restrict__ inv_pos) {
+                                                            int32_t* __restrict__ inv_pos, RowTables rt) {
   extern __shared__ int sm[];
   int* s_base = sm;       // [E]: counts, then exclusive bases
   int* s_wcnt = sm + E;   // [4][E]
@@ -559,7 +644,7 @@ __global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __res
     }
   }
   __syncthreads();
-  permute_scatter_range(idx, 0, P, E, nbits, s_base, s_wcnt, sorted_pair, inv_pos);
+  permute_scatter_range(idx, 0, P, E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
 }
 
 // ---- row movers: one wave per token, 16-byte lanes. KC > 0 is the top-k
@@ -831,22 +916,34 @@ hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out,
 }
 
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
-                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s) {
+                         int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s,
+                         int32_t* sorted_token, float* sorted_w, const void* w, int w_bf16) {
   const int P = T * K;
   const int nchunks = (P + chunk - 1) / chunk;
   if (E > 1024 || E < 1) return hipErrorInvalidValue;
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
+  RowTables rt;
+  rt.sorted_token = sorted_token;
+  rt.sorted_w = sorted_w;
+  rt.w = w;
+  rt.w_bf16 = w_bf16;
+  rt.K = K;
   if (nchunks <= 1) {
     hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits, counts,
-                       offs, sorted_pair, inv_pos);
+                       offs, sorted_pair, inv_pos, rt);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
                      chunk_hist);
+  if (nchunks <= kFusedScanChunks) {
+    hipLaunchKernelGGL(permute_scatter_scan_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E,
+                       nbits, chunk, nchunks, chunk_hist, counts, offs, sorted_pair, inv_pos, rt);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_hist, nchunks, E, counts, offs);
   hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits,
-                     chunk, chunk_hist, sorted_pair, inv_pos);
+                     chunk, chunk_hist, sorted_pair, inv_pos, rt);
   return hipGetLastError();
 }
 

@@ -301,9 +301,7 @@ def _ffn_forward(hidden, top_indices, top_weights, gate_up_proj, down_proj):
     E = gate_up_proj.shape[0]
     K = top_indices.shape[1]
     with _stage("permute"):
-        _, offs, sorted_pair, inv_pos = ops.permute(top_indices, E)
-    with _stage("sort_rows"):
-        sorted_token, sorted_w = ops.sort_rows(sorted_pair, top_weights, K)
+        _, offs, _sorted_pair, inv_pos, sorted_token, sorted_w = ops.permute_rows(top_indices, top_weights, E)
     with _stage("gate_up_fwd"):
         gu, mid = ops.gate_up_swiglu(hidden, gate_up_proj, offs, sorted_token, sorted_w)
     with _stage("down_fwd"):
@@ -667,9 +665,7 @@ def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_pro
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
             normed, router_weight, top_k, norm_topk_prob, logit_bias)
     with _stage("permute"):
-        _, offs, sorted_pair, inv_pos = ops.permute(top_i, gate_up_proj.shape[0])
-    with _stage("sort_rows"):
-        stok, sw = ops.sort_rows(sorted_pair, top_w, top_k)
+        _, offs, _sorted_pair, inv_pos, stok, sw = ops.permute_rows(top_i, top_w, gate_up_proj.shape[0])
     with _stage("gate_up_fwd"):
         gu, mid = ops.gate_up_swiglu(normed, gate_up_proj, offs, stok, sw)
     with _stage("down_fwd"):

@@ -68,6 +68,24 @@ def permute(top_indices, num_experts: int):
     return counts, offs, sorted_pair, inv_pos
 
 
+def permute_rows(top_indices, top_weights, num_experts: int):
+    """``permute`` and ``sort_rows`` in one pass: -> counts, offs, sorted_pair, inv_pos,
+    sorted_token (P,) int32, sorted_w (P,) fp32 (None when top_weights is None)."""
+    require_gpu(top_indices)
+    T, K = top_indices.shape
+    dev = top_indices.device
+    P = T * K
+    i32 = torch.int32
+    counts, offs = (torch.empty(num_experts, dtype=i32, device=dev) for _ in range(2))
+    sorted_pair, inv_pos, tok = (torch.empty(P, dtype=i32, device=dev) for _ in range(3))
+    sw = torch.empty(P, dtype=torch.float32, device=dev) if top_weights is not None else None
+    wcode = dtype_code(top_weights.dtype) if top_weights is not None else 0
+    ws = workspace(size("pmoe_permute_workspace_size", T, K, num_experts), dev)
+    call("pmoe_permute_rows", ptr(top_indices), ptr(top_weights), wcode, T, K, num_experts, ptr(counts), ptr(offs),
+         ptr(sorted_pair), ptr(inv_pos), ptr(tok), ptr(sw), ptr(ws), ws.numel(), stream_of(top_indices))
+    return counts, offs, sorted_pair, inv_pos, tok, sw
+
+
 def count_invalid_ids(top_indices, num_experts: int) -> torch.Tensor:
     """-> (1,) int32 device tensor: ids of top_indices outside [0, E)."""
     require_gpu(top_indices)

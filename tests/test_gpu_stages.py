@@ -34,6 +34,8 @@ def _ops():
     (100, 8, 8, "uniform"), (8192, 8, 128, "uniform"), (8192, 8, 128, "zipf"), (4099, 6, 1000, "low"),
     # one chunk of pairs or less: the single-block path (P = 2048 is its largest case)
     (256, 8, 128, "zipf"), (64, 8, 1000, "low"), (40, 3, 256, "one"), (257, 8, 128, "uniform"),
+    # 64 chunks, the most the scatter scans itself; then the separate-scan path
+    (16384, 8, 128, "zipf"), (20000, 8, 128, "uniform"), (9000, 8, 1000, "low"),
 ])
 def test_permute_bitexact(T, K, E, mode):
     say(f"permute T={T} K={K} E={E} mode={mode}")
@@ -45,6 +47,17 @@ def test_permute_bitexact(T, K, E, mode):
     assert np.array_equal(to_np(offs), ro)
     assert np.array_equal(to_np(sp), rsp)
     assert np.array_equal(to_np(inv), rinv)
+    # the one-pass form with the GEMMs' row tables (bf16 and fp32 weights, and none)
+    for wdt in (torch.bfloat16, torch.float32, None):
+        w = None if wdt is None else torch.rand(T, K, generator=gen(T)).to(wdt)
+        c2, o2, sp2, inv2, tok, sw = _ops().permute_rows(idx.to(DEV), None if w is None else w.to(DEV), E)
+        assert np.array_equal(to_np(c2), rc.astype(np.int32)) and np.array_equal(to_np(o2), ro)
+        assert np.array_equal(to_np(sp2), rsp) and np.array_equal(to_np(inv2), rinv)
+        assert np.array_equal(to_np(tok), rsp // K)
+        if w is None:
+            assert sw is None
+        else:
+            assert torch.equal(sw.cpu(), w.float().reshape(-1)[torch.from_numpy(rsp).long()])
 
 
 def test_permute_deterministic():
