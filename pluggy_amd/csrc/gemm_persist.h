@@ -29,31 +29,73 @@ struct PersistLayout {
   static_assert(EPI_LD % 4 == 0, "16-byte aligned staging rows");
 };
 
+// Lane l receives lane (l ^ 1)'s value (DPP quad permutation 1, 0, 3, 2).
+__device__ __forceinline__ float swap_lane_pair(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+
 // Epilogue through per-wave 16-row slabs: slab (i, h2) holds rows 16 h2 ..
 // 16 h2 + 15 of the wave's 32-row block i. In the MFMA 32x32 layout lane half
 // h holds rows 8 q + 4 h + r (r = 0..3) of a block, so slab h2 gathers q =
 // 2 h2 and 2 h2 + 1: local row 8 (q - 2 h2) + 4 h + r. Each lane then reads 8
 // consecutive outputs and stores 16 bytes.
-template <class Cfg, typename Tout, int GM, int EPI>
+//
+// The forward GEMMs (bf16 outputs) round in registers and stage packed: lanes 2c and 2c + 1 hold
+// columns 2c and 2c + 1 of the same four rows, so they swap half of their
+// values and each writes two dwords of (column 2c, 2c + 1) pairs, rows 0-1
+// from the even lane and rows 2-3 from the odd one. Packed rows are
+// WN / 2 + 8 dwords apart, so the four rows one write instruction touches
+// start 16 banks apart. The rounding is the v_cvt_pk_bf16_f32 the fp32 path
+// applies after staging, so both give the same bits; the packed staging
+// takes half the LDS of the fp32 one (measured: the same speed), which the
+// wide tiles' larger ring slots need.
+template <class Cfg, bool PACK>
+struct EpiStage {
+  static constexpr int ROW = PACK ? Cfg::WN / 2 + 8 : PersistLayout<Cfg>::EPI_LD;  // 4-byte words per staged row
+  static constexpr int WORDS = Cfg::NW * PersistLayout<Cfg>::SLAB * ROW;
+  static_assert(ROW % 4 == 0, "16-byte aligned staging rows");
+};
+
+template <class Cfg, typename Tout, int GM, int EPI, bool PACK>
 __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN;
   constexpr int LD = PersistLayout<Cfg>::EPI_LD, SLAB = PersistLayout<Cfg>::SLAB;
+  constexpr int LDW = EpiStage<Cfg, PACK>::ROW;  // packed: words per staged row
+  static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
   const int half = lane >> 5, col_l = lane & 31;
+  uint32_t* st32 = reinterpret_cast<uint32_t*>(stage);
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
+      if constexpr (PACK) {
+        const bool odd = lane & 1;
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq)
+        for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-        for (int j = 0; j < NI; ++j)
+          for (int j = 0; j < NI; ++j) {
+            const int q0 = 4 * (2 * h2 + qq);
+            const float v0 = acc[i][j][q0], v1 = acc[i][j][q0 + 1], v2 = acc[i][j][q0 + 2], v3 = acc[i][j][q0 + 3];
+            const float r0 = swap_lane_pair(odd ? v0 : v2), r1 = swap_lane_pair(odd ? v1 : v3);
+            const uint32_t p0 = odd ? cvt_pk_bf16(r0, v2) : cvt_pk_bf16(v0, r0);
+            const uint32_t p1 = odd ? cvt_pk_bf16(r1, v3) : cvt_pk_bf16(v1, r1);
+            const int row = 8 * qq + 4 * half + (odd ? 2 : 0);
+            st32[row * LDW + j * 16 + (col_l >> 1)] = p0;
+            st32[(row + 1) * LDW + j * 16 + (col_l >> 1)] = p1;
+          }
+      } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            stage[(8 * qq + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * (2 * h2 + qq) + r];
+        for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              stage[(8 * qq + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * (2 * h2 + qq) + r];
+      }
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
       asm volatile("" ::: "memory");
       const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * h2;
@@ -65,10 +107,10 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
           const int r = e / CPR, c = (e % CPR) * 8;
           const int row = row_base + r, col = ti.n0 + wn * H2 + c;
           if (row < ti.m_end && col < p.inter) {
+            static_assert(PACK, "the SwiGLU forward stages bf16");
             float g[8], u[8], m[8];
-            Vec8<float>::load(stage + r * LD + c, g);
-            Vec8<float>::load(stage + r * LD + H2 + c, u);
-            const u32x4 gw = Out8<bf16_t>::pack(g), uw = Out8<bf16_t>::pack(u);
+            const u32x4 gw = *reinterpret_cast<const u32x4*>(st32 + r * LDW + c / 2);
+            const u32x4 uw = *reinterpret_cast<const u32x4*>(st32 + r * LDW + H2 / 2 + c / 2);
             *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
             *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
             unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
@@ -90,9 +132,17 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
           float pd = 0.0f;  // this lane's share of <acc, silu(g) u> (EPI_SWIGLU_BWD with row_w)
           if (row < ti.m_end && col < p.N) {
             float v[8];
-            Vec8<float>::load(stage + r * LD + c, v);
-            if constexpr (EPI == EPI_SWIGLU_BWD) {
+            if constexpr (PACK) {
+              const u32x4 w = *reinterpret_cast<const u32x4*>(st32 + r * LDW + c / 2);
+              if (col + 8 <= p.N) {
+                *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = w;
+              } else {
+                unpack8(w, v);
+                for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+              }
+            } else if constexpr (EPI == EPI_SWIGLU_BWD) {
               // v = d(mid), or with row_w d(w * mid): then d(mid) = w v and d(w) += v . mid
+              Vec8<float>::load(stage + r * LD + c, v);
               const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
               float g[8], u[8], dg[8], du[8];
               Vec8<bf16_t>::load(GU + col, g);
@@ -109,10 +159,13 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
               }
               Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
               Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
-            } else if (col + 8 <= p.N) {
-              Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
             } else {
-              for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+              Vec8<float>::load(stage + r * LD + c, v);
+              if (col + 8 <= p.N) {
+                Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
+              } else {
+                for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
+              }
             }
           }
           if constexpr (EPI == EPI_SWIGLU_BWD) {
@@ -137,6 +190,97 @@ constexpr int dmas_before() {
   int c = 0;
   for (int i = 0; i < D; ++i) c += (i * TOTM) / D < PRE ? 1 : 0;
   return c;
+}
+
+// Slot of DMA DI among the TOTM MFMA slots of a stage: the D DMAs of a
+// regular tile at (DI * TOTM) / D, the extra one of a wide tile at TOTM / (2 D)
+// (between the first two).
+template <int D, int TOTM>
+constexpr int dma_slot(int di) {
+  return di < D ? (di * TOTM) / D : TOTM / (2 * D);
+}
+
+// Wide tiles. An expert's last m-tile that holds at most BM / 2 rows would
+// stream a whole weight block for few rows; the row-grouped GEMMs with two
+// k-contiguous operands (the two forward GEMMs) therefore cover it with
+// BM / 2 x 2 BN tiles instead, each wave taking BM / 2 rows of its own WN
+// columns. A stage slot then holds BM / 2 A rows and 2 BN B rows (5 DMAs per
+// wave instead of 4, measured ~1.05-1.1 of a regular tile's stage) and half as
+// many tiles cover the tail. The slot is one array of 1 KB DMA rows: DMA J of
+// wave w fills rows 16 (w + 8 J) ..+15 in both shapes (A rows first, then B),
+// so only the source rows of DMAs 1-4 depend on the shape.
+template <int NW, int BK>
+struct SlotDma {
+  static_assert(BK == 32 && NW == 8, "wide tiles: 32-deep stages of 1 KB DMAs, 8 waves");
+  static constexpr int NJ = 5;
+  uint32_t off[NJ];  // bytes of (row, this lane's chunk) at k = 0, or kOOB
+  int kc;            // this lane's k offset within the stage (the same for every DMA at BK 32)
+
+  // From the A DMAs of a BM = 256 tile (rows 16 w, 128 + 16 w) and the B DMAs
+  // of a 512-row B tile (rows 16 w + 128 i): a regular tile takes A 0, A 1,
+  // B 0, B 1; a wide tile A 0, B 0 .. B 3.
+  __device__ __forceinline__ void set(const KcDma<256, NW, BK>& a, const KcDma<512, NW, BK>& b, bool wide) {
+    off[0] = a.rowoff[0];
+    off[1] = wide ? b.rowoff[0] : a.rowoff[1];
+    off[2] = wide ? b.rowoff[1] : b.rowoff[0];
+    off[3] = wide ? b.rowoff[2] : b.rowoff[1];
+    off[4] = b.rowoff[3];
+    kc = a.kc[0];
+  }
+  __device__ __forceinline__ void select(bool second, const SlotDma& y, const SlotDma& x) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) off[j] = second ? y.off[j] : x.off[j];
+    kc = second ? y.kc : x.kc;
+  }
+  // DMA J of the stage into the slot at LDS byte address `slot`: J = 0 reads
+  // A, J >= 2 reads B, J = 1 reads A in a regular tile and B in a wide one.
+  template <int J>
+  __device__ __forceinline__ void issue1(const BufRsrc& rsA, const BufRsrc& rsB, bool wide, uint32_t slot, int k0,
+                                         int k_hi, bool tail, int wave) const {
+    uint32_t v = off[J] + (uint32_t)(k0 * 2);
+    if (tail && k0 + kc >= k_hi) v = kOOB;
+    if constexpr (J == 1) {
+      BufRsrc rs;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(wide ? rsB[w] : rsA[w]);
+      dma16(rs, slot + (wave + J * NW) * 1024, v);
+    } else {
+      dma16(J == 0 ? rsA : rsB, slot + (wave + J * NW) * 1024, v);
+    }
+  }
+};
+
+// Stand-in for the B loader of the wide-tile kernels (SlotDma carries both operands).
+struct NoDma {
+  __device__ __forceinline__ void select(bool, const NoDma&, const NoDma&) {}
+};
+
+// Tiles of the row-grouped GEMMs with wide tiles: a group of `rows` rows has
+// rows / BM full m-tiles of ntn n-tiles each, plus a last m-tile of ntn
+// regular tiles, or of ceil(ntn / 2) wide tiles when it holds at most BM / 2
+// rows. s_scan[g] = tiles of the groups before g (inclusive scan to groups + 1
+// entries, computed by wave 0); returns the total.
+template <int BM>
+__device__ __forceinline__ int rows_scan_wide(const int32_t* offs, int groups, int ntn, int* s_scan) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    int carry = 0;
+    for (int base = 0; base < groups; base += 64) {
+      const int g = base + lane;
+      int tiles = 0;
+      if (g < groups) {
+        const int rows = offs[g] - (g == 0 ? 0 : offs[g - 1]);
+        const int tail = rows % BM;
+        tiles = (rows / BM) * ntn + (tail == 0 ? 0 : (tail <= BM / 2 ? (ntn + 1) / 2 : ntn));
+      }
+      const int inc = wave_incl_scan(tiles, lane) + carry;
+      if (g < groups) s_scan[g + 1] = inc;
+      carry = __shfl(inc, 63, kWave);
+    }
+    if (lane == 0) s_scan[0] = 0;
+  }
+  __syncthreads();
+  return s_scan[groups];
 }
 
 // GM_RED cost model: a tile of group g runs max(ceil(rows_g / BK), NS - 1)
@@ -223,6 +367,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   typedef PersistLayout<Cfg> L;
+  // Wide tiles for short last m-tiles: the row-grouped GEMMs with two
+  // k-contiguous operands at the 256 x 256 shape (the forward GEMMs).
+  constexpr bool WIDE = GM == GM_ROWS && A_KC && B_KC && BM == 256 && BN == 256 && Cfg::WAVES_M == 2 &&
+                        Cfg::WAVES_N == 4 && BK == 32 && NS == 3;
+  constexpr int SLOT = Cfg::STAGE_BYTES + (WIDE ? Cfg::STAGE_BYTES / 4 : 0);  // ring slot bytes
+  // the forward GEMMs stage their bf16 outputs packed
+  constexpr bool PACK = sizeof(Tout) == 2 && GM == GM_ROWS && A_KC && B_KC && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
+  static_assert(PACK || EPI != EPI_SWIGLU, "the SwiGLU forward stages packed bf16");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");
@@ -230,8 +382,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
                     ((GATH == GA_KROWS || GATH == GB_KROWS) && GM == GM_RED),
                 "gathers: A's rows in GM_ROWS, A's or B's k-rows in GM_RED");
 
-  __shared__ __attribute__((aligned(1024))) char smem[L::RING];
-  __shared__ __attribute__((aligned(16))) float s_epi[L::EPI_FLOATS];
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SLOT];
+  __shared__ __attribute__((aligned(16))) float s_epi[EpiStage<Cfg, PACK>::WORDS];
   __shared__ int s_scan[1025];
   __shared__ int s_offs[1024];
   __shared__ int s_order[1024];  // GM_RED under skew: groups by tile cost, descending
@@ -248,7 +400,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   const int mt_red = (p.M + BM - 1) / BM;  // GM_RED: m-tiles per group
   int total;
-  if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
+  if constexpr (WIDE) total = rows_scan_wide<BM>(s_offs, groups, ntiles_n, s_scan);
+  else if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
   else total = groups * mt_red * ntiles_n;
   // XCD x (blocks with blockIdx % 8 == x) takes a contiguous share of the tiles
   // and its blocks walk it in a stride of their count. GM_ROWS tiles all run
@@ -308,11 +461,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   if (tile_at(0) < 0) return;
 
   const uint32_t lds0 = lds_addr(smem);
-  float* stage = s_epi + wave * L::SLAB * L::EPI_LD;
+  float* stage = s_epi + wave * L::SLAB * EpiStage<Cfg, PACK>::ROW;
   const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
-  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
-  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
+  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA0;
+  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB0;
+  // wide-tile kernels load both operands through one SlotDma
+  typedef typename std::conditional<WIDE, SlotDma<NW, BK>, LdA0>::type LdA;
+  typedef typename std::conditional<WIDE, NoDma, LdB0>::type LdB;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
@@ -331,8 +487,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // stay outstanding.
   constexpr int D_PRE = dmas_before<D, TOTM, (KS - 1) * MI * NI>();
   constexpr int WAIT_N = (NS - 3) * D + D_PRE;
+  // a wide tile's extra DMA sits at slot TOTM / (2 D); NS = 3 (see WIDE)
+  constexpr int DX = WIDE ? D + 1 : D;  // DMAs per stage of a wide tile
+  constexpr int WAIT_W = D_PRE + (dma_slot<D, TOTM>(D) < (KS - 1) * MI * NI ? 1 : 0);
   static_assert(WAIT_N >= 0 && D_PRE >= 1, "stage accounting");
+  static_assert(!WIDE || (D == 4 && Cfg::A_INSTR == 2 && TOTM >= 2 * D), "wide tiles: 4 + 1 DMAs per wave");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
+  // a wide tile's waves all take rows 0 .. BM/2 - 1, wave w the B rows (columns) of block w
+  const int a_row0w = 0, b_row0w = wave * Cfg::WN;
 
   // k-row gathers: the gathered [k][r] operand's DMA instructions per stage,
   // each covering KPI = 2 k-rows (lanes 0-31 the first, 32-63 the second).
@@ -351,7 +513,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     LdA la;
     LdB lb;
     int nk, kd0, kd_hi;
-    int klo;  // first reduction index of the tile (wave-uniform; k-row gathers)
+    int klo;   // first reduction index of the tile (wave-uniform; k-row gathers)
+    int wide;  // a wide tile (WIDE kernels; wave-uniform)
   };
   // Tile t of the list (t < 0: past the block's last tile; its descriptors
   // are empty, so every DMA reads zeros).
@@ -361,12 +524,42 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     T.kd0 = 0;
     T.kd_hi = 0;
     T.klo = 0;
+    T.wide = 0;
     const bf16_t* a_base = A0;
     const bf16_t* b_base = B0;
     uint64_t a_bytes = 0, b_bytes = 0;
     if (t >= 0) {
       int tn = t % ntiles_n, slot = t / ntiles_n;
-      if constexpr (GM == GM_ROWS) {
+      if constexpr (WIDE) {
+        // the tiles of group g: its full m-tiles n-tile major, each pair of
+        // n-tiles followed by the wide tile under them when the last m-tile
+        // is short, else (a regular last m-tile) every n-tile's m-tiles in turn
+        const int g = rows_group(s_scan, groups, t);
+        const int lo = g == 0 ? 0 : s_offs[g - 1], rows = s_offs[g] - lo;
+        const int nfull = rows / BM, tail = rows % BM, local = t - s_scan[g];
+        int mt;
+        if (tail > 0 && tail <= BM / 2) {
+          const int q = local / (2 * nfull + 1), r = local % (2 * nfull + 1);
+          const int npair = min(2, ntiles_n - 2 * q);
+          if (r == npair * nfull) {
+            T.wide = 1;
+            tn = q;
+            mt = nfull;
+          } else {
+            tn = 2 * q + r / nfull;
+            mt = r % nfull;
+          }
+        } else {
+          const int ns = nfull + (tail > 0 ? 1 : 0);
+          tn = local / ns;
+          mt = local % ns;
+        }
+        T.wide = __builtin_amdgcn_readfirstlane(T.wide);
+        T.ti.group = g; T.ti.m0 = lo + mt * BM; T.ti.m_end = s_offs[g];
+        T.ti.k_lo = 0; T.ti.k_hi = p.K;
+        b_base = B0 + (int64_t)g * p.strideB;
+        b_bytes = p.b_bytes;
+      } else if constexpr (GM == GM_ROWS) {
         // An expert's tiles are ordered n-tile major, its m-tiles inner, so
         // that the m-tiles sharing a weight block run next to each other.
         const int g = rows_group(s_scan, groups, slot);
@@ -384,7 +577,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         T.ti.k_lo = g == 0 ? 0 : s_offs[g - 1];
         T.ti.k_hi = s_offs[g];
       }
-      T.ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+      T.ti.n0 = ((EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN) * (T.wide ? 2 : 1);
       if constexpr (A_KC) {
         if constexpr (GATH == GA_ROWS) {
           a_bytes = p.a_bytes;  // the whole gathered storage
@@ -414,30 +607,41 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     }
     T.rsA = make_rsrc(a_base, a_bytes);
     T.rsB = make_rsrc(b_base, b_bytes);
-    if constexpr (A_KC) {
+    // B rows (columns) of the tile: with SwiGLU, wave column block w holds
+    // WN/2 gate columns then the matching up columns
+    const int n0 = T.ti.n0, N = p.N, I = p.inter;
+    auto b_row_of = [&](int c) {
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
+        const int gcol = n0 + w * h + (cc % h);
+        if (gcol >= I) return -1;
+        return cc < h ? gcol : I + gcol;
+      } else {
+        return n0 + c < N ? n0 + c : -1;
+      }
+    };
+    if constexpr (WIDE) {
+      KcDma<BM, NW, BK> la;
+      KcDma<2 * BN, NW, BK> lb;
       const int rows = T.ti.m_end - T.ti.m0;
       if constexpr (GATH == GA_ROWS)
-        T.la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
+        la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
       else
-        T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
+        la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
+      lb.init(b_row_of, p.ldb, wave, lane);
+      T.la.set(la, lb, T.wide != 0);
     } else {
-      T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
-    }
-    if constexpr (B_KC) {
-      const int n0 = T.ti.n0, N = p.N, I = p.inter;
-      if constexpr (EPI == EPI_SWIGLU) {
-        // wave column block w holds WN/2 gate columns then the matching up columns
-        T.lb.init([&](int c) {
-          const int w = c / Cfg::WN, cc = c % Cfg::WN, h = Cfg::WN / 2;
-          const int gcol = n0 + w * h + (cc % h);
-          if (gcol >= I) return -1;
-          return cc < h ? gcol : I + gcol;
-        }, p.ldb, wave, lane);
+      if constexpr (A_KC) {
+        const int rows = T.ti.m_end - T.ti.m0;
+        if constexpr (GATH == GA_ROWS)
+          T.la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
+        else
+          T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
       } else {
-        T.lb.init([&](int c) { return n0 + c < N ? n0 + c : -1; }, p.ldb, wave, lane);
+        T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
       }
-    } else {
-      T.lb.init(T.ti.n0, p.N, wave, lane);
+      if constexpr (B_KC) T.lb.init(b_row_of, p.ldb, wave, lane);
+      else T.lb.init(T.ti.n0, p.N, wave, lane);
     }
   };
 
@@ -461,14 +665,16 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   };
 
   int gs = 0;  // stream stage of the current tile's stage 0
-  auto slot_of = [&](int g) { return (uint32_t)((g % NS) * Cfg::STAGE_BYTES); };
+  auto slot_of = [&](int g) { return (uint32_t)((g % NS) * SLOT); };
   // DMA J of stage ls of tile T, into the ring slot of stream stage g; tok:
   // the gathered k-rows' tokens of that stage.
   auto dma_one = [&](const LoadTile& T, int ls, int g, const int (&tok)[GI][2], auto jc) {
     constexpr int J = decltype(jc)::value;
     const uint32_t st = lds0 + slot_of(g);
     const int k0 = T.kd0 + ls * BK;
-    if constexpr (J < Cfg::A_INSTR) {
+    if constexpr (WIDE) {
+      T.la.template issue1<J>(T.rsA, T.rsB, T.wide != 0, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+    } else if constexpr (J < Cfg::A_INSTR) {
       if constexpr (A_KC) T.la.template issue1<J>(T.rsA, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
       else if constexpr (GATH == GA_KROWS)
         T.la.template issue1_rows<J>(T.rsA, st, k0, T.kd_hi, lane < 32 ? tok[J][0] : tok[J][1], p.lda, wave);
@@ -482,16 +688,21 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
-  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+  // Fragments of substep ks from the slot at sa; a wide tile's B region
+  // starts after BM/2 A rows and its waves' first rows differ.
+  auto load_frags = [&](const char* sa, bool wide, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+    const bool w = WIDE && wide;
+    const char* sb = sa + (w ? Cfg::A_BYTES / 2 : Cfg::A_BYTES);
+    const int a0 = w ? a_row0w : a_row0, b0 = w ? b_row0w : b_row0;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
+      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else af[i] = t_frag<BM>(sa, a0 + i * 32, ks * 16, lane);
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
+      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else bfr[j] = t_frag<BN>(sb, b0 + j * 32, ks * 16, lane);
     }
   };
 
@@ -509,10 +720,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       acc[M / NI][M % NI] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
       constexpr int G = KSI * MI * NI + M;
-      static_for<0, D>([&](auto dc) {
+      static_for<0, DX>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
-        if constexpr ((DI * TOTM) / D == G) {
-          dma_one(T, ls, g, tok, dc);
+        if constexpr (dma_slot<D, TOTM>(DI) == G) {
+          if constexpr (DI < D) {
+            dma_one(T, ls, g, tok, dc);
+          } else if (T.wide) {  // a wide tile's fifth DMA
+            dma_one(T, ls, g, tok, dc);
+          }
           // keep the DMA between its MFMAs (MFMAs are not memory operations,
           // so the DMA's memory clobber alone would let them drift past it)
           __builtin_amdgcn_sched_barrier(0);
@@ -530,12 +745,14 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
   for (int s0 = 0; s0 < NS - 1; ++s0) {
     tokens(cur, s0, tok);
-    static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, tok, jc); });
+    static_for<0, DX>([&](auto jc) {
+      if (decltype(jc)::value < D || cur.wide) dma_one(cur, s0, s0, tok, jc);
+    });
   }
   wait_vmcnt<0>();  // stages 0 .. NS-2 have landed: a tile's stage 0 never waits
   lds_barrier();
   bf16x8 af[2][MI], bfr[2][NI];
-  load_frags(smem, smem + Cfg::A_BYTES, 0, af[0], bfr[0]);
+  load_frags(smem, cur.wide != 0, 0, af[0], bfr[0]);
 
   for (;;) {
 #pragma unroll
@@ -545,12 +762,12 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const int nk = cur.nk;
+    const bool wide_cur = cur.wide != 0, wide_next = nxt.wide != 0;
     // tokens of stage 0's DMAs (stream stage gs + NS - 1: this tile's stage NS - 1, or the next tile's)
     if constexpr (KGATH) tokens(NS - 1 >= nk ? nxt : cur, NS - 1 >= nk ? NS - 1 - nk : NS - 1, tok);
     for (int kt = 0; kt < nk; ++kt) {
       const int g = gs + kt;
       const char* sa = smem + slot_of(g);
-      const char* sb = sa + Cfg::A_BYTES;
       // the DMAs of this stage: stream stage g + NS - 1
       const int s = kt + NS - 1;
       const bool in_next = s >= nk;
@@ -564,13 +781,19 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       T.lb.select(in_next, nxt.lb, cur.lb);
       T.kd0 = in_next ? nxt.kd0 : cur.kd0;
       T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
+      T.wide = in_next ? nxt.wide : cur.wide;
       const int ls = in_next ? s - nk : s;
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
-        load_frags(sa, sb, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+        load_frags(sa, wide_cur, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
         substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok);
       });
-      if (kt > 0) wait_vmcnt<WAIT_N>();  // stream stage g + 1 has landed (this wave's share)
+      // stream stage g + 1 has landed (this wave's share): outstanding are
+      // only the DMAs this stage issued before here (one more from a wide tile)
+      if (kt > 0) {
+        if (WIDE && T.wide) wait_vmcnt<WAIT_W>();
+        else wait_vmcnt<WAIT_N>();
+      }
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
       if constexpr (KGATH) {
         // the next stage's DMAs (stream stage g + NS: within this tile or the
@@ -582,8 +805,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
           tokens(nn ? nxt : cur, nn ? s + 1 - nk : s + 1, tok_next);
         }
       }
-      const char* na = smem + slot_of(g + 1);
-      load_frags(na, na + Cfg::A_BYTES, 0, af[0], bfr[0]);
+      // stream stage g + 1: this tile's next stage, or the next tile's first
+      load_frags(smem + slot_of(g + 1), kt + 1 < nk ? wide_cur : wide_next, 0, af[0], bfr[0]);
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1, tok);
       if constexpr (KGATH) {
 #pragma unroll
@@ -599,7 +822,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     // next tile's stage 0) would hold every wave until its stores drained;
     // here the stores get a whole stage to drain before the next wait.
     wait_vmcnt<0>();
-    store_slabs<Cfg, Tout, GM, EPI>(acc, stage, cur.ti, p, wm, wn, lane);
+    // a wide tile's waves hold rows 0 .. BM/2 - 1 of column block `wave`
+    const bool ew = WIDE && cur.wide;
+    store_slabs<Cfg, Tout, GM, EPI, PACK>(acc, stage, cur.ti, p, ew ? 0 : wm, ew ? wave : wn, lane);
     gs += nk;
     ++kt_tile;
     if (tile_at(kt_tile) < 0) break;

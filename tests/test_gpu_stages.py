@@ -303,6 +303,49 @@ def test_gathered_rows_and_routing_weights(dtype, case):
         assert torch.equal(gw32.to(dtype), gwgu) and torch.equal(gd32.to(dtype), gdn)
 
 
+# Rows per expert chosen so that every short last m-tile case of the forward
+# GEMMs' wide (128 x 512) tiles occurs: last m-tiles of 1, 127, 128 rows (wide)
+# and 129, 255 rows (regular), experts of under 128 rows (nothing but a wide
+# tile), full experts (no last tile), an empty expert.
+WIDE_ROWS = [1, 127, 128, 129, 255, 256, 257, 383, 384, 385, 511, 640, 0, 64, 700, 900]
+
+
+@pytest.mark.parametrize("H, I", [(320, 640), (2048, 768), (768, 200)])
+def test_forward_gemms_short_last_tiles(H, I):
+    """gate_up (gathered and materialised rows) and down forward at row counts
+    that exercise the wide tiles, against fp64. H = 320 and 768: the down
+    GEMM's 512-column wide tiles end past N; I = 640 and 200: an odd count of
+    128-column gate_up tiles, so the last wide tile covers one (and a partial
+    one at I = 200)."""
+    say(f"short last tiles H={H} I={I}")
+    ops = _ops()
+    E, dt = len(WIDE_ROWS), torch.bfloat16
+    idx = torch.repeat_interleave(torch.arange(E), torch.tensor(WIDE_ROWS)).reshape(-1, 1)
+    idx = idx[torch.randperm(idx.shape[0], generator=gen(3))]
+    T = idx.shape[0]
+    g = gen(21)
+    x = torch.randn(T, H, generator=g).to(dt)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dt)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dt)
+    tw = torch.rand(T, 1, generator=g).to(dt)
+    counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
+    assert counts.cpu().tolist() == WIDE_ROWS
+    xp = ops.dispatch(x.to(DEV), inv, 1)
+    o = offs.cpu()
+    gu, mid = ops.gate_up_swiglu(xp, wgu.to(DEV), offs)
+    ref = ref_grouped(xp, wgu, o, trans_w=True)
+    check_close("gate_up", gu, ref, TOL[dt], MAX_ABS_FRAC[dt])
+    gq = gu.cpu().double()
+    check_close("mid", mid, silu64(gq[:, :I]) * gq[:, I:], TOL[dt], MAX_ABS_FRAC[dt])
+    stok, sw = ops.sort_rows(sp, tw.to(DEV), 1)
+    gu2, mid2 = ops.gate_up_swiglu(x.to(DEV), wgu.to(DEV), offs, stok, sw)
+    assert torch.equal(gu2, gu), "gathered rows give the materialised rows' pre-activations bit for bit"
+    w64 = sw.cpu().double().unsqueeze(1)
+    check_close("w * mid (gathered)", mid2, w64 * silu64(gq[:, :I]) * gq[:, I:], TOL[dt], MAX_ABS_FRAC[dt])
+    y = ops.down_proj(mid, wdn.to(DEV), offs)
+    check_close("y", y, ref_grouped(mid.cpu(), wdn, o, trans_w=True), TOL[dt], MAX_ABS_FRAC[dt])
+
+
 # ----------------------------------------------------------------- router
 
 
