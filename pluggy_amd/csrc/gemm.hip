@@ -90,12 +90,11 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
 // of an fp32 weight: 128 x 128 output blocks whose eight 64 x 96 wave tiles
 // hold the three pieces of the same 32 columns (the x stage is loaded once for
 // all three, and the epilogue sums them). From a bf16 weight (one piece):
-// 64 x 64 blocks of four 32 x 32 wave tiles. The two backward GEMMs: 128 x 128
-// blocks, the weight gradient's (a long reduction over tokens) with a 4-deep
-// ring.
+// 64 x 64 blocks of four 32 x 32 wave tiles. The weight gradient (a long
+// reduction over tokens, split into chunks): 128 x 128 blocks with a 4-deep
+// ring. (The input gradient runs on the persistent expert engine.)
 typedef DmaCfg<128, 384, 64, 96, 2, 64> DmaRouterLogits3;
 typedef DmaCfg<64, 64, 32, 32, 2> DmaRouterLogits;
-typedef DmaCfg<128, 128, 64, 64, 2> DmaRouterBwd;
 typedef DmaCfg<128, 128, 64, 64, 4> DmaRouterDw;
 
 // Router logits x . W^T in fp32 from bf16 x and npieces bf16 pieces of W
@@ -127,15 +126,16 @@ hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npie
 }
 
 // Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
-// (T, 3*ldl), w3t = [W_hi; W_hi; W_lo] (3*ldl, H).
+// (T, 3*ldl), w3t = [W_hi; W_hi; W_lo] (3*ldl, H). dx = dl3 . w3t has the
+// expert input-gradient GEMM's form (k-contiguous A, [k][n] B), so it runs on
+// the persistent engine as one group of T rows with reduction 3*ldl: its 256 x
+// 256 tiles move half the operand bytes of 128 x 128 ones (measured at config
+// 2: 24 -> 21.5 us; with one tile per CU the loads, MFMAs and the 33.5 MB of
+// stores follow each other rather than overlap).
 hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s) {
-  GemmParams p = zero_params();
-  p.A = dl3; p.lda = 3 * ldl;
-  p.B = w3t; p.ldb = H;  // B[k][n=h]
-  p.C = dx; p.ldc = H;
-  p.M = T; p.N = H; p.K = 3 * ldl;
-  p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)3 * ldl * H * 2;
-  return launch_gemm_dma<DmaRouterBwd, true, false, GM_NONE, EPI_STORE, bf16_t>(p, s);
+  if ((3 * ldl) % 2) return hipErrorInvalidValue;
+  return expert_gemm_persist<DmaExpert, bf16_t>(EG_GATE_UP_DGRAD, dl3, w3t, nullptr, dx, nullptr, nullptr, nullptr, T,
+                                                1, H, 3 * ldl / 2, ExpertGather(), num_cus(), s);
 }
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and

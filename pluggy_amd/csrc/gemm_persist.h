@@ -395,7 +395,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int groups = p.groups;
 
   // ---- tile list: GM_ROWS m-tiles follow the per-group row counts
-  for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs[g];
+  // offs null: one group of all M rows (a plain GEMM on the same engine)
+  for (int g = tid; g < groups; g += Cfg::NT) s_offs[g] = p.offs != nullptr ? p.offs[g] : p.M;
   __syncthreads();
   const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   const int mt_red = (p.M + BM - 1) / BM;  // GM_RED: m-tiles per group
