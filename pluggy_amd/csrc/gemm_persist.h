@@ -283,6 +283,45 @@ __device__ __forceinline__ int rows_scan_wide(const int32_t* offs, int groups, i
   return s_scan[groups];
 }
 
+// Tile `local` of an expert (a row group) with r regular m-tiles (the last
+// may be partial) and, with wide_tail, a short last m-tile covered by wide
+// tiles, over ntn n-tiles. The tiles go n-tile major, an n-tile's m-tiles side
+// by side so that they share its weight block in L2. An expert with more
+// m-tiles than n-tiles (its rows then outweigh its weights) goes in
+// super-blocks of mb m-tiles, mb x ntn tiles that run together on one XCD
+// (mb = the XCD's blocks / ntn): its rows are then staged from past L2 once
+// rather than once per n-tile, its weight blocks once per super-block. A wide
+// last m-tile's tiles follow each pair of n-tiles of the last super-block.
+__device__ __forceinline__ void rows_tile(int local, int r, bool wide_tail, int ntn, int mb, int& tn, int& mt,
+                                          int& wide) {
+  wide = 0;
+  const int k = (r > ntn && r > mb) ? (r - 1) / mb : 0;  // full super-blocks before the last
+  const int first = k * mb * ntn;
+  if (local < first) {
+    const int sb = local / (mb * ntn), q = local % (mb * ntn);
+    tn = q / mb;
+    mt = sb * mb + q % mb;
+    return;
+  }
+  local -= first;
+  const int h = r - k * mb, m0 = k * mb;  // the last super-block's regular m-tiles
+  if (wide_tail) {
+    const int q = local / (2 * h + 1), rr = local % (2 * h + 1);
+    const int npair = min(2, ntn - 2 * q);
+    if (rr == npair * h) {
+      wide = 1;
+      tn = q;
+      mt = m0 + h;
+    } else {
+      tn = 2 * q + rr / h;
+      mt = m0 + rr % h;
+    }
+  } else {
+    tn = local / h;
+    mt = m0 + local % h;
+  }
+}
+
 // GM_RED cost model: a tile of group g runs max(ceil(rows_g / BK), NS - 1)
 // k-stages plus an epilogue worth about kRedEpiStages stages (measured: a
 // 256x256 bf16 tile drains in ~3 stage times). s_cost[g] = cost of one tile of
@@ -417,6 +456,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int xcd = blockIdx.x & 7;
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
   const int bi = blockIdx.x >> 3;                  // this block's position on its XCD
+  const int mb = max(1, nb / ntiles_n);            // m-tiles per super-block of a row-heavy expert
   int cnt = 0, start = 0, tpg = 1, spos = 0;
   bool skew = false;
   if (total == 0) {
@@ -532,43 +572,23 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     if (t >= 0) {
       int tn = t % ntiles_n, slot = t / ntiles_n;
       if constexpr (WIDE) {
-        // the tiles of group g: its full m-tiles n-tile major, each pair of
-        // n-tiles followed by the wide tile under them when the last m-tile
-        // is short, else (a regular last m-tile) every n-tile's m-tiles in turn
         const int g = rows_group(s_scan, groups, t);
         const int lo = g == 0 ? 0 : s_offs[g - 1], rows = s_offs[g] - lo;
-        const int nfull = rows / BM, tail = rows % BM, local = t - s_scan[g];
-        int mt;
-        if (tail > 0 && tail <= BM / 2) {
-          const int q = local / (2 * nfull + 1), r = local % (2 * nfull + 1);
-          const int npair = min(2, ntiles_n - 2 * q);
-          if (r == npair * nfull) {
-            T.wide = 1;
-            tn = q;
-            mt = nfull;
-          } else {
-            tn = 2 * q + r / nfull;
-            mt = r % nfull;
-          }
-        } else {
-          const int ns = nfull + (tail > 0 ? 1 : 0);
-          tn = local / ns;
-          mt = local % ns;
-        }
-        T.wide = __builtin_amdgcn_readfirstlane(T.wide);
+        const int nfull = rows / BM, tail = rows % BM;
+        const bool wide_tail = tail > 0 && tail <= BM / 2;
+        int mt, wide;
+        rows_tile(t - s_scan[g], nfull + (tail > 0 && !wide_tail ? 1 : 0), wide_tail, ntiles_n, mb, tn, mt, wide);
+        T.wide = __builtin_amdgcn_readfirstlane(wide);
         T.ti.group = g; T.ti.m0 = lo + mt * BM; T.ti.m_end = s_offs[g];
         T.ti.k_lo = 0; T.ti.k_hi = p.K;
         b_base = B0 + (int64_t)g * p.strideB;
         b_bytes = p.b_bytes;
       } else if constexpr (GM == GM_ROWS) {
-        // An expert's tiles are ordered n-tile major, its m-tiles inner, so
-        // that the m-tiles sharing a weight block run next to each other.
         const int g = rows_group(s_scan, groups, slot);
-        const int ns = s_scan[g + 1] - s_scan[g], local = t - s_scan[g] * ntiles_n;
-        tn = local / ns;
-        slot = s_scan[g] + local % ns;
         const int lo = g == 0 ? 0 : s_offs[g - 1];
-        T.ti.group = g; T.ti.m0 = lo + (slot - s_scan[g]) * BM; T.ti.m_end = s_offs[g];
+        int mt, wide;
+        rows_tile(t - s_scan[g] * ntiles_n, s_scan[g + 1] - s_scan[g], false, ntiles_n, mb, tn, mt, wide);
+        T.ti.group = g; T.ti.m0 = lo + mt * BM; T.ti.m_end = s_offs[g];
         T.ti.k_lo = 0; T.ti.k_hi = p.K;
         b_base = B0 + (int64_t)g * p.strideB;
         b_bytes = p.b_bytes;
