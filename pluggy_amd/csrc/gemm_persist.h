@@ -456,7 +456,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int xcd = blockIdx.x & 7;
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
   const int bi = blockIdx.x >> 3;                  // this block's position on its XCD
-  const int mb = max(1, nb / ntiles_n);            // m-tiles per super-block of a row-heavy expert
+  // m-tiles per super-block of a row-heavy expert: the same for every block
+  // (the tile list must be), from the grid's blocks per XCD
+  const int mb = max(1, ((int)gridDim.x >> 3) / ntiles_n);
   int cnt = 0, start = 0, tpg = 1, spos = 0;
   bool skew = false;
   if (total == 0) {

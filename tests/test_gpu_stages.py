@@ -346,6 +346,44 @@ def test_forward_gemms_short_last_tiles(H, I):
     check_close("y", y, ref_grouped(mid.cpu(), wdn, o, trans_w=True), TOL[dt], MAX_ABS_FRAC[dt])
 
 
+def test_row_heavy_experts_super_blocks():
+    """Experts of 20 and 18 m-tiles against 2 n-tiles (H = 512, I = 256) take the
+    super-block tile order (16 m-tiles x 2 n-tiles, then the rest) in the
+    forward GEMMs and gate_up's input gradient; their last m-tiles hold 136
+    rows (regular) and 48 rows (wide in the forward GEMMs), and a 300-row
+    expert has a wide 44-row last tile. Against fp64."""
+    ops = _ops()
+    H, I, dt = 512, 256, torch.bfloat16
+    rows = [5000, 300, 4400]
+    say(f"super-blocks rows={rows} H={H} I={I}")
+    E = len(rows)
+    idx = torch.repeat_interleave(torch.arange(E), torch.tensor(rows)).reshape(-1, 1)
+    idx = idx[torch.randperm(idx.shape[0], generator=gen(5))]
+    T = idx.shape[0]
+    g = gen(23)
+    x = torch.randn(T, H, generator=g).to(dt)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dt)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dt)
+    counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
+    assert counts.cpu().tolist() == rows
+    xp = ops.dispatch(x.to(DEV), inv, 1)
+    o = offs.cpu()
+    gu, mid = ops.gate_up_swiglu(xp, wgu.to(DEV), offs)
+    check_close("gate_up", gu, ref_grouped(xp, wgu, o, trans_w=True), TOL[dt], MAX_ABS_FRAC[dt])
+    y = ops.down_proj(mid, wdn.to(DEV), offs)
+    check_close("y", y, ref_grouped(mid.cpu(), wdn, o, trans_w=True), TOL[dt], MAX_ABS_FRAC[dt])
+    gy = torch.randn(T, H, generator=gen(29)).to(dt)
+    ggu, gdn, _ = ops.down_proj_backward(gy.to(DEV), mid, gu, wdn.to(DEV), offs)
+    dmid = ref_grouped(gy, wdn, o, trans_w=False)
+    gq = gu.cpu().double()
+    gate, up = gq[:, :I], gq[:, I:]
+    s_ = torch.sigmoid(gate)
+    ref_ggu = torch.cat([dmid * up * s_ * (1 + gate * (1 - s_)), dmid * gate * s_], dim=1)
+    check_close("dgate_up", ggu, ref_ggu, TOL[dt], MAX_ABS_FRAC[dt])
+    gx = ops.gate_up_dgrad(ggu, wgu.to(DEV), offs)
+    check_close("dx_perm", gx, ref_grouped(ggu.cpu(), wgu, o, trans_w=False), TOL[dt], MAX_ABS_FRAC[dt])
+
+
 # ----------------------------------------------------------------- router
 
 
