@@ -12,8 +12,10 @@ fraction of the bf16 dense MFMA peak, per-stage HIP-event timings, the
 roofline of the dominant kernel, HBM GB/s of the row-movement kernels, the
 reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
 inputs, the MoE half-block with and without the fused RMSNorm / residual add
-(``neighbours``), and a CPU baseline (the restated reference CPU path) timed
-on this host.
+(``neighbours``), the other BASELINE.json configurations' steps (``decode``:
+config 5, ``config4``: skewed routing, ``config3``: the Qwen3-235B-A22B layer;
+``ep8_share``: one GPU's share at EP=8), and a CPU baseline (the restated
+reference CPU path) timed on this host.
 
 Two timed regions of --steps steps each: the first, bracketed by two events,
 gives ms_per_step and tokens/s; the second records an event pair around each
@@ -53,7 +55,8 @@ def parse_args():
     ap.add_argument("--cpu-tokens", type=int, default=256,
                     help="tokens of the CPU-baseline sample (0: the full workload)")
     ap.add_argument("--no-decode", action="store_true",
-                    help="skip the config-5 (decode, 64 tokens) forward leg and the EP=8 share leg")
+                    help="skip the legs after the config-2 line: config 5 (decode, 64 tokens), the EP=8 share, "
+                         "config 4 (skewed routing) and config 3 (the Qwen3-235B-A22B layer)")
     ap.add_argument("--copy-mib", type=int, default=256,
                     help="size of the device-to-device copy timed as the measured HBM reference (0: skip)")
     return ap.parse_args()
@@ -284,6 +287,68 @@ def decode_leg(dev, steps: int = 50, warmup: int = 5):
             "gate_up_fwd_GB/s": round(gu_b / (st["gate_up_fwd"]["mean_ms"] * 1e-3) / 1e9, 1),
             "down_fwd_GB/s": round(dn_b / (st["down_fwd"]["mean_ms"] * 1e-3) / 1e9, 1),
             "stages_ms": {n: round(v["mean_ms"], 4) for n, v in sorted(st.items(), key=lambda kv: -kv[1]["total_ms"])}}
+
+
+def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=None):
+    """Another BASELINE.json configuration's whole layer step (router, experts,
+    and the backward for fwd+bwd configs), timed like the headline line: HIP
+    events around `steps` steps after `warmup`. Config 4 reuses config 2's
+    tensors (`base_inp`: the same seeded draws) with its Zipf logit bias and
+    reports the routing's per-expert counts and its step time relative to
+    config 2's (`base_ms`)."""
+    import torch
+
+    import pluggy_amd
+    from pluggy_amd.workloads import CONFIGS, make_inputs, zipf_logit_bias
+
+    cfg = CONFIGS[cfg_id]
+    T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    if base_inp is not None:
+        inp = dict(base_inp)
+        if cfg.skew:
+            inp["logit_bias"] = zipf_logit_bias(E, cfg.skew).to(dev)
+    else:
+        inp = make_inputs(cfg, device=dev)
+    mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
+    with torch.no_grad():
+        mlp.router.weight.copy_(inp["router_weight"])
+    mlp.experts.gate_up_proj.data = inp["gate_up_proj"]
+    mlp.experts.down_proj.data = inp["down_proj"]
+    mlp.router.logit_bias = inp.get("logit_bias")
+    x = inp["x"].reshape(cfg.batch, T // cfg.batch, H)
+    gout = inp["grad_out"].reshape(x.shape) if cfg.backward else None
+
+    def step():
+        for p in mlp.parameters():
+            p.grad = None
+        xg = x.detach().requires_grad_(cfg.backward)
+        out = mlp(xg)
+        if cfg.backward:
+            out.backward(gout)
+
+    for _ in range(warmup):
+        step()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = cfg.gemm_flops() / (ms * 1e-3) / 1e12
+    out = {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if cfg.backward else 'fwd'} (T={T}, H={H}, E={E}, "
+                       f"K={K}, I={I})",
+           "ms_per_step": round(ms, 4), "tokens/s": round(T / (ms * 1e-3), 1), "steps": steps, "warmup": warmup,
+           "TFLOP/s": round(tflops, 1), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+    counts = mlp.router.last_stats.expert_counts
+    if cfg.skew:
+        out["expert_rows_min_max"] = [int(counts.min().item()), int(counts.max().item())]
+    if base_ms:
+        out["vs_config2_step"] = round(ms / base_ms, 3)
+    del mlp, inp
+    torch.cuda.empty_cache()
+    return out
 
 
 def ep_share_leg(dev, ep: int = 8, steps: int = 20, warmup: int = 5):
@@ -550,6 +615,8 @@ def main() -> int:
     if not args.no_decode and args.config == 2:
         result["decode"] = decode_leg(dev)
         result["ep8_share"] = ep_share_leg(dev)
+        result["config4"] = layer_leg(4, dev, args.steps, args.warmup, base_inp=inp, base_ms=ms)
+        result["config3"] = layer_leg(3, dev, min(args.steps, 10), 3)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
         if args.config == 2:
