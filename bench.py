@@ -14,8 +14,9 @@ reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
 inputs, the MoE half-block with and without the fused RMSNorm / residual add
 (``neighbours``), the other BASELINE.json configurations' steps (``decode``:
 config 5, ``config4``: skewed routing, ``config3``: the Qwen3-235B-A22B layer;
-``ep8_share``: one GPU's share at EP=8), and a CPU baseline (the restated
-reference CPU path) timed on this host.
+``ep8_share``: one GPU's share at EP=8), the forward expert GEMMs against
+hipBLASLt's batched product on equal experts (``vendor_gemm``), and a CPU
+baseline (the restated reference CPU path) timed on this host.
 
 Two timed regions of --steps steps each: the first, bracketed by two events,
 gives ms_per_step and tokens/s; the second records an event pair around each
@@ -351,6 +352,55 @@ def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=
     return out
 
 
+def vendor_gemm_leg(dev, launches: int = 20, warmup: int = 5):
+    """The forward expert GEMMs against the vendor library on the problem it can
+    run: 128 equal experts of 512 rows (config 2's shape with uniform routing),
+    where the grouped product is a plain batched one. Ours: gate_up with the
+    SwiGLU epilogue (it also writes the activation) and down, on the sorted rows;
+    the library's: torch.bmm (hipBLASLt) on the same operands, the weights
+    pre-transposed to contiguous (E, K, N) copies. Back-to-back launches timed
+    with HIP events."""
+    import torch
+
+    from pluggy_amd import ops
+
+    E, R, H, I = 128, 512, 2048, 768
+    g = torch.Generator().manual_seed(4)
+    xp = torch.randn(E * R, H, generator=g).to(torch.bfloat16).to(dev)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    offs = (torch.arange(1, E + 1, dtype=torch.int32) * R).to(dev)
+    wgu_t, wdn_t = wgu.transpose(1, 2).contiguous(), wdn.transpose(1, 2).contiguous()
+    _, mid = ops.gate_up_swiglu(xp, wgu, offs)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(launches):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / launches
+
+    xp3, mid3 = xp.view(E, R, H), mid.view(E, R, I)
+    out = {"problem": f"{E} experts x {R} rows, H={H}, I={I}, bf16", "launches": launches}
+    for name, ours, lib, flop in (
+            ("gate_up", lambda: ops.gate_up_swiglu(xp, wgu, offs), lambda: torch.bmm(xp3, wgu_t),
+             2.0 * E * R * H * 2 * I),
+            ("down", lambda: ops.down_proj(mid, wdn, offs), lambda: torch.bmm(mid3, wdn_t), 2.0 * E * R * I * H)):
+        t_ours, t_lib = timed(ours), timed(lib)
+        out[name] = {"ours_us": round(t_ours * 1e3, 1), "ours_TFLOP/s": round(flop / (t_ours * 1e-3) / 1e12, 1),
+                     "hipblaslt_bmm_us": round(t_lib * 1e3, 1),
+                     "hipblaslt_TFLOP/s": round(flop / (t_lib * 1e-3) / 1e12, 1),
+                     "speedup": round(t_lib / t_ours, 3)}
+    del xp, wgu, wdn, wgu_t, wdn_t, mid
+    torch.cuda.empty_cache()
+    return out
+
+
 def ep_share_leg(dev, ep: int = 8, steps: int = 20, warmup: int = 5):
     """One GPU's share of config 2 under expert parallelism over `ep` GPUs
     (design only in this build: no all-to-all runs). GPU 0 owns experts
@@ -617,6 +667,7 @@ def main() -> int:
         result["ep8_share"] = ep_share_leg(dev)
         result["config4"] = layer_leg(4, dev, args.steps, args.warmup, base_inp=inp, base_ms=ms)
         result["config3"] = layer_leg(3, dev, min(args.steps, 10), 3)
+        result["vendor_gemm"] = vendor_gemm_leg(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
         if args.config == 2:
