@@ -275,6 +275,29 @@ def decode_leg(dev, steps: int = 50, warmup: int = 5):
             for _ in range(steps):
                 mlp(x)
             torch.cuda.synchronize()
+        # the same forward captured in a HIP graph and replayed (a serving loop's form)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            mlp(x)
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(end) / steps
+        # one forward at a time, the host waiting for each (a decode loop's
+        # latency, host launch work included): eager calls, then graph replays
+        sync_ms = {}
+        for name, fn in (("eager", lambda: mlp(x)), ("graph", graph.replay)):
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+                torch.cuda.synchronize()
+            sync_ms[name] = (time.perf_counter() - t0) * 1e3 / steps
+        del graph
     st = timer.summary()
     hit = int((mlp.router.last_stats.expert_counts > 0).sum().item())
     es = 2
@@ -282,6 +305,8 @@ def decode_leg(dev, steps: int = 50, warmup: int = 5):
     gemm_ms = st["gate_up_fwd"]["mean_ms"] + st["down_fwd"]["mean_ms"]
     gbs = (gu_b + dn_b) / (gemm_ms * 1e-3) / 1e9
     return {"workload": f"{cfg.name} fwd (T={T}, layer as config 2)", "ms_per_forward": round(ms, 4),
+            "graph_ms_per_forward": round(graph_ms, 4),
+            "synced_ms_per_forward": {k: round(v, 4) for k, v in sync_ms.items()},
             "tokens/s": round(T / (ms * 1e-3), 1), "experts_hit": hit,
             "weight_bytes": gu_b + dn_b, "expert_gemms_ms": round(gemm_ms, 4),
             "weight_stream_GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
