@@ -1,12 +1,14 @@
-// Persistent grouped GEMM for the six expert GEMMs (GM_ROWS and GM_RED).
+// Persistent grouped GEMM for the six expert GEMMs (GM_ROWS and GM_RED) and
+// the router's input gradient (GM_ROWS, one group).
 //
-// One block per CU loops over the tiles of its XCD. The tile list is the
-// same as the non-persistent kernel's (n fastest within an m-tile, m-tiles of
-// a group consecutive); XCD x owns a contiguous share of it, and block i of
-// the XCD takes tiles i, i + nb, i + 2 nb, ... of that share (nb = blocks on
-// the XCD), so at any moment the XCD's CUs work on neighbouring tiles that
-// share operands in its L2. Per block, the expert offsets are read into LDS
-// and scanned once; a tile's group is then a binary search in LDS.
+// One block per CU loops over the tiles of its XCD. The tile list holds each
+// group's tiles together (GM_ROWS: n-tile major, see rows_tile; GM_RED: m-tile
+// major); XCD x owns a contiguous share of it, and block i of the XCD takes
+// tiles i, i + nb, i + 2 nb, ... of that share (nb = blocks on the XCD), so at
+// any moment the XCD's CUs work on neighbouring tiles that share operands in
+// its L2 (GM_RED under skew deals them differently, see below). Per block, the
+// expert offsets are read into LDS and scanned once; a tile's group is then a
+// binary search in LDS.
 //
 // The k loop is the ring pipeline of grouped_gemm_dma_kernel with a global
 // stage counter, so ring slots carry over from one tile to the next: stage
@@ -22,10 +24,8 @@ namespace pmoe {
 
 template <class Cfg>
 struct PersistLayout {
-  static constexpr int RING = Cfg::NS * Cfg::STAGE_BYTES;
-  static constexpr int SLAB = 16;                             // rows per epilogue slab
-  static constexpr int EPI_LD = Cfg::WN + 4;                  // floats per staged row
-  static constexpr int EPI_FLOATS = Cfg::NW * SLAB * EPI_LD;  // one slab per wave
+  static constexpr int SLAB = 16;             // rows per epilogue slab
+  static constexpr int EPI_LD = Cfg::WN + 4;  // floats per staged fp32 row
   static_assert(EPI_LD % 4 == 0, "16-byte aligned staging rows");
 };
 
