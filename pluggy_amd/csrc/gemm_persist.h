@@ -205,10 +205,11 @@ constexpr int dma_slot(int di) {
 // k-contiguous operands (the two forward GEMMs) therefore cover it with
 // BM / 2 x 2 BN tiles instead, each wave taking BM / 2 rows of its own WN
 // columns. A stage slot then holds BM / 2 A rows and 2 BN B rows (5 DMAs per
-// wave instead of 4, measured ~1.05-1.1 of a regular tile's stage) and half as
-// many tiles cover the tail. The slot is one array of 1 KB DMA rows: DMA J of
-// wave w fills rows 16 (w + 8 J) ..+15 in both shapes (A rows first, then B),
-// so only the source rows of DMAs 1-4 depend on the shape.
+// wave instead of 4; measured per block, a wide tile takes as long as a
+// regular one) and half as many tiles cover the tail. The slot is one array of
+// 64-byte rows (one 32-deep row piece each): DMA J of wave w fills rows
+// 16 (w + 8 J) ..+15 in both shapes (A rows first, then B), so only the source
+// rows of DMAs 1-4 depend on the shape.
 template <int NW, int BK>
 struct SlotDma {
   static_assert(BK == 32 && NW == 8, "wide tiles: 32-deep stages of 1 KB DMAs, 8 waves");
