@@ -4,8 +4,9 @@
   dtypes and loss, compared with the oracle's loop path (the reference CPU
   path) at the reference thresholds and at the north-star rel-L2 <= 1e-2.
 * The benchmark configurations at full size: routing and permutation bit-exact
-  (given the GPU's fp32 logits), values within tolerance on sampled token rows
-  and experts, bitwise run-to-run determinism.
+  (given the GPU's fp32 logits), router statistics against the oracle, every
+  output row, the whole input gradient and every weight gradient against fp64
+  truth with rel-L2 and max-abs bounds, bitwise run-to-run determinism.
 """
 
 from __future__ import annotations
