@@ -40,7 +40,7 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
 // 2 h2 and 2 h2 + 1: local row 8 (q - 2 h2) + 4 h + r. Each lane then reads 8
 // consecutive outputs and stores 16 bytes.
 //
-// The forward GEMMs (bf16 outputs) round in registers and stage packed: lanes 2c and 2c + 1 hold
+// bf16 outputs (all but the SwiGLU backward's) round in registers and stage packed: lanes 2c and 2c + 1 hold
 // columns 2c and 2c + 1 of the same four rows, so they swap half of their
 // values and each writes two dwords of (column 2c, 2c + 1) pairs, rows 0-1
 // from the even lane and rows 2-3 from the odd one. Packed rows are
@@ -48,7 +48,8 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
 // start 16 banks apart. The rounding is the v_cvt_pk_bf16_f32 the fp32 path
 // applies after staging, so both give the same bits; the packed staging
 // takes half the LDS of the fp32 one (measured: the same speed), which the
-// wide tiles' larger ring slots need.
+// wide tiles' larger ring slots and the four-slot ring of the backward GEMMs
+// need.
 template <class Cfg, bool PACK>
 struct EpiStage {
   static constexpr int ROW = PACK ? Cfg::WN / 2 + 8 : PersistLayout<Cfg>::EPI_LD;  // 4-byte words per staged row
@@ -412,8 +413,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr bool WIDE = GM == GM_ROWS && A_KC && B_KC && BM == 256 && BN == 256 && Cfg::WAVES_M == 2 &&
                         Cfg::WAVES_N == 4 && BK == 32 && NS == 3;
   constexpr int SLOT = Cfg::STAGE_BYTES + (WIDE ? Cfg::STAGE_BYTES / 4 : 0);  // ring slot bytes
-  // the forward GEMMs stage their bf16 outputs packed
-  constexpr bool PACK = sizeof(Tout) == 2 && GM == GM_ROWS && A_KC && B_KC && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
+  // bf16 outputs stage packed (the SwiGLU backward reads its fp32 accumulators back)
+  constexpr bool PACK = sizeof(Tout) == 2 && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
   static_assert(PACK || EPI != EPI_SWIGLU, "the SwiGLU forward stages packed bf16");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   __shared__ __attribute__((aligned(16))) float s_epi[EpiStage<Cfg, PACK>::WORDS];
   __shared__ int s_scan[1025];
   __shared__ int s_offs[1024];
-  __shared__ int s_order[1024];  // GM_RED under skew: groups by tile cost, descending
+  __shared__ unsigned short s_order[1024];  // GM_RED under skew: groups by tile cost, descending
   __shared__ int s_cmax;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -909,6 +910,32 @@ hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const
       if (kind == EG_DOWN_WGRAD)
         return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GA_KROWS>(p, num_cus, s);
       return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GB_KROWS>(p, num_cus, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+// gate_up dgrad and the bf16 weight gradients on a four-slot ring (Cfg::NS =
+// 4): a tile's first three stages are in flight before its predecessor's
+// epilogue stores, so the stores drain under two stages of MFMAs instead of
+// one before the first wait of the vector-memory counter, which also counts
+// them. Their bf16 outputs stage packed, which keeps the ring, the staging and
+// the group tables within the 160 KiB of LDS.
+template <class Cfg>
+hipError_t expert_gemm_persist_ring4(int kind, const bf16_t* A, const bf16_t* B, bf16_t* C, bf16_t* Cw,
+                                     const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
+                                     int num_cus, hipStream_t s) {
+  static_assert(Cfg::NS == 4, "four-slot ring");
+  GemmParams p = expert_params(kind, A, B, (const bf16_t*)nullptr, C, (bf16_t*)nullptr, offs, P, E, H, I, xg);
+  const bool gath = xg.index != nullptr;
+  switch (kind) {
+    case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
+    case EG_DOWN_WGRAD:
+    case EG_GATE_UP_WGRAD: {
+      p.C = Cw;
+      if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+      if (kind == EG_DOWN_WGRAD) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GA_KROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GB_KROWS>(p, num_cus, s);
     }
   }
   return hipErrorInvalidValue;
