@@ -23,12 +23,13 @@ template <> struct CfgFor<float> { typedef CfgF32 type; };
 // measurement at the Qwen3-30B-A3B shape over 128x128 .. 256x256 tilings,
 // 2..5 stages and 32/64-deep k tiles: larger tiles fetch fewer bytes per MFMA
 // through each CU's vector-memory path, which bounds the smaller ones. A
-// fourth stage does not speed up the k-loop, but it gives the epilogue stores
-// of the GEMMs with plain bf16 outputs (gate_up dgrad and the weight
-// gradients) a stage more to drain before the next tile's first wait
+// fourth stage does not speed up the k-loop, but it gives each tile's
+// epilogue stores a stage more to drain before the next tile's first wait
 // (measured at config 2, same bits: gate_up wgrad and down wgrad -1.7 %,
-// gate_up dgrad -0.5 %); the forward GEMMs' wide-tile slots and the SwiGLU
-// backward's fp32 staging leave no LDS for it.
+// gate_up fwd -1.2 % (more than its wide tiles gave on three stages), down
+// dgrad -0.8 %, gate_up dgrad -0.5 %), so every expert GEMM runs on four
+// stages except down fwd (+0.7 % there: it keeps its wide tiles, whose
+// larger slots fit only three) and fp32 weight gradients (no faster).
 typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaExpert;
 typedef DmaCfg<256, 256, 128, 64, 4, 32, 1> DmaExpert4;
 // Forward GEMMs of few-token (decode) batches, where each expert holds a few
@@ -65,10 +66,8 @@ hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C,
   if constexpr (sizeof(T) == 2) {
     if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
       return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
-    if constexpr (sizeof(Tw) == 2) {
-      if (kind == EG_GATE_UP_DGRAD || wgrad)
-        return expert_gemm_persist_ring4<DmaExpert4>(kind, A, B, C, Cw, offs, P, E, H, I, xg, num_cus(), s);
-    }
+    if (kind != EG_DOWN_FWD && !(wgrad && sizeof(Tw) == 4))
+      return expert_gemm_persist_ring4<DmaExpert4, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
     return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {
     static_assert(std::is_same<T, Tw>::value, "fp32 operands give fp32 weight gradients");

@@ -15,7 +15,9 @@
 // kt+NS-1 is issued during stage kt, and in a tile's last NS-1 stages that is
 // one of the next tile's first stages, so the next tile's data lands while
 // this tile finishes and stores. The epilogue stages accumulators through a
-// separate per-wave LDS region of 16-row slabs and never touches the ring.
+// separate per-wave LDS region of 16- or 8-row slabs and never touches the
+// ring. The ring has three slots (down fwd, with wide tiles; fp32 weight
+// gradients) or four (the other expert GEMMs: see expert_gemm_persist_ring4).
 #pragma once
 
 #include "gemm_dma.h"
@@ -24,7 +26,6 @@ namespace pmoe {
 
 template <class Cfg>
 struct PersistLayout {
-  static constexpr int SLAB = 16;             // rows per epilogue slab
   static constexpr int EPI_LD = Cfg::WN + 4;  // floats per staged fp32 row
   static_assert(EPI_LD % 4 == 0, "16-byte aligned staging rows");
 };
@@ -34,11 +35,12 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
 }
 
-// Epilogue through per-wave 16-row slabs: slab (i, h2) holds rows 16 h2 ..
-// 16 h2 + 15 of the wave's 32-row block i. In the MFMA 32x32 layout lane half
-// h holds rows 8 q + 4 h + r (r = 0..3) of a block, so slab h2 gathers q =
-// 2 h2 and 2 h2 + 1: local row 8 (q - 2 h2) + 4 h + r. Each lane then reads 8
-// consecutive outputs and stores 16 bytes.
+// Epilogue through per-wave slabs of SLAB rows (16, or 8 where fp32 staging
+// sits beside a four-slot ring): slab (i, s) holds rows SLAB s .. SLAB s +
+// SLAB - 1 of the wave's 32-row block i. In the MFMA 32x32 layout lane half h
+// holds rows 8 q + 4 h + r (r = 0..3) of a block, so slab s gathers the SLAB /
+// 8 values of q from (SLAB / 8) s on: local row 8 (q - (SLAB / 8) s) + 4 h + r.
+// Each lane then reads 8 consecutive outputs and stores 16 bytes.
 //
 // bf16 outputs (all but the SwiGLU backward's) round in registers and stage packed: lanes 2c and 2c + 1 hold
 // columns 2c and 2c + 1 of the same four rows, so they swap half of their
@@ -48,21 +50,22 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
 // start 16 banks apart. The rounding is the v_cvt_pk_bf16_f32 the fp32 path
 // applies after staging, so both give the same bits; the packed staging
 // takes half the LDS of the fp32 one (measured: the same speed), which the
-// wide tiles' larger ring slots and the four-slot ring of the backward GEMMs
-// need.
-template <class Cfg, bool PACK>
+// wide tiles' larger ring slots and the four-slot ring need.
+template <class Cfg, bool PACK, int SLAB>
 struct EpiStage {
   static constexpr int ROW = PACK ? Cfg::WN / 2 + 8 : PersistLayout<Cfg>::EPI_LD;  // 4-byte words per staged row
-  static constexpr int WORDS = Cfg::NW * PersistLayout<Cfg>::SLAB * ROW;
+  static constexpr int WORDS = Cfg::NW * SLAB * ROW;
+  static_assert(SLAB == 8 || SLAB == 16, "slabs of one or two MFMA row groups");
   static_assert(ROW % 4 == 0, "16-byte aligned staging rows");
 };
 
-template <class Cfg, typename Tout, int GM, int EPI, bool PACK>
+template <class Cfg, typename Tout, int GM, int EPI, bool PACK, int SLAB>
 __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI, WN = Cfg::WN;
-  constexpr int LD = PersistLayout<Cfg>::EPI_LD, SLAB = PersistLayout<Cfg>::SLAB;
-  constexpr int LDW = EpiStage<Cfg, PACK>::ROW;  // packed: words per staged row
+  constexpr int LD = PersistLayout<Cfg>::EPI_LD;
+  constexpr int LDW = EpiStage<Cfg, PACK, SLAB>::ROW;  // packed: words per staged row
+  constexpr int QPS = SLAB / 8, NSL = 32 / SLAB;         // row groups q per slab, slabs per 32-row block
   static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   Tout* C = reinterpret_cast<Tout*>(p.C);
@@ -72,14 +75,14 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
+    for (int hs = 0; hs < NSL; ++hs) {
       if constexpr (PACK) {
         const bool odd = lane & 1;
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
+        for (int qq = 0; qq < QPS; ++qq)
 #pragma unroll
           for (int j = 0; j < NI; ++j) {
-            const int q0 = 4 * (2 * h2 + qq);
+            const int q0 = 4 * (QPS * hs + qq);
             const float v0 = acc[i][j][q0], v1 = acc[i][j][q0 + 1], v2 = acc[i][j][q0 + 2], v3 = acc[i][j][q0 + 3];
             const float r0 = swap_lane_pair(odd ? v0 : v2), r1 = swap_lane_pair(odd ? v1 : v3);
             const uint32_t p0 = odd ? cvt_pk_bf16(r0, v2) : cvt_pk_bf16(v0, r0);
@@ -90,16 +93,16 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
           }
       } else {
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
+        for (int qq = 0; qq < QPS; ++qq)
 #pragma unroll
           for (int j = 0; j < NI; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              stage[(8 * qq + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * (2 * h2 + qq) + r];
+              stage[(8 * qq + 4 * half + r) * LD + j * 32 + col_l] = acc[i][j][4 * (QPS * hs + qq) + r];
       }
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): slab written
       asm volatile("" ::: "memory");
-      const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * h2;
+      const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * hs;
       if constexpr (EPI == EPI_SWIGLU) {
         constexpr int H2 = WN / 2, CPR = H2 / 8;
         bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
@@ -203,7 +206,7 @@ constexpr int dma_slot(int di) {
 
 // Wide tiles. An expert's last m-tile that holds at most BM / 2 rows would
 // stream a whole weight block for few rows; the row-grouped GEMMs with two
-// k-contiguous operands (the two forward GEMMs) therefore cover it with
+// k-contiguous operands on the three-slot ring (down fwd) therefore cover it with
 // BM / 2 x 2 BN tiles instead, each wave taking BM / 2 rows of its own WN
 // columns. A stage slot then holds BM / 2 A rows and 2 BN B rows (5 DMAs per
 // wave instead of 4; measured per block, a wide tile takes as long as a
@@ -407,9 +410,9 @@ template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI, int G
 __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
-  typedef PersistLayout<Cfg> L;
   // Wide tiles for short last m-tiles: the row-grouped GEMMs with two
-  // k-contiguous operands at the 256 x 256 shape (the forward GEMMs).
+  // k-contiguous operands at the 256 x 256 shape on the three-slot ring (down
+  // fwd; gate_up fwd runs faster on the four-slot ring without them).
   constexpr bool WIDE = GM == GM_ROWS && A_KC && B_KC && BM == 256 && BN == 256 && Cfg::WAVES_M == 2 &&
                         Cfg::WAVES_N == 4 && BK == 32 && NS == 3;
   constexpr int SLOT = Cfg::STAGE_BYTES + (WIDE ? Cfg::STAGE_BYTES / 4 : 0);  // ring slot bytes
@@ -424,7 +427,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
                 "gathers: A's rows in GM_ROWS, A's or B's k-rows in GM_RED");
 
   __shared__ __attribute__((aligned(1024))) char smem[NS * SLOT];
-  __shared__ __attribute__((aligned(16))) float s_epi[EpiStage<Cfg, PACK>::WORDS];
+  // fp32 staging beside a four-slot ring takes 8-row slabs (16 KiB less LDS)
+  constexpr int SLAB = (NS >= 4 && !PACK) ? 8 : 16;
+  __shared__ __attribute__((aligned(16))) float s_epi[EpiStage<Cfg, PACK, SLAB>::WORDS];
   __shared__ int s_scan[1025];
   __shared__ int s_offs[1024];
   __shared__ unsigned short s_order[1024];  // GM_RED under skew: groups by tile cost, descending
@@ -506,7 +511,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   if (tile_at(0) < 0) return;
 
   const uint32_t lds0 = lds_addr(smem);
-  float* stage = s_epi + wave * L::SLAB * EpiStage<Cfg, PACK>::ROW;
+  float* stage = s_epi + wave * SLAB * EpiStage<Cfg, PACK, SLAB>::ROW;
   const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
   typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA0;
@@ -849,7 +854,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     wait_vmcnt<0>();
     // a wide tile's waves hold rows 0 .. BM/2 - 1 of column block `wave`
     const bool ew = WIDE && cur.wide;
-    store_slabs<Cfg, Tout, GM, EPI, PACK>(acc, stage, cur.ti, p, ew ? 0 : wm, ew ? wave : wn, lane);
+    store_slabs<Cfg, Tout, GM, EPI, PACK, SLAB>(acc, stage, cur.ti, p, ew ? 0 : wm, ew ? wave : wn, lane);
     gs += nk;
     ++kt_tile;
     if (tile_at(kt_tile) < 0) break;
@@ -915,28 +920,39 @@ hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const
   return hipErrorInvalidValue;
 }
 
-// gate_up dgrad and the bf16 weight gradients on a four-slot ring (Cfg::NS =
-// 4): a tile's first three stages are in flight before its predecessor's
-// epilogue stores, so the stores drain under two stages of MFMAs instead of
-// one before the first wait of the vector-memory counter, which also counts
-// them. Their bf16 outputs stage packed, which keeps the ring, the staging and
-// the group tables within the 160 KiB of LDS.
-template <class Cfg>
-hipError_t expert_gemm_persist_ring4(int kind, const bf16_t* A, const bf16_t* B, bf16_t* C, bf16_t* Cw,
-                                     const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
-                                     int num_cus, hipStream_t s) {
+// The expert GEMMs on a four-slot ring (Cfg::NS = 4): all but down fwd,
+// which keeps the wide tiles of the three-slot ring, and the fp32 weight
+// gradients of fp32 master weights (no faster on four). A tile's first three
+// stages are in flight before its predecessor's epilogue stores, so the stores
+// drain under two stages of MFMAs instead of one before the first wait of the
+// vector-memory counter, which also counts them. bf16 outputs stage packed and
+// the SwiGLU backward's fp32 staging takes 8-row slabs, which keeps the ring,
+// the staging and the group tables within the 160 KiB of LDS.
+template <class Cfg, typename Tw>
+hipError_t expert_gemm_persist_ring4(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
+                                     bf16_t* C2, Tw* Cw, const int32_t* offs, int P, int E, int H, int I,
+                                     const ExpertGather& xg, int num_cus, hipStream_t s) {
   static_assert(Cfg::NS == 4, "four-slot ring");
-  GemmParams p = expert_params(kind, A, B, (const bf16_t*)nullptr, C, (bf16_t*)nullptr, offs, P, E, H, I, xg);
+  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
   const bool gath = xg.index != nullptr;
   switch (kind) {
+    case EG_GATE_UP_FWD:
+      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_DOWN_DGRAD:
+      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
     case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
     case EG_DOWN_WGRAD:
-    case EG_GATE_UP_WGRAD: {
-      p.C = Cw;
-      if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
-      if (kind == EG_DOWN_WGRAD) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GA_KROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GB_KROWS>(p, num_cus, s);
-    }
+    case EG_GATE_UP_WGRAD:
+      if constexpr (sizeof(Tw) == 2) {
+        p.C = Cw;
+        if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
+        if (kind == EG_DOWN_WGRAD)
+          return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GA_KROWS>(p, num_cus, s);
+        return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GB_KROWS>(p, num_cus, s);
+      }
+      break;
   }
   return hipErrorInvalidValue;
 }

@@ -303,8 +303,8 @@ def test_gathered_rows_and_routing_weights(dtype, case):
         assert torch.equal(gw32.to(dtype), gwgu) and torch.equal(gd32.to(dtype), gdn)
 
 
-# Rows per expert chosen so that every short last m-tile case of the forward
-# GEMMs' wide (128 x 512) tiles occurs: last m-tiles of 1, 127, 128 rows (wide)
+# Rows per expert chosen so that every short last m-tile case of down fwd's
+# wide (128 x 512) tiles occurs: last m-tiles of 1, 127, 128 rows (wide)
 # and 129, 255 rows (regular), experts of under 128 rows (nothing but a wide
 # tile), full experts (no last tile), an empty expert.
 WIDE_ROWS = [1, 127, 128, 129, 255, 256, 257, 383, 384, 385, 511, 640, 0, 64, 700, 900]
@@ -313,10 +313,11 @@ WIDE_ROWS = [1, 127, 128, 129, 255, 256, 257, 383, 384, 385, 511, 640, 0, 64, 70
 @pytest.mark.parametrize("H, I", [(320, 640), (2048, 768), (768, 200)])
 def test_forward_gemms_short_last_tiles(H, I):
     """gate_up (gathered and materialised rows) and down forward at row counts
-    that exercise the wide tiles, against fp64. H = 320 and 768: the down
-    GEMM's 512-column wide tiles end past N; I = 640 and 200: an odd count of
-    128-column gate_up tiles, so the last wide tile covers one (and a partial
-    one at I = 200)."""
+    whose experts end in short last m-tiles, against fp64: down fwd covers them
+    with wide tiles (H = 320 and 768: the 512-column wide tiles end past N),
+    gate_up fwd with the regular tiles of the four-slot ring (I = 640 and 200:
+    an odd count of 128-column activation tiles, the last one partial at
+    I = 200)."""
     say(f"short last tiles H={H} I={I}")
     ops = _ops()
     E, dt = len(WIDE_ROWS), torch.bfloat16
