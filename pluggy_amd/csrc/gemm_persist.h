@@ -522,13 +522,16 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
-  // of stage g. The gate_up forward at 32-deep stages spreads them over all
-  // KS substeps, the last of which runs after the stage's barrier (measured:
-  // -3 %); the other GEMMs keep them before the barrier (spread, the other
-  // row-grouped GEMMs lost 5-9 % and the weight gradients 3 %). With a double
-  // buffer (NS = 2) the next stage has only the current one to land in, so
-  // its DMAs go out in the first substep.
-  constexpr int SPREAD = NS == 2 ? 1 : ((EPI == EPI_SWIGLU && KS == 2) ? KS : KS - 1);
+  // of stage g. Spread over all KS substeps, the last of which runs after the
+  // stage's barrier: the gate_up forward (measured: -3 % on three slots, and
+  // keeping them before the barrier costs 7 % on four) and, on the four-slot
+  // ring, the other row-grouped GEMMs (down dgrad -1.6 %, gate_up dgrad
+  // -1.4 %; on three slots they lost 5-9 %). The weight gradients keep them
+  // before the barrier (spread: +1 % on four slots, +3 % on three). With a
+  // double buffer (NS = 2) the next stage has only the current one to land
+  // in, so its DMAs go out in the first substep.
+  constexpr int SPREAD =
+      NS == 2 ? 1 : (((EPI == EPI_SWIGLU && KS == 2) || (NS == 4 && GM == GM_ROWS)) ? KS : KS - 1);
   constexpr int TOTM = SPREAD * MI * NI;  // MFMA slots the DMAs are spread over (several may share one)
   static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
   // The stage's DMAs issued before its barrier. At that barrier stream stage
