@@ -18,20 +18,22 @@ template <> struct CfgFor<bf16_t> { typedef CfgBf16 type; };
 template <> struct CfgFor<float> { typedef CfgF32 type; };
 
 // bf16 expert GEMMs run on the persistent DMA engine: 256x256 blocks of eight
-// 128x64 wave tiles (two waves per SIMD, one block per CU) with a three-stage
-// ring of 32-deep k tiles (96 KiB of LDS) and 16-row epilogue slabs. Chosen by
-// measurement at the Qwen3-30B-A3B shape over 128x128 .. 256x256 tilings,
-// 2..5 stages and 32/64-deep k tiles: larger tiles fetch fewer bytes per MFMA
-// through each CU's vector-memory path, which bounds the smaller ones. A
-// fourth stage does not speed up the k-loop, but it gives each tile's
-// epilogue stores a stage more to drain before the next tile's first wait
-// (measured at config 2, same bits: gate_up wgrad and down wgrad -1.7 %,
-// gate_up fwd -1.2 % (more than its wide tiles gave on three stages), down
-// dgrad -0.8 %, gate_up dgrad -0.5 %), so every expert GEMM runs on four
-// stages except down fwd (+0.7 % there: it keeps its wide tiles, whose
-// larger slots fit only three) and fp32 weight gradients (no faster).
-typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaExpert;
-typedef DmaCfg<256, 256, 128, 64, 4, 32, 1> DmaExpert4;
+// 128x64 wave tiles (two waves per SIMD, one block per CU) with a four-stage
+// ring of 32-deep k tiles (128 KiB of LDS) and 16-row epilogue slabs (8-row
+// for fp32 staging). Chosen by measurement at the Qwen3-30B-A3B shape over
+// 128x128 .. 256x256 tilings, 2..5 stages and 32/64-deep k tiles: larger
+// tiles fetch fewer bytes per MFMA through each CU's vector-memory path, which
+// bounds the smaller ones. A fourth stage does not speed up the k-loop, but
+// the next tile's first three stages are then in flight before a tile's
+// epilogue stores, which drain while they are used (measured at config 2 against
+// three stages, same bits: down fwd -2.7 % (against three stages with
+// 128 x 512 tiles for short last m-tiles, which need 40 KiB slots), gate_up
+// wgrad and down wgrad -1.7 %, gate_up fwd -1.2 %, down dgrad -0.8 %, gate_up
+// dgrad -0.5 %; fp32 weight gradients the same).
+typedef DmaCfg<256, 256, 128, 64, 4, 32, 1> DmaExpert;
+// The router's input gradient: one tile per CU, so no epilogue to hide; the
+// three-stage ring as measured.
+typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaRouterDx;
 // Forward GEMMs of few-token (decode) batches, where each expert holds a few
 // rows and the GEMM is a stream of expert weights: 32-row x 128-column blocks
 // of four 32x32 wave tiles, 128-deep k stages (256-byte weight-row pieces, which
@@ -66,8 +68,6 @@ hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C,
   if constexpr (sizeof(T) == 2) {
     if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
       return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
-    if (kind != EG_DOWN_FWD && !(wgrad && sizeof(Tw) == 4))
-      return expert_gemm_persist_ring4<DmaExpert4, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
     return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {
     static_assert(std::is_same<T, Tw>::value, "fp32 operands give fp32 weight gradients");
@@ -143,8 +143,9 @@ hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npie
 // stores follow each other rather than overlap).
 hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s) {
   if ((3 * ldl) % 2) return hipErrorInvalidValue;
-  return expert_gemm_persist<DmaExpert, bf16_t>(EG_GATE_UP_DGRAD, dl3, w3t, nullptr, dx, nullptr, nullptr, nullptr, T,
-                                                1, H, 3 * ldl / 2, ExpertGather(), num_cus(), s);
+  const GemmParams p = expert_params<bf16_t>(EG_GATE_UP_DGRAD, dl3, w3t, nullptr, dx, nullptr, nullptr, T, 1, H,
+                                             3 * ldl / 2);
+  return launch_gemm_persist<DmaRouterDx, true, false, GM_ROWS, EPI_STORE>(p, num_cus(), s);
 }
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and

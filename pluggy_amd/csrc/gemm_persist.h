@@ -16,8 +16,8 @@
 // one of the next tile's first stages, so the next tile's data lands while
 // this tile finishes and stores. The epilogue stages accumulators through a
 // separate per-wave LDS region of 16- or 8-row slabs and never touches the
-// ring. The ring has three slots (down fwd, with wide tiles; fp32 weight
-// gradients) or four (the other expert GEMMs: see expert_gemm_persist_ring4).
+// ring. The expert GEMMs run on a four-slot ring, the router's input gradient
+// (one tile per CU) on three.
 #pragma once
 
 #include "gemm_dma.h"
@@ -50,7 +50,7 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
 // start 16 banks apart. The rounding is the v_cvt_pk_bf16_f32 the fp32 path
 // applies after staging, so both give the same bits; the packed staging
 // takes half the LDS of the fp32 one (measured: the same speed), which the
-// wide tiles' larger ring slots and the four-slot ring need.
+// four-slot ring needs.
 template <class Cfg, bool PACK, int SLAB>
 struct EpiStage {
   static constexpr int ROW = PACK ? Cfg::WN / 2 + 8 : PersistLayout<Cfg>::EPI_LD;  // 4-byte words per staged row
@@ -196,110 +196,21 @@ constexpr int dmas_before() {
   return c;
 }
 
-// Slot of DMA DI among the TOTM MFMA slots of a stage: the D DMAs of a
-// regular tile at (DI * TOTM) / D, the extra one of a wide tile at TOTM / (2 D)
-// (between the first two).
+// Slot of DMA DI among the TOTM MFMA slots of a stage: the D DMAs at
+// (DI * TOTM) / D.
 template <int D, int TOTM>
 constexpr int dma_slot(int di) {
-  return di < D ? (di * TOTM) / D : TOTM / (2 * D);
+  return (di * TOTM) / D;
 }
 
-// Wide tiles. An expert's last m-tile that holds at most BM / 2 rows would
-// stream a whole weight block for few rows; the row-grouped GEMMs with two
-// k-contiguous operands on the three-slot ring (down fwd) therefore cover it with
-// BM / 2 x 2 BN tiles instead, each wave taking BM / 2 rows of its own WN
-// columns. A stage slot then holds BM / 2 A rows and 2 BN B rows (5 DMAs per
-// wave instead of 4; measured per block, a wide tile takes as long as a
-// regular one) and half as many tiles cover the tail. The slot is one array of
-// 64-byte rows (one 32-deep row piece each): DMA J of wave w fills rows
-// 16 (w + 8 J) ..+15 in both shapes (A rows first, then B), so only the source
-// rows of DMAs 1-4 depend on the shape.
-template <int NW, int BK>
-struct SlotDma {
-  static_assert(BK == 32 && NW == 8, "wide tiles: 32-deep stages of 1 KB DMAs, 8 waves");
-  static constexpr int NJ = 5;
-  uint32_t off[NJ];  // bytes of (row, this lane's chunk) at k = 0, or kOOB
-  int kc;            // this lane's k offset within the stage (the same for every DMA at BK 32)
-
-  // From the A DMAs of a BM = 256 tile (rows 16 w, 128 + 16 w) and the B DMAs
-  // of a 512-row B tile (rows 16 w + 128 i): a regular tile takes A 0, A 1,
-  // B 0, B 1; a wide tile A 0, B 0 .. B 3.
-  __device__ __forceinline__ void set(const KcDma<256, NW, BK>& a, const KcDma<512, NW, BK>& b, bool wide) {
-    off[0] = a.rowoff[0];
-    off[1] = wide ? b.rowoff[0] : a.rowoff[1];
-    off[2] = wide ? b.rowoff[1] : b.rowoff[0];
-    off[3] = wide ? b.rowoff[2] : b.rowoff[1];
-    off[4] = b.rowoff[3];
-    kc = a.kc[0];
-  }
-  __device__ __forceinline__ void select(bool second, const SlotDma& y, const SlotDma& x) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) off[j] = second ? y.off[j] : x.off[j];
-    kc = second ? y.kc : x.kc;
-  }
-  // DMA J of the stage into the slot at LDS byte address `slot`: J = 0 reads
-  // A, J >= 2 reads B, J = 1 reads A in a regular tile and B in a wide one.
-  template <int J>
-  __device__ __forceinline__ void issue1(const BufRsrc& rsA, const BufRsrc& rsB, bool wide, uint32_t slot, int k0,
-                                         int k_hi, bool tail, int wave) const {
-    uint32_t v = off[J] + (uint32_t)(k0 * 2);
-    if (tail && k0 + kc >= k_hi) v = kOOB;
-    if constexpr (J == 1) {
-      BufRsrc rs;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(wide ? rsB[w] : rsA[w]);
-      dma16(rs, slot + (wave + J * NW) * 1024, v);
-    } else {
-      dma16(J == 0 ? rsA : rsB, slot + (wave + J * NW) * 1024, v);
-    }
-  }
-};
-
-// Stand-in for the B loader of the wide-tile kernels (SlotDma carries both operands).
-struct NoDma {
-  __device__ __forceinline__ void select(bool, const NoDma&, const NoDma&) {}
-};
-
-// Tiles of the row-grouped GEMMs with wide tiles: a group of `rows` rows has
-// rows / BM full m-tiles of ntn n-tiles each, plus a last m-tile of ntn
-// regular tiles, or of ceil(ntn / 2) wide tiles when it holds at most BM / 2
-// rows. s_scan[g] = tiles of the groups before g (inclusive scan to groups + 1
-// entries, computed by wave 0); returns the total.
-template <int BM>
-__device__ __forceinline__ int rows_scan_wide(const int32_t* offs, int groups, int ntn, int* s_scan) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  if (tid < 64) {
-    int carry = 0;
-    for (int base = 0; base < groups; base += 64) {
-      const int g = base + lane;
-      int tiles = 0;
-      if (g < groups) {
-        const int rows = offs[g] - (g == 0 ? 0 : offs[g - 1]);
-        const int tail = rows % BM;
-        tiles = (rows / BM) * ntn + (tail == 0 ? 0 : (tail <= BM / 2 ? (ntn + 1) / 2 : ntn));
-      }
-      const int inc = wave_incl_scan(tiles, lane) + carry;
-      if (g < groups) s_scan[g + 1] = inc;
-      carry = __shfl(inc, 63, kWave);
-    }
-    if (lane == 0) s_scan[0] = 0;
-  }
-  __syncthreads();
-  return s_scan[groups];
-}
-
-// Tile `local` of an expert (a row group) with r regular m-tiles (the last
-// may be partial) and, with wide_tail, a short last m-tile covered by wide
-// tiles, over ntn n-tiles. The tiles go n-tile major, an n-tile's m-tiles side
-// by side so that they share its weight block in L2. An expert with more
+// Tile `local` of an expert (a row group) with r m-tiles (the last may be
+// partial) over ntn n-tiles. The tiles go n-tile major, an n-tile's m-tiles
+// side by side so that they share its weight block in L2. An expert with more
 // m-tiles than n-tiles (its rows then outweigh its weights) goes in
 // super-blocks of mb m-tiles, mb x ntn tiles that run together on one XCD
 // (mb = the XCD's blocks / ntn): its rows are then staged from past L2 once
-// rather than once per n-tile, its weight blocks once per super-block. A wide
-// last m-tile's tiles follow each pair of n-tiles of the last super-block.
-__device__ __forceinline__ void rows_tile(int local, int r, bool wide_tail, int ntn, int mb, int& tn, int& mt,
-                                          int& wide) {
-  wide = 0;
+// rather than once per n-tile, its weight blocks once per super-block.
+__device__ __forceinline__ void rows_tile(int local, int r, int ntn, int mb, int& tn, int& mt) {
   const int k = (r > ntn && r > mb) ? (r - 1) / mb : 0;  // full super-blocks before the last
   const int first = k * mb * ntn;
   if (local < first) {
@@ -309,22 +220,9 @@ __device__ __forceinline__ void rows_tile(int local, int r, bool wide_tail, int 
     return;
   }
   local -= first;
-  const int h = r - k * mb, m0 = k * mb;  // the last super-block's regular m-tiles
-  if (wide_tail) {
-    const int q = local / (2 * h + 1), rr = local % (2 * h + 1);
-    const int npair = min(2, ntn - 2 * q);
-    if (rr == npair * h) {
-      wide = 1;
-      tn = q;
-      mt = m0 + h;
-    } else {
-      tn = 2 * q + rr / h;
-      mt = m0 + rr % h;
-    }
-  } else {
-    tn = local / h;
-    mt = m0 + local % h;
-  }
+  const int h = r - k * mb, m0 = k * mb;  // the last super-block's m-tiles
+  tn = local / h;
+  mt = m0 + local % h;
 }
 
 // GM_RED cost model: a tile of group g runs max(ceil(rows_g / BK), NS - 1)
@@ -410,12 +308,7 @@ template <class Cfg, typename Tout, bool A_KC, bool B_KC, int GM, int EPI, int G
 __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmParams p) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NW = Cfg::NW, NS = Cfg::NS, D = Cfg::D;
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
-  // Wide tiles for short last m-tiles: the row-grouped GEMMs with two
-  // k-contiguous operands at the 256 x 256 shape on the three-slot ring (down
-  // fwd; gate_up fwd runs faster on the four-slot ring without them).
-  constexpr bool WIDE = GM == GM_ROWS && A_KC && B_KC && BM == 256 && BN == 256 && Cfg::WAVES_M == 2 &&
-                        Cfg::WAVES_N == 4 && BK == 32 && NS == 3;
-  constexpr int SLOT = Cfg::STAGE_BYTES + (WIDE ? Cfg::STAGE_BYTES / 4 : 0);  // ring slot bytes
+  constexpr int SLOT = Cfg::STAGE_BYTES;  // ring slot bytes
   // bf16 outputs stage packed (the SwiGLU backward reads its fp32 accumulators back)
   constexpr bool PACK = sizeof(Tout) == 2 && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
   static_assert(PACK || EPI != EPI_SWIGLU, "the SwiGLU forward stages packed bf16");
@@ -447,8 +340,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   const int ntiles_n = (EPI == EPI_SWIGLU) ? (p.inter + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   const int mt_red = (p.M + BM - 1) / BM;  // GM_RED: m-tiles per group
   int total;
-  if constexpr (WIDE) total = rows_scan_wide<BM>(s_offs, groups, ntiles_n, s_scan);
-  else if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
+  if constexpr (GM == GM_ROWS) total = rows_scan<BM>(s_offs, groups, s_scan) * ntiles_n;
   else total = groups * mt_red * ntiles_n;
   // XCD x (blocks with blockIdx % 8 == x) takes a contiguous share of the tiles
   // and its blocks walk it in a stride of their count. GM_ROWS tiles all run
@@ -514,11 +406,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   float* stage = s_epi + wave * SLAB * EpiStage<Cfg, PACK, SLAB>::ROW;
   const bf16_t* A0 = reinterpret_cast<const bf16_t*>(p.A);
   const bf16_t* B0 = reinterpret_cast<const bf16_t*>(p.B);
-  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA0;
-  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB0;
-  // wide-tile kernels load both operands through one SlotDma
-  typedef typename std::conditional<WIDE, SlotDma<NW, BK>, LdA0>::type LdA;
-  typedef typename std::conditional<WIDE, NoDma, LdB0>::type LdB;
+  typedef typename std::conditional<A_KC, KcDma<BM, NW, BK>, TDma<BM, NW, BK>>::type LdA;
+  typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
@@ -540,14 +429,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // stay outstanding.
   constexpr int D_PRE = dmas_before<D, TOTM, (KS - 1) * MI * NI>();
   constexpr int WAIT_N = (NS - 3) * D + D_PRE;
-  // a wide tile's extra DMA sits at slot TOTM / (2 D); NS = 3 (see WIDE)
-  constexpr int DX = WIDE ? D + 1 : D;  // DMAs per stage of a wide tile
-  constexpr int WAIT_W = D_PRE + (dma_slot<D, TOTM>(D) < (KS - 1) * MI * NI ? 1 : 0);
   static_assert(WAIT_N >= 0 && D_PRE >= 1, "stage accounting");
-  static_assert(!WIDE || (D == 4 && Cfg::A_INSTR == 2 && TOTM >= 2 * D), "wide tiles: 4 + 1 DMAs per wave");
   const int a_row0 = wm * Cfg::WM, b_row0 = wn * Cfg::WN;
-  // a wide tile's waves all take rows 0 .. BM/2 - 1, wave w the B rows (columns) of block w
-  const int a_row0w = 0, b_row0w = wave * Cfg::WN;
 
   // k-row gathers: the gathered [k][r] operand's DMA instructions per stage,
   // each covering KPI = 2 k-rows (lanes 0-31 the first, 32-63 the second).
@@ -566,8 +449,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     LdA la;
     LdB lb;
     int nk, kd0, kd_hi;
-    int klo;   // first reduction index of the tile (wave-uniform; k-row gathers)
-    int wide;  // a wide tile (WIDE kernels; wave-uniform)
+    int klo;  // first reduction index of the tile (wave-uniform; k-row gathers)
   };
   // Tile t of the list (t < 0: past the block's last tile; its descriptors
   // are empty, so every DMA reads zeros).
@@ -577,29 +459,16 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     T.kd0 = 0;
     T.kd_hi = 0;
     T.klo = 0;
-    T.wide = 0;
     const bf16_t* a_base = A0;
     const bf16_t* b_base = B0;
     uint64_t a_bytes = 0, b_bytes = 0;
     if (t >= 0) {
       int tn = t % ntiles_n, slot = t / ntiles_n;
-      if constexpr (WIDE) {
-        const int g = rows_group(s_scan, groups, t);
-        const int lo = g == 0 ? 0 : s_offs[g - 1], rows = s_offs[g] - lo;
-        const int nfull = rows / BM, tail = rows % BM;
-        const bool wide_tail = tail > 0 && tail <= BM / 2;
-        int mt, wide;
-        rows_tile(t - s_scan[g], nfull + (tail > 0 && !wide_tail ? 1 : 0), wide_tail, ntiles_n, mb, tn, mt, wide);
-        T.wide = __builtin_amdgcn_readfirstlane(wide);
-        T.ti.group = g; T.ti.m0 = lo + mt * BM; T.ti.m_end = s_offs[g];
-        T.ti.k_lo = 0; T.ti.k_hi = p.K;
-        b_base = B0 + (int64_t)g * p.strideB;
-        b_bytes = p.b_bytes;
-      } else if constexpr (GM == GM_ROWS) {
+      if constexpr (GM == GM_ROWS) {
         const int g = rows_group(s_scan, groups, slot);
         const int lo = g == 0 ? 0 : s_offs[g - 1];
-        int mt, wide;
-        rows_tile(t - s_scan[g] * ntiles_n, s_scan[g + 1] - s_scan[g], false, ntiles_n, mb, tn, mt, wide);
+        int mt;
+        rows_tile(t - s_scan[g] * ntiles_n, s_scan[g + 1] - s_scan[g], ntiles_n, mb, tn, mt);
         T.ti.group = g; T.ti.m0 = lo + mt * BM; T.ti.m_end = s_offs[g];
         T.ti.k_lo = 0; T.ti.k_hi = p.K;
         b_base = B0 + (int64_t)g * p.strideB;
@@ -610,7 +479,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         T.ti.k_lo = g == 0 ? 0 : s_offs[g - 1];
         T.ti.k_hi = s_offs[g];
       }
-      T.ti.n0 = ((EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN) * (T.wide ? 2 : 1);
+      T.ti.n0 = (EPI == EPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
       if constexpr (A_KC) {
         if constexpr (GATH == GA_ROWS) {
           a_bytes = p.a_bytes;  // the whole gathered storage
@@ -653,29 +522,17 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         return n0 + c < N ? n0 + c : -1;
       }
     };
-    if constexpr (WIDE) {
-      KcDma<BM, NW, BK> la;
-      KcDma<2 * BN, NW, BK> lb;
+    if constexpr (A_KC) {
       const int rows = T.ti.m_end - T.ti.m0;
       if constexpr (GATH == GA_ROWS)
-        la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
+        T.la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
       else
-        la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
-      lb.init(b_row_of, p.ldb, wave, lane);
-      T.la.set(la, lb, T.wide != 0);
+        T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
     } else {
-      if constexpr (A_KC) {
-        const int rows = T.ti.m_end - T.ti.m0;
-        if constexpr (GATH == GA_ROWS)
-          T.la.init_gather(p.a_index, p.n_index, __builtin_amdgcn_readfirstlane(T.ti.m0), rows, p.lda, wave, lane);
-        else
-          T.la.init([&](int r) { return r < rows ? r : -1; }, p.lda, wave, lane);
-      } else {
-        T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
-      }
-      if constexpr (B_KC) T.lb.init(b_row_of, p.ldb, wave, lane);
-      else T.lb.init(T.ti.n0, p.N, wave, lane);
+      T.la.init(T.ti.m0, T.ti.m_end, wave, lane);
     }
+    if constexpr (B_KC) T.lb.init(b_row_of, p.ldb, wave, lane);
+    else T.lb.init(T.ti.n0, p.N, wave, lane);
   };
 
   // Tokens of the gathered k-rows of tile-local stage ls of T: instruction i
@@ -705,9 +562,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     constexpr int J = decltype(jc)::value;
     const uint32_t st = lds0 + slot_of(g);
     const int k0 = T.kd0 + ls * BK;
-    if constexpr (WIDE) {
-      T.la.template issue1<J>(T.rsA, T.rsB, T.wide != 0, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
-    } else if constexpr (J < Cfg::A_INSTR) {
+    if constexpr (J < Cfg::A_INSTR) {
       if constexpr (A_KC) T.la.template issue1<J>(T.rsA, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
       else if constexpr (GATH == GA_KROWS)
         T.la.template issue1_rows<J>(T.rsA, st, k0, T.kd_hi, lane < 32 ? tok[J][0] : tok[J][1], p.lda, wave);
@@ -721,21 +576,18 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
-  // Fragments of substep ks from the slot at sa; a wide tile's B region
-  // starts after BM/2 A rows and its waves' first rows differ.
-  auto load_frags = [&](const char* sa, bool wide, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
-    const bool w = WIDE && wide;
-    const char* sb = sa + (w ? Cfg::A_BYTES / 2 : Cfg::A_BYTES);
-    const int a0 = w ? a_row0w : a_row0, b0 = w ? b_row0w : b_row0;
+  // Fragments of substep ks from the slot at sa (A rows, then B rows).
+  auto load_frags = [&](const char* sa, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+    const char* sb = sa + Cfg::A_BYTES;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else af[i] = t_frag<BM>(sa, a0 + i * 32, ks * 16, lane);
+      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else bfr[j] = t_frag<BN>(sb, b0 + j * 32, ks * 16, lane);
+      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
     }
   };
 
@@ -753,14 +605,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       acc[M / NI][M % NI] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
       constexpr int G = KSI * MI * NI + M;
-      static_for<0, DX>([&](auto dc) {
+      static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
         if constexpr (dma_slot<D, TOTM>(DI) == G) {
-          if constexpr (DI < D) {
-            dma_one(T, ls, g, tok, dc);
-          } else if (T.wide) {  // a wide tile's fifth DMA
-            dma_one(T, ls, g, tok, dc);
-          }
+          dma_one(T, ls, g, tok, dc);
           // keep the DMA between its MFMAs (MFMAs are not memory operations,
           // so the DMA's memory clobber alone would let them drift past it)
           __builtin_amdgcn_sched_barrier(0);
@@ -778,14 +626,12 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // prologue: stream stages 0 .. NS-2 (all in the first tile: nk >= NS - 1)
   for (int s0 = 0; s0 < NS - 1; ++s0) {
     tokens(cur, s0, tok);
-    static_for<0, DX>([&](auto jc) {
-      if (decltype(jc)::value < D || cur.wide) dma_one(cur, s0, s0, tok, jc);
-    });
+    static_for<0, D>([&](auto jc) { dma_one(cur, s0, s0, tok, jc); });
   }
   wait_vmcnt<0>();  // stages 0 .. NS-2 have landed: a tile's stage 0 never waits
   lds_barrier();
   bf16x8 af[2][MI], bfr[2][NI];
-  load_frags(smem, cur.wide != 0, 0, af[0], bfr[0]);
+  load_frags(smem, 0, af[0], bfr[0]);
 
   for (;;) {
 #pragma unroll
@@ -795,7 +641,6 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const int nk = cur.nk;
-    const bool wide_cur = cur.wide != 0, wide_next = nxt.wide != 0;
     // tokens of stage 0's DMAs (stream stage gs + NS - 1: this tile's stage NS - 1, or the next tile's)
     if constexpr (KGATH) tokens(NS - 1 >= nk ? nxt : cur, NS - 1 >= nk ? NS - 1 - nk : NS - 1, tok);
     for (int kt = 0; kt < nk; ++kt) {
@@ -814,19 +659,16 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       T.lb.select(in_next, nxt.lb, cur.lb);
       T.kd0 = in_next ? nxt.kd0 : cur.kd0;
       T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
-      T.wide = in_next ? nxt.wide : cur.wide;
       const int ls = in_next ? s - nk : s;
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
-        load_frags(sa, wide_cur, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+        load_frags(sa, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
         substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok);
       });
       // stream stage g + 1 has landed (this wave's share): outstanding are
-      // only the DMAs this stage issued before here (one more from a wide tile)
-      if (kt > 0) {
-        if (WIDE && T.wide) wait_vmcnt<WAIT_W>();
-        else wait_vmcnt<WAIT_N>();
-      }
+      // only the full stages g + 2 .. g + NS - 2 and the DMAs this stage
+      // issued before here
+      if (kt > 0) wait_vmcnt<WAIT_N>();
       lds_barrier();               // ... every wave's share; every wave is done with slot g but for registers
       if constexpr (KGATH) {
         // the next stage's DMAs (stream stage g + NS: within this tile or the
@@ -839,7 +681,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         }
       }
       // stream stage g + 1: this tile's next stage, or the next tile's first
-      load_frags(smem + slot_of(g + 1), kt + 1 < nk ? wide_cur : wide_next, 0, af[0], bfr[0]);
+      load_frags(smem + slot_of(g + 1), 0, af[0], bfr[0]);
       substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1, tok);
       if constexpr (KGATH) {
 #pragma unroll
@@ -855,9 +697,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     // next tile's stage 0) would hold every wave until its stores drained;
     // here the stores get a whole stage to drain before the next wait.
     wait_vmcnt<0>();
-    // a wide tile's waves hold rows 0 .. BM/2 - 1 of column block `wave`
-    const bool ew = WIDE && cur.wide;
-    store_slabs<Cfg, Tout, GM, EPI, PACK, SLAB>(acc, stage, cur.ti, p, ew ? 0 : wm, ew ? wave : wn, lane);
+    store_slabs<Cfg, Tout, GM, EPI, PACK, SLAB>(acc, stage, cur.ti, p, wm, wn, lane);
     gs += nk;
     ++kt_tile;
     if (tile_at(kt_tile) < 0) break;
@@ -919,43 +759,6 @@ hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const
         return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GA_KROWS>(p, num_cus, s);
       return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GB_KROWS>(p, num_cus, s);
     }
-  }
-  return hipErrorInvalidValue;
-}
-
-// The expert GEMMs on a four-slot ring (Cfg::NS = 4): all but down fwd,
-// which keeps the wide tiles of the three-slot ring, and the fp32 weight
-// gradients of fp32 master weights (no faster on four). A tile's first three
-// stages are in flight before its predecessor's epilogue stores, so the stores
-// drain under two stages of MFMAs instead of one before the first wait of the
-// vector-memory counter, which also counts them. bf16 outputs stage packed and
-// the SwiGLU backward's fp32 staging takes 8-row slabs, which keeps the ring,
-// the staging and the group tables within the 160 KiB of LDS.
-template <class Cfg, typename Tw>
-hipError_t expert_gemm_persist_ring4(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
-                                     bf16_t* C2, Tw* Cw, const int32_t* offs, int P, int E, int H, int I,
-                                     const ExpertGather& xg, int num_cus, hipStream_t s) {
-  static_assert(Cfg::NS == 4, "four-slot ring");
-  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
-  const bool gath = xg.index != nullptr;
-  switch (kind) {
-    case EG_GATE_UP_FWD:
-      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
-    case EG_DOWN_DGRAD:
-      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
-    case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
-    case EG_DOWN_WGRAD:
-    case EG_GATE_UP_WGRAD:
-      if constexpr (sizeof(Tw) == 2) {
-        p.C = Cw;
-        if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE>(p, num_cus, s);
-        if (kind == EG_DOWN_WGRAD)
-          return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GA_KROWS>(p, num_cus, s);
-        return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, bf16_t, GB_KROWS>(p, num_cus, s);
-      }
-      break;
   }
   return hipErrorInvalidValue;
 }

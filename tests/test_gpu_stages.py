@@ -303,25 +303,22 @@ def test_gathered_rows_and_routing_weights(dtype, case):
         assert torch.equal(gw32.to(dtype), gwgu) and torch.equal(gd32.to(dtype), gdn)
 
 
-# Rows per expert chosen so that every short last m-tile case of down fwd's
-# wide (128 x 512) tiles occurs: last m-tiles of 1, 127, 128 rows (wide)
-# and 129, 255 rows (regular), experts of under 128 rows (nothing but a wide
-# tile), full experts (no last tile), an empty expert.
-WIDE_ROWS = [1, 127, 128, 129, 255, 256, 257, 383, 384, 385, 511, 640, 0, 64, 700, 900]
+# Rows per expert with every kind of short last m-tile (1, 127, 128, 129 and
+# 255 rows of a 256-row tile), experts of under 128 rows (nothing but a short
+# tile), full experts (no last tile) and an empty expert.
+SHORT_ROWS = [1, 127, 128, 129, 255, 256, 257, 383, 384, 385, 511, 640, 0, 64, 700, 900]
 
 
 @pytest.mark.parametrize("H, I", [(320, 640), (2048, 768), (768, 200)])
 def test_forward_gemms_short_last_tiles(H, I):
     """gate_up (gathered and materialised rows) and down forward at row counts
-    whose experts end in short last m-tiles, against fp64: down fwd covers them
-    with wide tiles (H = 320 and 768: the 512-column wide tiles end past N),
-    gate_up fwd with the regular tiles of the four-slot ring (I = 640 and 200:
-    an odd count of 128-column activation tiles, the last one partial at
-    I = 200)."""
+    whose experts end in short last m-tiles, against fp64. H = 320 and 768: the
+    down GEMM's last 256-column tile ends past N; I = 640 and 200: an odd count
+    of 128-column activation tiles, the last one partial at I = 200."""
     say(f"short last tiles H={H} I={I}")
     ops = _ops()
-    E, dt = len(WIDE_ROWS), torch.bfloat16
-    idx = torch.repeat_interleave(torch.arange(E), torch.tensor(WIDE_ROWS)).reshape(-1, 1)
+    E, dt = len(SHORT_ROWS), torch.bfloat16
+    idx = torch.repeat_interleave(torch.arange(E), torch.tensor(SHORT_ROWS)).reshape(-1, 1)
     idx = idx[torch.randperm(idx.shape[0], generator=gen(3))]
     T = idx.shape[0]
     g = gen(21)
@@ -330,7 +327,7 @@ def test_forward_gemms_short_last_tiles(H, I):
     wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dt)
     tw = torch.rand(T, 1, generator=g).to(dt)
     counts, offs, sp, inv = ops.permute(idx.to(DEV), E)
-    assert counts.cpu().tolist() == WIDE_ROWS
+    assert counts.cpu().tolist() == SHORT_ROWS
     xp = ops.dispatch(x.to(DEV), inv, 1)
     o = offs.cpu()
     gu, mid = ops.gate_up_swiglu(xp, wgu.to(DEV), offs)
