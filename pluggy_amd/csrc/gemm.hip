@@ -25,11 +25,12 @@ template <> struct CfgFor<float> { typedef CfgF32 type; };
 // tiles fetch fewer bytes per MFMA through each CU's vector-memory path, which
 // bounds the smaller ones. A fourth stage does not speed up the k-loop, but
 // the next tile's first three stages are then in flight before a tile's
-// epilogue stores, which drain while they are used (measured at config 2 against
-// three stages, same bits: down fwd -2.7 % (against three stages with
-// 128 x 512 tiles for short last m-tiles, which need 40 KiB slots), gate_up
-// wgrad and down wgrad -1.7 %, gate_up fwd -1.2 %, down dgrad -0.8 %, gate_up
-// dgrad -0.5 %; fp32 weight gradients the same).
+// epilogue stores, which drain while they are used. Against three stages
+// (with 128 x 512 tiles covering short last m-tiles in the forward GEMMs,
+// whose 40 KiB slots fit only three), same bits, alternating runs on one box:
+// the config-2 step -0.4 to -0.8 % on two boxes (down dgrad -2 %, the other
+// GEMMs within +-1 %), config 3 -0.8 %, config 4 +0.5 % (its many short last
+// m-tiles: gate_up fwd +3 %, down fwd -5 %); fp32 weight gradients the same.
 typedef DmaCfg<256, 256, 128, 64, 4, 32, 1> DmaExpert;
 // The router's input gradient: one tile per CU, so no epilogue to hide; the
 // three-stage ring as measured.

@@ -415,8 +415,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // stage's barrier: the gate_up forward (measured: -3 % on three slots, and
   // keeping them before the barrier costs 7 % on four) and, on the four-slot
   // ring, the other row-grouped GEMMs (down dgrad -1.6 %, gate_up dgrad
-  // -1.4 %; on three slots they lost 5-9 %). The weight gradients keep them
-  // before the barrier (spread: +1 % on four slots, +3 % on three). With a
+  // -1.4 % on one box; on three slots they lost 5-9 %). The weight gradients
+  // keep them before the barrier (spread: +1 % on four slots, +3 % on three). With a
   // double buffer (NS = 2) the next stage has only the current one to land
   // in, so its DMAs go out in the first substep.
   constexpr int SPREAD =
