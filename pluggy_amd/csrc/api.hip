@@ -68,13 +68,11 @@ constexpr int64_t kMaxIndex = 0x7fffffffLL;
 // wave): 16 when there are enough rows to fill the GPU, else one row per wave.
 int router_rows(int64_t T) { return T >= 2048 ? 16 : 4; }
 int64_t router_blocks(int64_t T) { return (T + router_rows(T) - 1) / router_rows(T); }
-// Split-K planes of the bf16-pieces router logits GEMM: its 64-row m-tiles
-// times three piece n-tiles fall short of the 256 CUs when tokens are few
-// (decode), so the reduction over H is split (chunks of at least 256) until
-// there are about 256 tiles; the top-k kernel sums the planes in order.
-// Split of the logits GEMM's reduction over H: enough blocks to cover the
-// GPU's 256 CUs. pieces: the three-piece tiles of an fp32 weight (128 x 128
-// outputs) rather than the 64 x 64 tiles of a bf16 weight.
+// Split-K planes of the router logits GEMM: its output tiles (128 x 128 for
+// the three bf16 pieces of an fp32 weight, 64 x 64 for a bf16 weight) fall
+// short of the 256 CUs unless tokens are many, so the reduction over H is
+// split (chunks of at least 256) until there are about 256 blocks; the top-k
+// kernel sums the planes in order.
 int router_logit_splits(int64_t T, int64_t H, int64_t E, bool pieces) {
   if (T <= 0) return 1;
   const int64_t tiles = pieces ? ((T + 127) / 128) * ((E + 127) / 128) : ((T + 63) / 64) * ((E + 63) / 64);
