@@ -42,10 +42,11 @@ __device__ __forceinline__ float swap_lane_pair(float v) {
 // 8 values of q from (SLAB / 8) s on: local row 8 (q - (SLAB / 8) s) + 4 h + r.
 // Each lane then reads 8 consecutive outputs and stores 16 bytes.
 //
-// bf16 outputs (all but the SwiGLU backward's) round in registers and stage packed: lanes 2c and 2c + 1 hold
-// columns 2c and 2c + 1 of the same four rows, so they swap half of their
-// values and each writes two dwords of (column 2c, 2c + 1) pairs, rows 0-1
-// from the even lane and rows 2-3 from the odd one. Packed rows are
+// bf16 outputs (all but the SwiGLU backward's) round in registers and stage
+// packed: lanes 2c and 2c + 1 hold columns 2c and 2c + 1 of the same four
+// rows, so they swap half of their values and each writes two dwords of
+// (column 2c, 2c + 1) pairs, rows 0-1 from the even lane and rows 2-3 from
+// the odd one. Packed rows are
 // WN / 2 + 8 dwords apart, so the four rows one write instruction touches
 // start 16 banks apart. The rounding is the v_cvt_pk_bf16_f32 the fp32 path
 // applies after staging, so both give the same bits; the packed staging
