@@ -32,6 +32,13 @@ template <> struct CfgFor<float> { typedef CfgF32 type; };
 // GEMMs within +-1 %), config 3 -0.8 %, config 4 +0.5 % (its many short last
 // m-tiles: gate_up fwd +3 %, down fwd -5 %); fp32 weight gradients the same.
 typedef DmaCfg<256, 256, 128, 64, 4, 32, 1> DmaExpert;
+// Row-grouped GEMMs whose 256-row tiles would leave whole rounds of the
+// persistent walk idle: 128 x 256 blocks of eight 64 x 64 wave tiles (same
+// ring and k order, so the same bits). A 128-row tile moves 3/4 of a 256-row
+// tile's bytes per stage and, the k-loop being bound by those bytes, takes
+// ≈0.75 of its time (measured 0.70-0.77 on one GPU's EP=8 share of config 2),
+// so it pays only where it keeps the number of rounds: see use_rows128.
+typedef DmaCfg<128, 256, 64, 64, 4, 32, 1> DmaExpert128;
 // The router's input gradient: one tile per CU, so no epilogue to hide; the
 // three-stage ring as measured.
 typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaRouterDx;
@@ -60,6 +67,26 @@ int num_cus() {
   return g_cus[dev];
 }
 
+// Whether a row-grouped GEMM runs on 128-row tiles: when its estimated rounds
+// of tiles per CU, weighted 0.75 for 128-row tiles, come out lower. The host
+// has the pair count, not the experts' row counts (those are on the device),
+// so each expert is taken to hold P / E rows and its last m-tile half full.
+// Only where experts average at least 128 rows (fewer leave a tile's A bytes
+// the same in both shapes) and the GEMM has few column tiles: at one GPU's
+// EP=8 share of config 2 (16 experts, ≈520 rows) down dgrad (3 column tiles)
+// fits one round either way and takes 0.75 of the time, while gate_up fwd
+// (6) would need two rounds instead of one.
+bool use_rows128(int kind, int P, int E, int H, int I, int cus) {
+  if (kind == EG_DOWN_WGRAD || kind == EG_GATE_UP_WGRAD || E <= 0 || P < 128 * E) return false;
+  const int ntn = kind == EG_GATE_UP_FWD ? (I + 127) / 128 : (kind == EG_DOWN_DGRAD ? (I + 255) / 256 : (H + 255) / 256);
+  const double a = (double)P / E;
+  auto rounds = [&](int bm) {
+    const double tiles = E * (a / bm + 0.5) * ntn;
+    return std::ceil(tiles / cus);
+  };
+  return 0.75 * rounds(128) < rounds(256);
+}
+
 }  // namespace
 
 template <typename T, typename Tw>
@@ -69,6 +96,8 @@ hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C,
   if constexpr (sizeof(T) == 2) {
     if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
       return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
+    if (use_rows128(kind, P, E, H, I, num_cus()))
+      return expert_gemm_persist_rows<DmaExpert128>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus(), s);
     return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {
     static_assert(std::is_same<T, Tw>::value, "fp32 operands give fp32 weight gradients");

@@ -764,4 +764,25 @@ hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const
   return hipErrorInvalidValue;
 }
 
+// The row-grouped expert GEMMs alone (forward and dgrad), for tile shapes that
+// serve only them (the weight gradients' k-row gathers take 256-row tiles).
+template <class Cfg>
+hipError_t expert_gemm_persist_rows(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
+                                    bf16_t* C2, const int32_t* offs, int P, int E, int H, int I,
+                                    const ExpertGather& xg, int num_cus, hipStream_t s) {
+  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
+  const bool gath = xg.index != nullptr;
+  switch (kind) {
+    case EG_GATE_UP_FWD:
+      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
+    case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
+    case EG_DOWN_DGRAD:
+      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
+      return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
+    case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 }  // namespace pmoe

@@ -127,6 +127,10 @@ GEMM_CASES = [
     # the Qwen3-235B-A22B layer widths (H = 4096, I = 1536: 128-stage gate_up reductions, 3072-wide
     # gate_up rows) with about 1024 rows per expert, skewed
     (1024, 8, 8, 4096, 1536, "zipf"),
+    # one GPU's share at EP = 8 of config 2 (16 experts of about 520 rows, K = 1): down dgrad on the
+    # 128-row tiles, the other row-grouped GEMMs on 256-row ones (cases above with 128 to 256 rows
+    # per expert and few column tiles take 128-row tiles throughout)
+    (8320, 1, 16, 2048, 768, "uniform"),
 ]
 
 
