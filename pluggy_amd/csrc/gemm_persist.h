@@ -734,38 +734,9 @@ hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, b
   return hipErrorInvalidValue;
 }
 
-// The six expert GEMMs on the persistent kernel; Tw is the weight gradients'
-// type (bf16, or fp32 for fp32 master weights: the accumulators stored
-// unrounded). A gathered operand takes the GATH instance of its GEMM.
-template <class Cfg, typename Tw = bf16_t>
-hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C, bf16_t* C2,
-                               Tw* Cw, const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
-                               int num_cus, hipStream_t s) {
-  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
-  const bool gath = xg.index != nullptr;
-  switch (kind) {
-    case EG_GATE_UP_FWD:
-      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
-    case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
-    case EG_DOWN_DGRAD:
-      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
-    case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
-    case EG_DOWN_WGRAD:
-    case EG_GATE_UP_WGRAD: {
-      p.C = Cw;
-      if (!gath) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw>(p, num_cus, s);
-      if (kind == EG_DOWN_WGRAD)
-        return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GA_KROWS>(p, num_cus, s);
-      return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GB_KROWS>(p, num_cus, s);
-    }
-  }
-  return hipErrorInvalidValue;
-}
-
-// The row-grouped expert GEMMs alone (forward and dgrad), for tile shapes that
-// serve only them (the weight gradients' k-row gathers take 256-row tiles).
+// The row-grouped expert GEMMs (forward and dgrad) on the persistent kernel;
+// a tile shape that serves only them (the weight gradients' k-row gathers
+// take 256-row tiles) is instantiated through this alone.
 template <class Cfg>
 hipError_t expert_gemm_persist_rows(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
                                     bf16_t* C2, const int32_t* offs, int P, int E, int H, int I,
@@ -783,6 +754,22 @@ hipError_t expert_gemm_persist_rows(int kind, const bf16_t* A, const bf16_t* B, 
     case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
   }
   return hipErrorInvalidValue;
+}
+
+// The six expert GEMMs on the persistent kernel; Tw is the weight gradients'
+// type (bf16, or fp32 for fp32 master weights: the accumulators stored
+// unrounded). A gathered operand takes the GATH instance of its GEMM.
+template <class Cfg, typename Tw = bf16_t>
+hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C, bf16_t* C2,
+                               Tw* Cw, const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
+                               int num_cus, hipStream_t s) {
+  if (kind != EG_DOWN_WGRAD && kind != EG_GATE_UP_WGRAD)
+    return expert_gemm_persist_rows<Cfg>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus, s);
+  GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
+  p.C = Cw;
+  if (xg.index == nullptr) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw>(p, num_cus, s);
+  if (kind == EG_DOWN_WGRAD) return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GA_KROWS>(p, num_cus, s);
+  return launch_gemm_persist<Cfg, false, false, GM_RED, EPI_STORE, Tw, GB_KROWS>(p, num_cus, s);
 }
 
 }  // namespace pmoe
