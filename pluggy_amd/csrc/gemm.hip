@@ -72,10 +72,11 @@ int num_cus() {
 // has the pair count, not the experts' row counts (those are on the device),
 // so each expert is taken to hold P / E rows and its last m-tile half full.
 // Only where experts average at least 128 rows (fewer leave a tile's A bytes
-// the same in both shapes) and the GEMM has few column tiles: at one GPU's
-// EP=8 share of config 2 (16 experts, ≈520 rows) down dgrad (3 column tiles)
-// fits one round either way and takes 0.75 of the time, while gate_up fwd
-// (6) would need two rounds instead of one.
+// the same in both shapes). The comparison favours GEMMs with few column
+// tiles: at one GPU's EP=8 share of config 2 (16 experts, ≈520 rows) down
+// dgrad (3 column tiles) fits one round either way and takes 0.75 of the
+// time, while gate_up fwd (6) would need two rounds instead of one; configs
+// 2-4 keep 256-row tiles throughout.
 bool use_rows128(int kind, int P, int E, int H, int I, int cus) {
   if (kind == EG_DOWN_WGRAD || kind == EG_GATE_UP_WGRAD || E <= 0 || P < 128 * E) return false;
   const int ntn = kind == EG_GATE_UP_FWD ? (I + 127) / 128 : (kind == EG_DOWN_DGRAD ? (I + 255) / 256 : (H + 255) / 256);
