@@ -24,6 +24,8 @@
 
 namespace pmoe {
 
+constexpr bool kNtAllEpilogues = false;
+
 template <class Cfg>
 struct PersistLayout {
   static constexpr int EPI_LD = Cfg::WN + 4;  // floats per staged fp32 row
@@ -60,6 +62,31 @@ struct EpiStage {
   static_assert(ROW % 4 == 0, "16-byte aligned staging rows");
 };
 
+// 16-byte global store of 8 outputs (bf16 packed in a u32x4, or half of 8
+// fp32). NT: non-temporal, so the output streams past L2 instead of evicting
+// the operand rows that the stages in flight read through it.
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, const u32x4& v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+  else *reinterpret_cast<u32x4*>(p) = v;
+}
+template <bool NT>
+__device__ __forceinline__ void st_out8(bf16_t* p, const float* v) { st16<NT>(p, Out8<bf16_t>::pack(v)); }
+template <bool NT>
+__device__ __forceinline__ void st_out8(float* p, const float* v) {
+  st16<NT>(p, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+  st16<NT>(p + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
+}
+
+// Which epilogues store non-temporally: the weight gradients (GM_RED), whose
+// outputs (an expert's whole weight block per tile, 0.8 GB at the
+// Qwen3-30B-A3B shape) would otherwise push the gathered rows the next tiles
+// read out of L2 (measured on a walk of the gate_up weight-gradient loads:
+// 64 GB/s per CU without stores, 29 with cached stores, 50 with
+// non-temporal ones).
+template <int GM>
+constexpr bool nt_epilogue() { return GM == GM_RED || kNtAllEpilogues; }
+
 template <class Cfg, typename Tout, int GM, int EPI, bool PACK, int SLAB>
 __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
@@ -69,6 +96,7 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   constexpr int QPS = SLAB / 8, NSL = 32 / SLAB;         // row groups q per slab, slabs per 32-row block
   static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
+  constexpr bool NT = nt_epilogue<GM>();
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
   const int half = lane >> 5, col_l = lane & 31;
@@ -116,14 +144,14 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             float g[8], u[8], m[8];
             const u32x4 gw = *reinterpret_cast<const u32x4*>(st32 + r * LDW + c / 2);
             const u32x4 uw = *reinterpret_cast<const u32x4*>(st32 + r * LDW + H2 / 2 + c / 2);
-            *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = gw;
-            *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + p.inter + col) = uw;
+            st16<NT>(C + (int64_t)row * p.ldc + col, gw);
+            st16<NT>(C + (int64_t)row * p.ldc + p.inter + col, uw);
             unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
             unpack8(uw, u);
             const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;  // the routing weight
 #pragma unroll
             for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t] * ws;
-            Out8<bf16_t>::store(MID + (int64_t)row * p.ldc2 + col, m);
+            st_out8<NT>(MID + (int64_t)row * p.ldc2 + col, m);
           }
         }
       } else {
@@ -140,7 +168,7 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             if constexpr (PACK) {
               const u32x4 w = *reinterpret_cast<const u32x4*>(st32 + r * LDW + c / 2);
               if (col + 8 <= p.N) {
-                *reinterpret_cast<u32x4*>(C + (int64_t)row * p.ldc + col) = w;
+                st16<NT>(C + (int64_t)row * p.ldc + col, w);
               } else {
                 unpack8(w, v);
                 for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
@@ -162,12 +190,12 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
                 dg[t] = dm * u[t] * (sg + silu * (1.0f - sg));
                 du[t] = dm * silu;
               }
-              Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
-              Out8<bf16_t>::store(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
+              st_out8<NT>(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
+              st_out8<NT>(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
             } else {
               Vec8<float>::load(stage + r * LD + c, v);
               if (col + 8 <= p.N) {
-                Out8<Tout>::store(C + (int64_t)row * p.ldc + col, v);
+                st_out8<NT>(C + (int64_t)row * p.ldc + col, v);
               } else {
                 for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
               }
@@ -411,17 +439,19 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   typedef typename std::conditional<B_KC, KcDma<BN, NW, BK>, TDma<BN, NW, BK>>::type LdB;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
+  constexpr bool kInterleaveFrags = true;
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
   // of stage g. Spread over all KS substeps, the last of which runs after the
   // stage's barrier: the gate_up forward (measured: -3 % on three slots, and
   // keeping them before the barrier costs 7 % on four) and, on the four-slot
   // ring, the other row-grouped GEMMs (down dgrad -1.6 %, gate_up dgrad
   // -1.4 % on one box; on three slots they lost 5-9 %). The weight gradients
-  // keep them before the barrier (spread: +1 % on four slots, +3 % on three). With a
-  // double buffer (NS = 2) the next stage has only the current one to land
-  // in, so its DMAs go out in the first substep.
-  constexpr int SPREAD =
-      NS == 2 ? 1 : (((EPI == EPI_SWIGLU && KS == 2) || (NS == 4 && GM == GM_ROWS)) ? KS : KS - 1);
+  // keep them before the barrier (spread: +1 % on four slots, +3 % on three).
+  // At least three slots: a tile's stage 0 does not wait, because its first
+  // NS - 1 >= 2 stages were fetched before it started; with two slots stage 1
+  // would be issued during stage 0 and read before it had landed.
+  static_assert(NS >= 3, "the persistent ring needs three slots or more");
+  constexpr int SPREAD = ((EPI == EPI_SWIGLU && KS == 2) || (NS == 4 && GM == GM_ROWS)) ? KS : KS - 1;
   constexpr int TOTM = SPREAD * MI * NI;  // MFMA slots the DMAs are spread over (several may share one)
   static_assert(SPREAD >= 1, "the DMAs of a stage need MFMA slots");
   // The stage's DMAs issued before its barrier. At that barrier stream stage
@@ -577,25 +607,33 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
-  // Fragments of substep ks from the slot at sa (A rows, then B rows).
+  // Fragment F of substep ks from the slot at sa: F < MI the A rows of block
+  // F, then the B rows of block F - MI.
+  auto load_frag = [&](const char* sa, int ks, auto fc, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
+    constexpr int F = decltype(fc)::value;
+    if constexpr (F < MI) {
+      if constexpr (A_KC) af[F] = kc_frag<BK>(sa, a_row0 + F * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else af[F] = t_frag<BM>(sa, a_row0 + F * 32, ks * 16, lane);
+    } else {
+      const char* sb = sa + Cfg::A_BYTES;
+      constexpr int J = F - MI;
+      if constexpr (B_KC) bfr[J] = kc_frag<BK>(sb, b_row0 + J * 32 + (lane & 31), ks * 2 + (lane >> 5));
+      else bfr[J] = t_frag<BN>(sb, b_row0 + J * 32, ks * 16, lane);
+    }
+  };
   auto load_frags = [&](const char* sa, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
-    const char* sb = sa + Cfg::A_BYTES;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      if constexpr (A_KC) af[i] = kc_frag<BK>(sa, a_row0 + i * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else af[i] = t_frag<BM>(sa, a_row0 + i * 32, ks * 16, lane);
-    }
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      if constexpr (B_KC) bfr[j] = kc_frag<BK>(sb, b_row0 + j * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else bfr[j] = t_frag<BN>(sb, b_row0 + j * 32, ks * 16, lane);
-    }
+    static_for<0, MI + NI>([&](auto fc) { load_frag(sa, ks, fc, af, bfr); });
   };
 
   f32x16 acc[MI][NI];
-  // One 16-k substep; the stage's D DMAs ride on its MFMAs.
+  // One 16-k substep; the stage's D DMAs ride on its MFMAs, and the MI + NI
+  // fragments of the next substep (substep ksn of the slot at sn, into afn /
+  // bfn) are read one after each MFMA rather than all before the first: a wave
+  // issues in order, so a burst of fragment reads that waits for room in the
+  // LDS queue (every wave reads at once after a barrier) would hold back the
+  // MFMAs behind it.
   auto substep = [&](auto ksc, const bf16x8 (&af)[MI], const bf16x8 (&bfr)[NI], const LoadTile& T, int ls,
-                     int g, const int (&tok)[GI][2]) {
+                     int g, const int (&tok)[GI][2], const char* sn, int ksn, bf16x8 (&afn)[MI], bf16x8 (&bfn)[NI]) {
     constexpr int KSI = decltype(ksc)::value;
     // The weight gradients (short k-loops, an epilogue per 16 stages) gain
     // from letting the wave that issues its MFMAs keep the SIMD (measured
@@ -605,6 +643,11 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       constexpr int M = decltype(mc)::value;
       acc[M / NI][M % NI] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
+      if constexpr (kInterleaveFrags) {
+        // the fragments left when this is the last MFMA (fewer MFMAs than fragments)
+        constexpr int F1 = M + 1 < MI * NI ? M + 1 : MI + NI;
+        static_for<M, (F1 < MI + NI ? F1 : MI + NI)>([&](auto fc) { load_frag(sn, ksn, fc, afn, bfn); });
+      }
       constexpr int G = KSI * MI * NI + M;
       static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;
@@ -615,6 +658,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
           __builtin_amdgcn_sched_barrier(0);
         }
       });
+      // pin each MFMA's fragment reads behind it
+      if constexpr (kInterleaveFrags) __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (GM == GM_RED) __builtin_amdgcn_s_setprio(0);
   };
@@ -661,10 +706,22 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       T.kd0 = in_next ? nxt.kd0 : cur.kd0;
       T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
       const int ls = in_next ? s - nk : s;
+      if constexpr (KGATH) {
+        // The token reads of the k-row gathers are scalar loads, which return
+        // out of order: while one is outstanding the compiler can only wait
+        // for an LDS fragment with lgkmcnt(0), which would also wait for the
+        // fragments of the next substep just issued. Waiting here, where the
+        // tokens (issued a substep ago) and this substep's fragments have
+        // landed, leaves no scalar load in flight, so the fragment waits below
+        // count LDS reads exactly. (Measured at the Qwen3-30B-A3B shape: the
+        // same speed either way; this loop is bound by its loads.)
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+      }
       static_for<0, KS - 1>([&](auto ksc) {
         constexpr int KSI = decltype(ksc)::value;
-        load_frags(sa, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
-        substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok);
+        if constexpr (!kInterleaveFrags) load_frags(sa, KSI + 1, af[(KSI + 1) & 1], bfr[(KSI + 1) & 1]);
+        substep(ksc, af[KSI & 1], bfr[KSI & 1], T, ls, g + NS - 1, tok, sa, KSI + 1, af[(KSI + 1) & 1],
+                bfr[(KSI + 1) & 1]);
       });
       // stream stage g + 1 has landed (this wave's share): outstanding are
       // only the full stages g + 2 .. g + NS - 2 and the DMAs this stage
@@ -682,8 +739,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
         }
       }
       // stream stage g + 1: this tile's next stage, or the next tile's first
-      load_frags(smem + slot_of(g + 1), 0, af[0], bfr[0]);
-      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1, tok);
+      if constexpr (!kInterleaveFrags) load_frags(smem + slot_of(g + 1), 0, af[0], bfr[0]);
+      substep(std::integral_constant<int, KS - 1>(), af[1], bfr[1], T, ls, g + NS - 1, tok, smem + slot_of(g + 1), 0,
+              af[0], bfr[0]);
       if constexpr (KGATH) {
 #pragma unroll
         for (int i = 0; i < GI; ++i) {
