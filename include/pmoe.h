@@ -256,7 +256,10 @@ PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32
  * consumes; y (P, H), the weighted expert rows, is only needed by the combine.
  * hidden (T,H), top_indices (T,K) int64, top_weights (T,K) w_dtype,
  * gate_up_proj (E,2I,H), down_proj (E,H,I), out (T,H); sorted_token (P,)
- * int32; sorted_w (P,) fp32; gate_up_out (P,2I), mid (P,I), y (P,H) dtype. */
+ * int32; sorted_w (P,) fp32; gate_up_out (P,2I), mid (P,I), y (P,H) dtype.
+ * top_weights and sorted_w are required when T > 0 (the weights reach the
+ * output only through sorted_w); NULL returns PMOE_ERR_INVALID before any
+ * launch. */
 PMOE_API size_t pmoe_expert_ffn_forward_workspace_size(int64_t T, int64_t K, int64_t E);
 PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indices, const void* top_weights,
                                      int w_dtype, const void* gate_up_proj, const void* down_proj, int dtype,
@@ -285,7 +288,7 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
  * grad_down_proj may be NULL. grad_weight_dtype is the dtype of the two weight
  * gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master weights).
  * Workspace holds grad_gate_up_out, the sorted rows' input gradient and the
- * routing-weight partials. */
+ * routing-weight partials. sorted_w (the forward's) is required when T > 0. */
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype);
 PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, int w_dtype, const void* gate_up_proj,
                                       const void* down_proj, int dtype, int64_t T, int64_t K, int64_t E, int64_t H,

@@ -216,12 +216,12 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
   const int splits = (int)router_splits(T);
   Carver cv(workspace);
   if (T == 0) {
+    // no tokens: dW = 0, written by the reduction kernel over zero partial
+    // planes (a kernel write, not hipMemsetAsync, so a captured graph replays it)
     if (grad_weight) {
-      float* zero = cv.take<float>((size_t)E * H);
-      PMOE_TRY(hipMemsetAsync(zero, 0, (size_t)E * H * sizeof(float), s), "router dW zero");
-      hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(zero, 1, E * H, (bf16_t*)grad_weight, s)
-                                           : reduce_partials<float>(zero, 1, E * H, (float*)grad_weight, s);
-      PMOE_TRY(st, "router dW reduce");
+      hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(nullptr, 0, E * H, (bf16_t*)grad_weight, s)
+                                           : reduce_partials<float>(nullptr, 0, E * H, (float*)grad_weight, s);
+      PMOE_TRY(st, "router dW zero");
     }
     return PMOE_OK;
   }
@@ -586,6 +586,12 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
   PMOE_REQUIRE(I > 0 && dtype_ok(dtype) && dtype_ok(w_dtype), "expert_ffn_forward: bad dtype or I");
+  // The routing weights reach the output only through sorted_w (the SwiGLU
+  // epilogue scales each sorted row by it; the combine is unweighted), so both
+  // are required: without them the sum would silently be unweighted.
+  PMOE_REQUIRE(T == 0 || (top_weights && sorted_w),
+               "expert_ffn_forward: top_weights and sorted_w are required (the routing weights enter through "
+               "sorted_w)");
   if (int rc = pmoe_permute_rows(top_indices, top_weights, w_dtype, T, K, E, counts, offs, sorted_pair, inv_pos,
                                  sorted_token, sorted_w, workspace, workspace_bytes, stream))
     return rc;
@@ -646,6 +652,9 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
                                              int32_t* inv_pos, int32_t* sorted_token, float* sorted_w,
                                              void* gate_up_out, void* mid, void* y, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
+  PMOE_REQUIRE(T == 0 || (top_weights && sorted_w),
+               "expert_ffn_forward_noalloc: top_weights and sorted_w are required (the routing weights enter "
+               "through sorted_w)");
   const size_t need = pmoe_expert_ffn_forward_workspace_size(T, K, E);
   if (need > kStaticScratchBytes)
     return fail(PMOE_ERR_UNSUPPORTED,
@@ -677,6 +686,9 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
   PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
   PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
                "expert_ffn_backward: weight gradient dtype must be the operands' or fp32");
+  // sorted_w scales the gradient of every sorted row (the forward's weighted
+  // rows); without it every gradient would be that of the unweighted sum
+  PMOE_REQUIRE(T == 0 || sorted_w, "expert_ffn_backward: sorted_w (the routing weight of each sorted row) is required");
   const size_t need = pmoe_expert_ffn_backward_workspace_size(T, K, H, I, dtype);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(PMOE_ERR_WORKSPACE, "expert_ffn_backward: workspace %zu < %zu bytes", workspace_bytes, need);

@@ -91,6 +91,18 @@ def _stage(name: str):
     return _timer.mark(name) if _timer is not None else contextlib.nullcontext()
 
 
+def _refuse_capture(op: str) -> None:
+    """The backward ops refuse to run while the current stream is capturing a
+    HIP graph, before any C-ABI call. The forward captures and replays bitwise
+    equal to eager (its entry points allocate nothing, never synchronise and
+    clear no memory with hipMemsetAsync); the backward is not claimed under
+    capture: the one trial capture of it (torch.cuda.make_graphed_callables on
+    the block) ended in a host segmentation fault whose cause is not known."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"pmoe::{op}: the MoE backward is not supported under HIP graph capture "
+                           "(capture the forward only)")
+
+
 # ---------------------------------------------------------------- autocast
 
 
@@ -225,6 +237,7 @@ def _(x, weight, top_k, norm_topk_prob, logit_bias):
                          schema="(Tensor x, Tensor weight, Tensor logits, Tensor top_i, Tensor top_w32, "
                                 "Tensor? grad_top_w, Tensor? grad_logits, bool norm_topk_prob) -> (Tensor, Tensor)")
 def _router_bwd(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob):
+    _refuse_capture("router_bwd")
     with _stage("router_bwd"):
         return ops.router_backward(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob)
 
@@ -360,6 +373,7 @@ def _expert_bwd_dgrad(grad_out, down_proj, offs, inv_pos, sorted_token, sorted_w
     (P, 2I) and, with need_top_w, the routing weights' gradient (T, K) fp32
     (an empty stand-in otherwise). grad_out (T, H) is the layer's output
     gradient; its rows are gathered by sorted_token."""
+    _refuse_capture("expert_bwd_dgrad")
     with _stage("down_dgrad"):
         g_gu, part = ops.down_proj_dgrad(grad_out, gu, down_proj, offs, sorted_token, sorted_w,
                                          need_part=need_top_w)
@@ -412,6 +426,8 @@ def _expert_bwd(g_gu, grad_out, hidden, gate_up, down, offs, inv_pos, sorted_tok
     grad_hidden_add), grad_gate_up, grad_down; an empty tensor where needs[i] is
     false (needs: hidden, gate_up, down). f32_wgrads (gate_up, down): that weight
     gradient is fp32 (an fp32 master's) instead of the operands' dtype."""
+    _refuse_capture("expert_bwd")
+
     def reduce_rows(g_xp):
         with _stage("dispatch_bwd"):
             return ops.dispatch_backward(g_xp, inv_pos, hidden.shape[0], top_k, add=grad_hidden_add)
@@ -704,6 +720,7 @@ def _sublayer_bwd(g_gu, grad_out_c, normed, gate_up, down, offs, inv_pos, sorted
     norm_weight, gate_up, down). grad_out_c is the output gradient in the
     compute dtype (the down wgrad gathers its rows). f32_wgrads (gate_up,
     down): that weight gradient is fp32 (an fp32 master's)."""
+    _refuse_capture("sublayer_bwd")
     need_x = needs[0] or needs[1]
 
     def reduce_rows(g_xp):

@@ -112,3 +112,30 @@ def test_sublayer_backward_fakes(pmoe_ops):
                                  [False, True])
     assert _sig(outs) == [((T, H), torch.float32), ((0,), torch.float32), ((E, 2 * I, H), torch.bfloat16),
                           ((E, H, I), torch.float32)]
+
+
+@pytest.mark.parametrize("op", ["router_bwd", "expert_bwd_dgrad", "expert_bwd", "sublayer_bwd"])
+def test_backward_ops_refuse_a_capturing_stream(monkeypatch, op):
+    """Under HIP graph capture each backward op raises before any C-ABI call
+    (the capture state is faked here, so nothing reaches the library: CPU
+    tensors would make a C-ABI call fail differently)."""
+    import torch
+
+    import pluggy_amd  # noqa: F401  (registers torch.ops.pmoe)
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    t = torch.zeros(4, 8)
+    i32 = torch.zeros(4, dtype=torch.int32)
+    args = {
+        "router_bwd": (t, torch.zeros(2, 8), torch.zeros(4, 2), torch.zeros(4, 1, dtype=torch.int64),
+                       torch.zeros(4, 1), None, None, True),
+        "expert_bwd_dgrad": (t, torch.zeros(2, 8, 4), i32[:2], i32, i32, torch.zeros(4), torch.zeros(4, 8), 1, False),
+        "expert_bwd": (torch.zeros(4, 8), t, t, torch.zeros(2, 8, 8), torch.zeros(2, 8, 4), i32[:2], i32, i32,
+                       torch.zeros(4, 4), None, 1, [True, False, False], [False, False]),
+        "sublayer_bwd": (torch.zeros(4, 8), t, t, torch.zeros(2, 8, 8), torch.zeros(2, 8, 4), i32[:2], i32, i32,
+                         torch.zeros(4, 4), None, t, torch.ones(8), torch.ones(4), None, 1,
+                         [True, False, False, False], [False, False]),
+    }[op]
+    with pytest.raises(RuntimeError, match="not supported under HIP graph capture"):
+        getattr(torch.ops.pmoe, op)(*args)

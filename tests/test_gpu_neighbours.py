@@ -262,3 +262,77 @@ def test_moe_sublayer_compiled_matches_eager(backend):
         else:
             check_close(f"record {i} (inductor vs eager)", b, a, 1e-2, MAX_ABS_FRAC[bf16])
         assert torch.equal(b, c), i
+
+
+@pytest.mark.timeout(600)
+def test_moe_sublayer_trainer_regime_config2():
+    """The trainer's form of the MoE half-block at the Qwen3-30B-A3B shape
+    (config 2: T = 8192, H = 2048, E = 128, K = 8, I = 768): ``moe_sublayer``
+    under bf16 autocast with an fp32 residual stream, an fp32 norm weight and
+    fp32 master weights (trainer.py:466-472, qwen3_moe.py:281). Every value and
+    gradient against fp64 truth given the kernels' routing and normed rows
+    (``ref_layer_fp64`` on the GPU, plus the RMSNorm and the logits' own
+    gradient in fp64): out, the input gradient, the norm-weight gradient, the
+    router weight gradient and both fp32 expert weight gradients, with the
+    rel-L2 <= 1e-2 and max-abs bounds of the full-size configuration tests."""
+    import pluggy_amd as pa
+    from pluggy_amd.workloads import CONFIGS, make_inputs
+    from tests._gpu_helpers import ref_layer_fp64
+
+    cfg = CONFIGS[2]
+    inp = make_inputs(cfg)
+    T, H, E, K, I = inp["x"].shape[0], cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
+    say(f"moe_sublayer trainer regime at config 2: T={T} H={H} E={E} K={K} I={I}, fp32 stream + masters, autocast bf16")
+    g = gen(57)
+    x = inp["x"].float()                      # the fp32 residual stream
+    nw = 1 + 0.1 * torch.randn(H, generator=g)
+    gout = inp["grad_out"].float()
+    glog = torch.randn(T, E, generator=g) * 0.01
+    eps = torch.finfo(f32).eps
+    norm = nn.RMSNorm(H, eps=eps).to(DEV)
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        norm.weight.copy_(nw)
+        mlp.router.weight.copy_(inp["router_weight"])
+        mlp.experts.gate_up_proj.copy_(inp["gate_up_proj"].float())  # fp32 masters holding bf16 values
+        mlp.experts.down_proj.copy_(inp["down_proj"].float())
+    xg = x.to(DEV).reshape(1, T, H).requires_grad_(True)
+    with torch.autocast("cuda", dtype=bf16):
+        out = pa.moe_sublayer(xg, norm, mlp)
+        logits = mlp.last_router_logits
+        loss = (out.reshape(T, H).float() * gout.to(DEV)).sum() + (logits * glog.to(DEV)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    assert out.dtype == f32 and xg.grad.dtype == f32
+    assert mlp.experts.gate_up_proj.grad.dtype == f32 and mlp.experts.down_proj.grad.dtype == f32
+    lg = logits.detach().float().cpu()
+    idx = torch.from_numpy(O.select_topk(lg, K))
+    # the normed rows the kernels saw (the same kernel gives the same bits)
+    n_kernel, _ = _ops().rmsnorm_forward(x.to(DEV), nw.to(DEV), eps, bf16)
+    nr = _check_routing_vs_cpu(n_kernel.cpu(), inp["router_weight"].to(bf16), lg, K)
+    say(f"  routing ok (near-tie rows vs CPU logits: {nr})")
+    # under autocast the router runs on the bf16 copy of its fp32 weight (the
+    # master's gradient is the copy's)
+    wr_b = inp["router_weight"].to(bf16).float()
+    ref = ref_layer_fp64(n_kernel, wr_b, inp["gate_up_proj"], inp["down_proj"], idx, lg, True, gout=gout)
+    # the logits' own gradient (the aux-loss path): d n += glog W_r, d W_r += glog^T n
+    Wr = wr_b.to(DEV).double()
+    n64 = n_kernel.double()
+    gl = glog.to(DEV).double()
+    dn = ref["dx"] + gl @ Wr
+    dWr = ref["dWr"] + gl.t() @ n64
+    # RMSNorm backward and the residual term in fp64 autograd (forward values
+    # replaced by the kernel's rounded rows, gradients through the exact norm)
+    x64 = x.to(DEV).double().requires_grad_(True)
+    w64 = nw.to(DEV).double().requires_grad_(True)
+    n_exact = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + eps) * w64
+    gx, gw = torch.autograd.grad(n_exact, (x64, w64), grad_outputs=dn)
+    gx = gx + gout.to(DEV).double()
+    out_ref = x.to(DEV).double() + ref["out"]
+    frac = MAX_ABS_FRAC[bf16]
+    check_close("out", out.reshape(T, H), out_ref, 1e-2, frac)
+    check_close("dx", xg.grad.reshape(T, H), gx, 1e-2, frac)
+    check_close("d norm.weight", norm.weight.grad, gw, 1e-2, frac)
+    check_close("d router.weight", mlp.router.weight.grad, dWr, 1e-2, frac)
+    check_close("d gate_up_proj (fp32 master)", mlp.experts.gate_up_proj.grad, ref["dWgu"], 1e-2, frac)
+    check_close("d down_proj (fp32 master)", mlp.experts.down_proj.grad, ref["dWdn"], 1e-2, frac)

@@ -126,6 +126,32 @@ def test_noalloc_forward_rejects_sizes_beyond_its_static_scratch(lib):
     from pluggy_amd import _lib
 
     T, K, E, H, I = 131073, 8, 128, 64, 32  # 513 chunks x 128 experts x 4 bytes > 256 KiB
+    dev = ctypes.c_void_p(256)  # the routing weights must be given; never dereferenced here
+    outs = [None] * 10
+    outs[6] = dev  # sorted_w
     with pytest.raises(RuntimeError, match="static maximum"):
-        _lib.call("pmoe_expert_ffn_forward_noalloc", *([None] * 3), _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
-                  T, K, E, H, I, *([None] * 10), None)
+        _lib.call("pmoe_expert_ffn_forward_noalloc", None, None, dev, _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
+                  T, K, E, H, I, *outs, None)
+
+
+def test_expert_ffn_requires_the_routing_weights(lib):
+    """The routing weights reach the output only through sorted_w (the SwiGLU
+    epilogue scales each sorted row; the combine is unweighted), so the C-ABI
+    forward and backward refuse NULL top_weights / sorted_w before any launch
+    instead of returning the unweighted sum or its gradients."""
+    from pluggy_amd import _lib
+
+    T, K, E, H, I = 64, 2, 8, 64, 32
+    dev = ctypes.c_void_p(256)  # never dereferenced: the argument check returns first
+    fwd = lambda top_w, sorted_w: lib.pmoe_expert_ffn_forward(  # noqa: E731
+        dev, dev, top_w, _lib.PMOE_F32, dev, dev, _lib.PMOE_BF16, T, K, E, H, I, dev, dev, dev, dev, dev, dev,
+        sorted_w, dev, dev, dev, dev, 1 << 20, None)
+    for top_w, sorted_w in ((None, dev), (dev, None), (None, None)):
+        assert fwd(top_w, sorted_w) == -1
+        assert b"top_weights and sorted_w are required" in lib.pmoe_last_error_string()
+    rc = lib.pmoe_expert_ffn_forward_noalloc(dev, dev, dev, _lib.PMOE_F32, dev, dev, _lib.PMOE_BF16, T, K, E, H, I,
+                                            dev, dev, dev, dev, dev, dev, None, dev, dev, dev, None)
+    assert rc == -1 and b"top_weights and sorted_w are required" in lib.pmoe_last_error_string()
+    rc = lib.pmoe_expert_ffn_backward(dev, dev, _lib.PMOE_F32, dev, dev, _lib.PMOE_BF16, T, K, E, H, I, dev, dev,
+                                      dev, None, dev, dev, dev, dev, dev, dev, _lib.PMOE_BF16, dev, 1 << 30, None)
+    assert rc == -1 and b"sorted_w (the routing weight of each sorted row) is required" in lib.pmoe_last_error_string()

@@ -9,6 +9,8 @@ sizes beyond it are rejected before any launch.
 
 from __future__ import annotations
 
+import ctypes
+
 import pytest
 import torch
 
@@ -74,6 +76,9 @@ def test_noalloc_rejects_sizes_beyond_the_static_scratch():
     from pluggy_amd import _lib
 
     T, K, E, H, I = 131073, 8, 128, 64, 32  # one chunk more than 256 KiB of histograms hold
+    dev = ctypes.c_void_p(256)  # routing weights must be given; the size check returns before any launch
+    outs = [None] * 10
+    outs[6] = dev  # sorted_w
     with pytest.raises(RuntimeError, match="static maximum"):
-        _lib.call("pmoe_expert_ffn_forward_noalloc", *([None] * 3), _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
-                  T, K, E, H, I, *([None] * 10), None)
+        _lib.call("pmoe_expert_ffn_forward_noalloc", None, None, dev, _lib.PMOE_F32, None, None, _lib.PMOE_BF16,
+                  T, K, E, H, I, *outs, None)
