@@ -238,7 +238,8 @@ PMOE_API int pmoe_combine_residual_backward(const void* grad_out, int res_dtype,
  * grad_residual and grad_x are (T,H) x_dtype; weight and rstd (from
  * pmoe_rmsnorm_forward) fp32; grad_weight (H,) w_dtype. grad_x_perm,
  * grad_normed_add, grad_residual and grad_weight may each be NULL (no term /
- * not wanted). H <= 4096 (PMOE_ERR_UNSUPPORTED beyond). */
+ * not wanted). H <= 16384 (PMOE_ERR_UNSUPPORTED beyond): rows up to 4096 are
+ * held in registers, wider ones walked twice (twice the grad_x_perm reads). */
 PMOE_API size_t pmoe_dispatch_rmsnorm_backward_workspace_size(int64_t T, int64_t H);
 PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32_t* inv_pos,
                                             const void* grad_normed_add, int dtype, const void* x, int x_dtype,

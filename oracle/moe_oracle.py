@@ -295,13 +295,14 @@ def expert_ffn_dense_fp64(hidden, top_indices, top_weights, gate_up_proj, down_p
 
 
 def sparse_mlp_forward(x, router_weight, gate_up_proj, down_proj, top_k: int,
-                       norm_topk_prob: bool = True, ffn=expert_ffn_loop):
+                       norm_topk_prob: bool = True, ffn=expert_ffn_loop, logit_bias=None):
     """Restates ``Qwen3MoeSparseMLP.forward`` (qwen3_moe.py:233-239).
 
-    Returns ``(y (B,S,H), router_logits (T,E))``.
+    Returns ``(y (B,S,H), router_logits (T,E))``. ``logit_bias`` as in
+    ``router_forward`` (the benchmark's skewed routing; None in the reference).
     """
     B, S, H = x.shape
     flat = x.reshape(B * S, H)
-    logits, w, idx, _ = router_forward(flat, router_weight, top_k, norm_topk_prob)
+    logits, w, idx, _ = router_forward(flat, router_weight, top_k, norm_topk_prob, logit_bias)
     y = ffn(flat, idx, w, gate_up_proj, down_proj)
     return y.reshape(B, S, H), logits

@@ -5,7 +5,7 @@ and operator (pluggy/kernels/moe.py:127-168), backed by hand-written HIP kernels
 in ``libpmoe.so`` (C ABI in ``include/pmoe.h``).
 """
 
-from .moe import RouterStats, moe_expert_ffn, moe_sublayer, router_topk, sparse_moe_block
+from .moe import RouterStats, moe_expert_ffn, moe_sublayer, router_topk, sparse_moe_block, weight_cast_cache
 from .qwen3_moe import Qwen3MoeExperts, Qwen3MoeSparseMLP, Qwen3MoeTopKRouter
 from .router_aux import (
     expert_counts_from_stats,
@@ -31,4 +31,5 @@ __all__ = [
     "router_z_loss_from_stats",
     "select_lower_id",
     "sparse_moe_block",
+    "weight_cast_cache",
 ]

@@ -109,7 +109,11 @@ template <typename T, typename TX>
 hipError_t dispatch_rmsnorm_bwd(const T* gxp, const int32_t* inv_pos, const T* add, const TX* x, const float* w,
                                 const float* rstd, const TX* res, int T_, int K, int H, TX* gx, float* gw_partial,
                                 hipStream_t s);
-constexpr int kRmsnormMaxH = 4096;
+// rows up to kRmsnormRegH are held in registers by the backward; wider rows
+// (up to kRmsnormMaxH: two waves' norm-weight partials of 2 * H floats in LDS)
+// are walked twice in chunks
+constexpr int kRmsnormRegH = 4096;
+constexpr int kRmsnormMaxH = 16384;
 constexpr int kRmsnormBwdMaxBlocks = 1024;
 int rmsnorm_bwd_blocks(int T_);
 // Tall partial matrices (rows x n) are reduced in two passes: groups of

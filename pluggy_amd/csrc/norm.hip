@@ -165,6 +165,73 @@ __global__ __launch_bounds__(256) void dispatch_rmsnorm_bwd_kernel(
   }
 }
 
+// The same row backward for rows too wide to hold in registers (H > 512 *
+// 8): each row is walked twice in 512-column chunks, first for <g * w, x>,
+// then for gx, re-reading its K expert rows (twice the gxp traffic of the
+// register kernel). The norm-weight partial of each of the block's two waves
+// accumulates in its own LDS row (dynamic shared memory, 2 * H floats); the
+// two rows are summed in wave order at the end, as in the register kernel.
+template <typename T, typename TX>
+__global__ __launch_bounds__(128) void dispatch_rmsnorm_bwd_wide_kernel(
+    const T* __restrict__ gxp, const int32_t* __restrict__ inv_pos, const T* __restrict__ add,
+    const TX* __restrict__ x, const float* __restrict__ w, const float* __restrict__ rstd, const TX* __restrict__ res,
+    int T_, int K, int H, TX* __restrict__ gx, float* __restrict__ gw_partial) {
+  extern __shared__ float s_gw_wide[];  // [2][H]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = gridDim.x * 2;
+  float* my_gw = s_gw_wide + (size_t)wave * H;
+  for (int c = lane; c < H; c += 64) my_gw[c] = 0.0f;
+  // g (dL/dn) of 8 columns from c of row t: add + the K expert rows in order
+  auto row_grad = [&](int t, int c, float* g) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = 0.0f;
+    if (add != nullptr) Vec8<T>::load(add + (int64_t)t * H + c, g);
+    if (gxp != nullptr) {
+      for (int k = 0; k < K; ++k) {
+        float v[8];
+        Vec8<T>::load(gxp + (int64_t)inv_pos[(int64_t)t * K + k] * H + c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] += v[e];
+      }
+    }
+  };
+  for (int t = blockIdx.x * 2 + wave; t < T_; t += nwaves) {
+    const TX* xr = x + (int64_t)t * H;
+    float dot = 0.0f;
+    for (int c = lane * 8; c < H; c += 512) {
+      float g[8], xv[8], wv[8];
+      row_grad(t, c, g);
+      Vec8<TX>::load(xr + c, xv);
+      Vec8<float>::load(w + c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += g[e] * wv[e] * xv[e];
+    }
+    dot = wave_sum(dot);
+    const float r = rstd[t];
+    const float coef = r * r * r * dot / (float)H;
+    for (int c = lane * 8; c < H; c += 512) {
+      float g[8], xv[8], wv[8], o[8];
+      row_grad(t, c, g);
+      Vec8<TX>::load(xr + c, xv);
+      Vec8<float>::load(w + c, wv);
+      if (res != nullptr) Vec8<TX>::load(res + (int64_t)t * H + c, o);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] += r * wv[e] * g[e] - coef * xv[e];
+        my_gw[c + e] += g[e] * (xv[e] * r);  // this lane's own columns: no other lane writes them
+      }
+      Vec8<TX>::store(gx + (int64_t)t * H + c, o);
+    }
+  }
+  if (gw_partial == nullptr) return;  // uniform over the grid
+  __syncthreads();
+  for (int c = threadIdx.x; c < H; c += 128)
+    gw_partial[(int64_t)blockIdx.x * H + c] = s_gw_wide[c] + s_gw_wide[(size_t)H + c];
+}
+
 // tmp[g, j] = sum_{r in group g} partial[r, j], groups of kRowGroup rows in
 // order: the first of two passes that reduce a tall (rows x n) partial matrix
 // with the whole grid busy (one thread per column and group).
@@ -215,8 +282,14 @@ hipError_t dispatch_rmsnorm_bwd(const T* gxp, const int32_t* inv_pos, const T* a
   };
   if (H <= 1024) return by_k(std::integral_constant<int, 2>());
   if (H <= 2048) return by_k(std::integral_constant<int, 4>());
-  if (H <= kRmsnormMaxH) return by_k(std::integral_constant<int, 8>());
-  return hipErrorInvalidValue;
+  if (H <= kRmsnormRegH) return by_k(std::integral_constant<int, 8>());
+  if (H > kRmsnormMaxH) return hipErrorInvalidValue;
+  const size_t lds = (size_t)2 * H * sizeof(float);
+  auto wide = dispatch_rmsnorm_bwd_wide_kernel<T, TX>;
+  const hipError_t ea = hipFuncSetAttribute((const void*)wide, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (ea != hipSuccess) return ea;
+  hipLaunchKernelGGL(wide, dim3(nb), dim3(128), lds, s, gxp, inv_pos, add, x, w, rstd, res, T_, K, H, gx, gw_partial);
+  return hipGetLastError();
 }
 
 #define PMOE_INST_NORM(TX, TO) \

@@ -23,6 +23,7 @@ combine, and their backward) is one C-ABI call on the current stream;
 from __future__ import annotations
 
 import contextlib
+import weakref
 from collections import defaultdict
 from dataclasses import dataclass
 
@@ -171,6 +172,52 @@ def _pad_experts(gate_up_proj: torch.Tensor, down_proj: torch.Tensor, Hp: int, I
     return torch.cat([gate, up], dim=1), F.pad(down_proj, (0, Ip - I, 0, Hp - H))
 
 
+# bf16 copies of fp32 master weights kept across calls (see weight_cast_cache):
+# id(master) -> (weakref to the master, (version, data_ptr, shape, stride), copy)
+_cast_cache: dict[int, tuple] = {}
+_cast_cache_on = False
+
+
+@contextlib.contextmanager
+def weight_cast_cache(enabled: bool = True):
+    """Reuse the bf16 copies of fp32 master expert weights across calls.
+
+    Under bf16 autocast the kernels take bf16 copies of fp32 master weights,
+    as the reference casts them on every call (moe.py:110-112); its trainer
+    runs several micro-batches per optimizer step (trainer.py:466-486), each
+    casting again (2.4 GB read, 1.2 GB written per layer at the
+    Qwen3-30B-A3B shape). Inside this context a master's copy is made once
+    and reused while the master is unchanged: while its version counter,
+    storage and layout are those of the cached copy. Optimizer steps,
+    ``load_state_dict`` and in-place writes under ``torch.no_grad()`` bump the
+    version and so recast. Writes through ``.data`` do not bump it and are not
+    seen: inside the context, change masters through the tensor itself (or
+    leave the context). The copies stay alive as long as their masters (half
+    the masters' bytes). Eager mode only: under ``torch.compile`` every call
+    casts, as without the context.
+    """
+    global _cast_cache_on
+    prev, _cast_cache_on = _cast_cache_on, bool(enabled)
+    try:
+        yield
+    finally:
+        _cast_cache_on = prev
+        if not _cast_cache_on:
+            _cast_cache.clear()
+
+
+def _cached_bf16(w: torch.Tensor) -> torch.Tensor:
+    key = id(w)
+    state = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()))
+    hit = _cast_cache.get(key)
+    if hit is not None and hit[0]() is w and hit[1] == state:
+        return hit[2]
+    with torch.no_grad():
+        copy = w.detach().to(torch.bfloat16).contiguous()
+    _cast_cache[key] = (weakref.ref(w, lambda _r, k=key: _cast_cache.pop(k, None)), state, copy)
+    return copy
+
+
 def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, torch.Tensor | None]:
     """-> (the weight in the kernels' dtype, its fp32 master or None).
 
@@ -178,12 +225,28 @@ def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, tor
     outside autograd and passed to the op beside its bf16 copy. The op's
     backward then writes the master's gradient in fp32 straight from the
     weight-gradient GEMM, with no bf16 gradient and no cast kernel between.
-    Otherwise the cast, if any, is an ordinary differentiable one.
+    Inside ``weight_cast_cache`` the copy of a leaf master is reused while
+    the master is unchanged. Otherwise the cast, if any, is an ordinary
+    differentiable one.
     """
     if w.dtype == torch.float32 and dt == torch.bfloat16 and w.requires_grad and torch.is_grad_enabled():
+        if _cast_cache_on and w.is_leaf and not torch.compiler.is_compiling():
+            return _cached_bf16(w), w
         with torch.no_grad():
             return w.detach().to(dt).contiguous(), w
     return w.to(dtype=dt).contiguous(), None
+
+
+def _expert_weights(gate_up_proj: torch.Tensor, down_proj: torch.Tensor, dt: torch.dtype, Hp: int, Ip: int):
+    """-> gu, gu_master, dn, dn_master: the expert weights in the kernels'
+    dtype (``_compute_weight``), zero-padded to the kernels' multiples of 8
+    first when needed. The pad happens in the weights' own dtype, so fp32
+    masters keep their fp32 weight gradients (autograd slices them back)."""
+    if (Hp, Ip) != (gate_up_proj.shape[2], gate_up_proj.shape[1] // 2):
+        gate_up_proj, down_proj = _pad_experts(gate_up_proj, down_proj, Hp, Ip)
+    gu, gu_master = _compute_weight(gate_up_proj, dt)
+    dn, dn_master = _compute_weight(down_proj, dt)
+    return gu, gu_master, dn, dn_master
 
 
 def _needs(ctx, n: int) -> tuple[bool, ...]:
@@ -603,12 +666,7 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     Hp, Ip = _pad8(H), _pad8(I)
     x = _pad_last(hidden.to(dt), Hp).contiguous()
     rw = _pad_last(_router_operand(router_weight, amp), Hp).contiguous()
-    if (Hp, Ip) != (H, I):
-        gu, dn = _pad_experts(gate_up_proj.to(dt), down_proj.to(dt), Hp, Ip)
-        gu, gu_master, dn, dn_master = gu.contiguous(), None, dn.contiguous(), None
-    else:
-        gu, gu_master = _compute_weight(gate_up_proj, dt)
-        dn, dn_master = _compute_weight(down_proj, dt)
+    gu, gu_master, dn, dn_master = _expert_weights(gate_up_proj, down_proj, dt, Hp, Ip)
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
@@ -643,12 +701,7 @@ def moe_expert_ffn(
     H = hidden.shape[1]
     I = gate_up_proj.shape[1] // 2
     Hp, Ip = _pad8(H), _pad8(I)
-    if (Hp, Ip) != (H, I):
-        gu, dn = _pad_experts(gate_up_proj.to(dt), down_proj.to(dt), Hp, Ip)
-        gu, gu_master, dn, dn_master = gu.contiguous(), None, dn.contiguous(), None
-    else:
-        gu, gu_master = _compute_weight(gate_up_proj, dt)
-        dn, dn_master = _compute_weight(down_proj, dt)
+    gu, gu_master, dn, dn_master = _expert_weights(gate_up_proj, down_proj, dt, Hp, Ip)
     tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
     out = torch.ops.pmoe.expert_ffn_fwd(_pad_last(hidden.to(dt), Hp).contiguous(),
                                         top_indices.to(torch.int64).contiguous(), tw.contiguous(), gu, dn,
@@ -825,9 +878,10 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     require_gpu(x)
     assert isinstance(norm, torch.nn.RMSNorm) and tuple(norm.normalized_shape) == (H,) and norm.weight is not None
     I = mlp.experts.gate_up_proj.shape[1] // 2
-    if H > 4096 or H % 8 or I % 8 or x.dtype not in (torch.float32, torch.bfloat16):
-        # the fused backward keeps a row in registers, and its row kernels take
-        # 16-byte rows of an fp32 or bf16 stream; other shapes take the unfused path
+    if H > 16384 or H % 8 or I % 8 or x.dtype not in (torch.float32, torch.bfloat16):
+        # the fused backward's row kernels take 16-byte rows of an fp32 or bf16
+        # stream up to 16384 wide (beyond 4096 the rows are walked twice, with
+        # the norm-weight partials in LDS); other shapes take the unfused path
         return x + mlp(norm(x))
     r = mlp.router
     flat = x.reshape(B * S, H).contiguous()

@@ -139,3 +139,33 @@ def test_backward_ops_refuse_a_capturing_stream(monkeypatch, op):
     }[op]
     with pytest.raises(RuntimeError, match="not supported under HIP graph capture"):
         getattr(torch.ops.pmoe, op)(*args)
+
+
+def test_weight_cast_cache_keys_on_the_master_version():
+    """The cached bf16 copy of an fp32 master is reused while its version,
+    storage and layout are unchanged, remade after an in-place update, and
+    (the documented limit) not remade after a write through ``.data``."""
+    import pluggy_amd
+    import pluggy_amd.moe as M
+
+    w = torch.nn.Parameter(torch.randn(4, 8))
+    with pluggy_amd.weight_cast_cache():
+        c1, master = M._compute_weight(w, torch.bfloat16)
+        assert master is w and c1.dtype == torch.bfloat16 and torch.equal(c1, w.detach().to(torch.bfloat16))
+        c2, _ = M._compute_weight(w, torch.bfloat16)
+        assert c2 is c1
+        with torch.no_grad():
+            w.add_(1.0)
+        c3, _ = M._compute_weight(w, torch.bfloat16)
+        assert c3 is not c1 and torch.equal(c3, w.detach().to(torch.bfloat16))
+        w.data.mul_(2.0)  # not tracked by the version counter
+        c4, _ = M._compute_weight(w, torch.bfloat16)
+        assert c4 is c3
+        # non-leaf tensors (e.g. the padded master) are cast every time
+        p = w * 1.0
+        a, _ = M._compute_weight(p, torch.bfloat16)
+        b, _ = M._compute_weight(p, torch.bfloat16)
+        assert a is not b
+    assert not M._cast_cache
+    c5, _ = M._compute_weight(w, torch.bfloat16)
+    assert torch.equal(c5, w.detach().to(torch.bfloat16))

@@ -458,3 +458,84 @@ def test_config5_decode():
 
 def test_config3_qwen3_235b_a22b():
     _run_config(3)
+
+
+def test_fp32_masters_any_size_under_autocast():
+    """Unaligned H and I (zero-padded on the host) with fp32 master weights
+    under bf16 autocast: the pad happens in fp32, so the expert weight
+    gradients still arrive in fp32 from the GEMMs (autograd slices them back),
+    and they match fp64 autograd on the bf16 copies at the bf16 bar."""
+    pa = _mod()
+    B, S, H, E, K, I = 2, 96, 100, 8, 2, 52
+    say(f"fp32 masters, any size, autocast: H={H} I={I} E={E} K={K}")
+    g = gen(29)
+    x = torch.randn(B, S, H, generator=g)
+    Wr = torch.randn(E, H, generator=g) * 0.05
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).float()
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16).float()
+    gout = torch.randn(B * S, H, generator=g)
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        mlp.router.weight.copy_(Wr)
+        mlp.experts.gate_up_proj.copy_(Wgu)
+        mlp.experts.down_proj.copy_(Wdn)
+    xg = x.to(DEV).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = mlp(xg)
+    out.reshape(B * S, H).backward(gout.to(DEV))
+    for prm in (mlp.experts.gate_up_proj, mlp.experts.down_proj):
+        assert prm.grad.dtype == torch.float32 and prm.grad.shape == prm.shape
+    # fp64 truth on the operands the kernels saw: bf16 x and router weight, the masters' (bf16-valued) copies
+    idx = torch.from_numpy(O.select_topk(mlp.last_router_logits.detach().cpu(), K))
+    ref = _ref_block_fp64(x.reshape(B * S, H).to(torch.bfloat16).float(), Wr.to(torch.bfloat16).float(), Wgu, Wdn,
+                          idx, True, gout, torch.zeros(B * S, E))
+    frac = MAX_ABS_FRAC[torch.bfloat16]
+    check_close("out", out.reshape(B * S, H), ref[0], 1e-2, frac)
+    check_close("d gate_up_proj (fp32)", mlp.experts.gate_up_proj.grad, ref[4], 1e-2, frac)
+    check_close("d down_proj (fp32)", mlp.experts.down_proj.grad, ref[5], 1e-2, frac)
+
+
+def test_weight_cast_cache_reuses_copies_until_the_master_changes():
+    """Inside pluggy_amd.weight_cast_cache the bf16 copies of fp32 masters are
+    made once and reused (outputs and fp32 weight gradients bitwise equal to
+    the uncached path); an in-place update of a master (an optimizer step)
+    makes a new copy, again bitwise equal to the uncached path on the updated
+    weights; leaving the context drops the copies."""
+    import pluggy_amd.moe as M
+
+    pa = _mod()
+    T, H, E, K, I = 512, 256, 16, 4, 128
+    say(f"weight cast cache T={T} H={H} E={E} K={K} I={I}")
+    g = gen(67)
+    x = torch.randn(T, H, generator=g).to(DEV)
+    gout = torch.randn(T, H, generator=g).to(DEV)
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        for prm in mlp.parameters():
+            prm.copy_(torch.randn(prm.shape, generator=g) * 0.05)
+
+    def step():
+        mlp.zero_grad(set_to_none=True)
+        xg = x.clone().reshape(1, T, H).requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = mlp(xg)
+        out.reshape(T, H).backward(gout)
+        return [out.detach().clone(), xg.grad.clone()] + [p.grad.clone() for p in mlp.parameters()]
+
+    plain = step()
+    with pa.weight_cast_cache():
+        first = step()
+        copies = {k: v[2] for k, v in M._cast_cache.items()}
+        assert len(copies) == 2  # the two expert masters
+        second = step()
+        assert all(M._cast_cache[k][2] is c for k, c in copies.items()), "the copies were made again"
+        for a, b, c in zip(plain, first, second):
+            assert torch.equal(a, b) and torch.equal(a, c)
+        with torch.no_grad():  # an optimizer-style in-place update bumps the version
+            mlp.experts.gate_up_proj.mul_(0.5)
+        third = step()
+        assert M._cast_cache[id(mlp.experts.gate_up_proj)][2] is not copies[id(mlp.experts.gate_up_proj)]
+    assert not M._cast_cache
+    fresh = step()
+    for a, b in zip(third, fresh):
+        assert torch.equal(a, b)

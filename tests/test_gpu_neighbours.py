@@ -99,7 +99,10 @@ def _ref_norm_bwd(gxp, inv_pos, add, x, w, res, eps):
 
 @pytest.mark.parametrize("K,H,x_dtype,terms", [(8, 2048, f32, "all"), (3, 776, f32, "all"), (8, 3000, f32, "all"),
                                                (8, 2048, bf16, "all"), (8, 2048, f32, "no_perm"),
-                                               (8, 2048, f32, "no_add_res")])
+                                               (8, 2048, f32, "no_add_res"),
+                                               # rows wider than the register kernel's 4096: walked twice
+                                               (8, 7168, f32, "all"), (3, 5000, bf16, "all"),
+                                               (8, 16384, f32, "no_add_res"), (4, 6144, f32, "no_perm")])
 def test_dispatch_rmsnorm_backward(K, H, x_dtype, terms):
     T = 300
     P = T * K
@@ -205,6 +208,56 @@ def test_moe_sublayer_vs_fp64_and_unfused(x_dtype, autocast):
         check_close(n, a, b, 1e-2, MAX_ABS_FRAC[torch.bfloat16])
     unfused = run(False)
     for n, a, b in zip(names, got, unfused):
+        r = rel(a, b)
+        say(f"  vs unfused {n}: rel={r:.2e}")
+        assert r < 1e-2, n
+
+
+def test_moe_sublayer_wide_hidden():
+    """The fused half-block beyond H = 4096 (the RMSNorm backward walks each
+    row twice): H = 5120 under bf16 autocast with an fp32 stream, values and
+    every gradient against fp64 autograd and against the unfused composition."""
+    import pluggy_amd as pa
+    B, S, H, E, K, I = 1, 96, 5120, 8, 2, 64
+    say(f"moe_sublayer wide hidden B={B} S={S} H={H} E={E} K={K} I={I}")
+    g = gen(58)
+    x = torch.randn(B, S, H, generator=g) * 2
+    nw = 1 + 0.1 * torch.randn(H, generator=g)
+    Wr = torch.randn(E, H, generator=g) * 0.02
+    Wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(bf16)
+    Wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(bf16)
+    gout = torch.randn(B * S, H, generator=g)
+    glog = torch.randn(B * S, E, generator=g) * 0.01
+    norm = nn.RMSNorm(H).to(DEV)
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        norm.weight.copy_(nw)
+        mlp.router.weight.copy_(Wr)
+        mlp.experts.gate_up_proj.copy_(Wgu.float())
+        mlp.experts.down_proj.copy_(Wdn.float())
+
+    def run(fused):
+        for p in list(norm.parameters()) + list(mlp.parameters()):
+            p.grad = None
+        xg = x.to(DEV).requires_grad_(True)
+        with torch.autocast("cuda", dtype=bf16):
+            out = pa.moe_sublayer(xg, norm, mlp) if fused else xg + mlp(norm(xg))
+            logits = mlp.last_router_logits
+            loss = (out.reshape(B * S, H).float() * gout.to(DEV)).sum() + (logits * glog.to(DEV)).sum()
+        loss.backward()
+        return [out.reshape(B * S, H), logits, xg.grad.reshape(B * S, H), norm.weight.grad, mlp.router.weight.grad,
+                mlp.experts.gate_up_proj.grad, mlp.experts.down_proj.grad]
+
+    got = [t.detach().clone() for t in run(True)]
+    eps = torch.finfo(f32).eps
+    idx = torch.from_numpy(O.select_topk(got[1].cpu(), K))
+    n_kernel, _ = _ops().rmsnorm_forward(x.reshape(B * S, H).to(DEV), nw.to(DEV), eps, bf16)
+    ref, _ = _ref_sublayer_fp64(x.reshape(B * S, H), nw, eps, Wr.to(bf16).float(), Wgu.float(), Wdn.float(), idx,
+                                gout, glog, n_kernel.cpu())
+    names = ["out", "logits", "dx", "dnorm_w", "dWr", "dWgu", "dWdn"]
+    for n, a, b in zip(names, got, ref):
+        check_close(n, a, b, 1e-2, MAX_ABS_FRAC[bf16])
+    for n, a, b in zip(names, got, run(False)):
         r = rel(a, b)
         say(f"  vs unfused {n}: rel={r:.2e}")
         assert r < 1e-2, n
