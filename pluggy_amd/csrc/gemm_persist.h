@@ -25,6 +25,7 @@
 namespace pmoe {
 
 constexpr bool kNtAllEpilogues = false;
+constexpr bool kFastStoreEpilogue = true;
 
 template <class Cfg>
 struct PersistLayout {
@@ -87,6 +88,59 @@ __device__ __forceinline__ void st_out8(float* p, const float* v) {
 template <int GM>
 constexpr bool nt_epilogue() { return GM == GM_RED || kNtAllEpilogues; }
 
+// Epilogue of a plain-store tile (EPI_STORE) whose columns all lie inside N,
+// the common case. Each 8-row slab of a wave's 32-row block goes through the
+// wave's LDS region in fp32, written straight from the MFMA layout (lane
+// half h holds rows 4 h + r of the slab for its column: no lane exchange) and
+// read back as 8 consecutive outputs per lane, which one 16-byte raw buffer
+// store writes (two for fp32 outputs). The buffer covers the wave's valid
+// rows only, so rows past the tile's last row are dropped by the hardware's
+// bound check: no per-lane branch and no 64-bit address arithmetic. A wave's
+// LDS operations run in order, so each slab's reads follow its writes, and the
+// next slab's writes follow those reads, without a wait between them.
+// Per lane per slab: 4 write2, 2 ds_read_b128, 4 conversions, 1-2 stores.
+template <class Cfg, typename Tout, int GM, bool NT>
+__device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
+                                                     const TileInfo& ti, const GemmParams& p, int wm, int wn,
+                                                     int lane) {
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, WM = Cfg::WM, WN = Cfg::WN;
+  constexpr int LD = PersistLayout<Cfg>::EPI_LD;  // floats per staged row
+  constexpr int CPR = WN / 8;                     // 8-output chunks per row
+  static_assert(8 * CPR == kWave, "one chunk per lane per 8-row slab (64-column wave tiles)");
+  Tout* C = reinterpret_cast<Tout*>(p.C);
+  if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
+  const int row0 = ti.m0 + wm * WM;
+  const int rows = min(max(ti.m_end - row0, 0), WM);
+  Tout* base = C + (int64_t)row0 * p.ldc + ti.n0 + wn * WN;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      base, (short)0, rows > 0 ? (int)(((int64_t)(rows - 1) * p.ldc + WN) * (int64_t)sizeof(Tout)) : 0, 0x00020000);
+  const int half = lane >> 5, col_l = lane & 31;
+  const int r = lane / CPR, c = (lane % CPR) * 8;
+  const int ld_bytes = (int)(p.ldc * sizeof(Tout));
+  constexpr int AUX = NT ? 2 : 0;  // nt
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) stage[(4 * half + rr) * LD + j * 32 + col_l] = acc[i][j][4 * q + rr];
+      float v[8];
+      Vec8<float>::load(stage + r * LD + c, v);
+      const int off = (i * 32 + 8 * q + r) * ld_bytes + c * (int)sizeof(Tout);
+      if constexpr (sizeof(Tout) == 2) {
+        __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(v), rs, off, 0, AUX);
+      } else {
+        const u32x4 lo = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+        const u32x4 hi = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])};
+        __builtin_amdgcn_raw_buffer_store_b128(lo, rs, off, 0, AUX);
+        __builtin_amdgcn_raw_buffer_store_b128(hi, rs, off + 16, 0, AUX);
+      }
+    }
+  }
+}
+
 template <class Cfg, typename Tout, int GM, int EPI, bool PACK, int SLAB>
 __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
@@ -97,6 +151,12 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   constexpr bool NT = nt_epilogue<GM>();
+  if constexpr (EPI == EPI_STORE && Cfg::WN == 64 && kFastStoreEpilogue) {
+    if (ti.n0 + Cfg::BN <= p.N && (int64_t)Cfg::WM * p.ldc * (int64_t)sizeof(Tout) < ((int64_t)1 << 31)) {
+      store_tile_full_cols<Cfg, Tout, GM, NT>(acc, stage, ti, p, wm, wn, lane);
+      return;
+    }
+  }
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
   const int half = lane >> 5, col_l = lane & 31;
