@@ -299,6 +299,25 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
                                       void* grad_gate_up_proj, void* grad_down_proj, int grad_weight_dtype,
                                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------- engine queries ---
+ * No counterpart in the reference (which has no kernels of its own): which
+ * tile the grouped-GEMM engine gives an expert GEMM, for tests and tuning.
+ * kind: PMOE_GEMM_* below; dtype: the operands' (PMOE_BF16 takes the
+ * persistent DMA engine: 32-row tiles for the forward GEMMs of few-token
+ * batches, 128 or 256 otherwise; PMOE_F32 the register-staged one: 64 rows);
+ * num_cus <= 0: the current device's compute units. Returns the tile's rows,
+ * or a negative PMOE_ERR_* code. Host-only: launches nothing. */
+enum {
+  PMOE_GEMM_GATE_UP_FWD = 0,
+  PMOE_GEMM_DOWN_FWD = 1,
+  PMOE_GEMM_DOWN_DGRAD = 2,
+  PMOE_GEMM_DOWN_WGRAD = 3,
+  PMOE_GEMM_GATE_UP_DGRAD = 4,
+  PMOE_GEMM_GATE_UP_WGRAD = 5
+};
+PMOE_API int pmoe_expert_gemm_tile_rows(int kind, int64_t P, int64_t E, int64_t H, int64_t I, int dtype,
+                                        int num_cus);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,7 @@ SIGNATURES = {
     "pmoe_expert_ffn_forward_noalloc": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P,
                                                _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "pmoe_expert_ffn_backward_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _INT]),
+    "pmoe_expert_gemm_tile_rows": (_INT, [_INT, _I64, _I64, _I64, _I64, _INT, _INT]),
     "pmoe_expert_ffn_backward": (_INT, [_P, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
                                         _P, _P, _P, _P, _P, _P, _INT, _P, _SZ, _P]),
 }

@@ -732,6 +732,17 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
   return PMOE_OK;
 }
 
+// ------------------------------------------------------- engine queries
+
+PMOE_API int pmoe_expert_gemm_tile_rows(int kind, int64_t P, int64_t E, int64_t H, int64_t I, int dtype,
+                                        int num_cus) {
+  PMOE_REQUIRE(kind >= EG_GATE_UP_FWD && kind <= EG_GATE_UP_WGRAD, "expert_gemm_tile_rows: unknown kind %d", kind);
+  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  PMOE_REQUIRE(P >= 0 && P <= kMaxIndex && E >= 1 && E <= 1024 && H > 0 && I > 0 && H <= INT32_MAX && I <= INT32_MAX,
+               "expert_gemm_tile_rows: bad sizes");
+  return expert_gemm_tile_rows(kind, (int)P, (int)E, (int)H, (int)I, dtype == PMOE_BF16, num_cus);
+}
+
 // ------------------------------------------------------- block neighbours
 
 PMOE_API int pmoe_rmsnorm_forward(const void* x, int x_dtype, const float* weight, float eps, int64_t T, int64_t H,

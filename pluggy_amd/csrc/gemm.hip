@@ -90,14 +90,24 @@ bool use_rows128(int kind, int P, int E, int H, int I, int cus) {
 
 }  // namespace
 
+int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool bf16, int cus) {
+  if (!bf16) return CfgF32::BM;
+  if (cus <= 0) cus = num_cus();
+  if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
+    return DmaDecode::BM;
+  if (use_rows128(kind, P, E, H, I, cus)) return DmaExpert128::BM;
+  return DmaExpert::BM;
+}
+
 template <typename T, typename Tw>
 hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, Tw* Cw, const int32_t* offs,
                            int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s) {
   const bool wgrad = kind == EG_DOWN_WGRAD || kind == EG_GATE_UP_WGRAD;
   if constexpr (sizeof(T) == 2) {
-    if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
+    const int rows = expert_gemm_tile_rows(kind, P, E, H, I, true, num_cus());
+    if (rows == DmaDecode::BM)
       return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
-    if (use_rows128(kind, P, E, H, I, num_cus()))
+    if (rows == DmaExpert128::BM)
       return expert_gemm_persist_rows<DmaExpert128>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus(), s);
     return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {

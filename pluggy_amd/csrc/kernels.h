@@ -21,6 +21,11 @@ template <typename T, typename Tw>
 hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, Tw* Cw, const int32_t* offs,
                            int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s);
 
+// Rows of the tiles expert_gemm_run gives GEMM `kind` (32, 128 or 256 for bf16
+// operands, the register-staged engine's for fp32) on `cus` compute units
+// (<= 0: the current device's).
+int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool bf16, int cus);
+
 // ---- router GEMMs in fp32 arithmetic (gemm.hip). TX: x dtype, TW: router weight dtype.
 template <typename TX, typename TW>
 hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, float* logits, hipStream_t s);

@@ -537,13 +537,16 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
 }
 
 // The scatter for at most kFusedScanChunks chunks, with the scan folded in:
-// every block reads the whole chunk histogram (nchunks x E counts, a few
-// KiB), sums each expert's column (its total, and the part before this
-// block's chunk), and scans the totals over the experts, so the bases need no
-// kernel of their own; block 0 also writes counts and offs. The sums run in
-// chunk order and the scan in expert order, so every block derives the same
-// bases as the separate scan would.
+// every block reads the whole chunk histogram (nchunks x E counts, at most
+// kFusedScanEntries: 32 KiB), sums each expert's column (its total, and the
+// part before this block's chunk), and scans the totals over the experts, so
+// the bases need no kernel of their own; block 0 also writes counts and offs.
+// The sums run in chunk order and the scan in expert order, so every block
+// derives the same bases as the separate scan would. Larger histograms (many
+// experts and chunks: every block would re-read up to 256 KiB) take the
+// separate scan kernel.
 constexpr int kFusedScanChunks = 64;
+constexpr int kFusedScanEntries = 8192;
 __global__ __launch_bounds__(256) void permute_scatter_scan_kernel(const int64_t* __restrict__ idx, int P, int E,
                                                                    int nbits, int chunk, int nchunks,
                                                                    const int32_t* __restrict__ chunk_hist,
@@ -936,7 +939,7 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   }
   hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
                      chunk_hist);
-  if (nchunks <= kFusedScanChunks) {
+  if (nchunks <= kFusedScanChunks && nchunks * E <= kFusedScanEntries) {
     hipLaunchKernelGGL(permute_scatter_scan_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E,
                        nbits, chunk, nchunks, chunk_hist, counts, offs, sorted_pair, inv_pos, rt);
     return hipGetLastError();

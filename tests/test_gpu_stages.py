@@ -134,6 +134,20 @@ GEMM_CASES = [
 ]
 
 
+def test_gemm_cases_cover_both_row_tile_shapes():
+    """The EP=8-share case above runs down dgrad on the 128-row tiles on this
+    device (the engine's choice depends on the CU count), the larger cases on
+    256-row tiles, so the stage tests below cover both shapes."""
+    from pluggy_amd import _lib
+
+    q = lambda kind, T, K, E, H, I: _lib.load().pmoe_expert_gemm_tile_rows(  # noqa: E731
+        kind, T * K, E, H, I, _lib.PMOE_BF16, 0)
+    assert q(2, 8320, 1, 16, 2048, 768) == 128  # down dgrad at the EP=8 share
+    assert q(0, 8320, 1, 16, 2048, 768) == 256  # gate_up fwd there
+    assert q(0, 1024, 8, 8, 4096, 1536) == 256
+    assert q(0, 64, 8, 128, 2048, 768) == 32    # the decode shape's forward
+
+
 def _gemm_inputs(T, K, E, H, I, mode, dtype, seed=0):
     ops = _ops()
     g = gen(seed)

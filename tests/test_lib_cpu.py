@@ -155,3 +155,31 @@ def test_expert_ffn_requires_the_routing_weights(lib):
     rc = lib.pmoe_expert_ffn_backward(dev, dev, _lib.PMOE_F32, dev, dev, _lib.PMOE_BF16, T, K, E, H, I, dev, dev,
                                       dev, None, dev, dev, dev, dev, dev, dev, _lib.PMOE_BF16, dev, 1 << 30, None)
     assert rc == -1 and b"sorted_w (the routing weight of each sorted row) is required" in lib.pmoe_last_error_string()
+
+
+# PMOE_GEMM_* kinds: gate_up fwd, down fwd, down dgrad, down wgrad, gate_up dgrad, gate_up wgrad
+_KINDS = range(6)
+
+
+@pytest.mark.parametrize("cus,ep_share", [
+    (256, [256, 256, 128, 256, 256, 256]),   # MI355X
+    (304, [256, 128, 128, 256, 128, 256]),   # a 304-CU part: two rounds either way for down fwd / gate_up dgrad
+])
+def test_expert_gemm_tile_rows(lib, cus, ep_share):
+    """The grouped-GEMM engine's tile choice (host-only query, no launch): the
+    benchmark layers take 256-row tiles in every GEMM; one GPU's share at EP=8
+    of config 2 takes 128-row tiles where that keeps the number of rounds of
+    tiles per CU (each 128-row tile about 0.75 of a 256-row one): on 256 CUs
+    down dgrad only; the decode batch's forward GEMMs take the 32-row
+    few-token tiles; fp32 operands take the register-staged engine's 64-row
+    tiles."""
+    from pluggy_amd import _lib
+
+    bf, f32 = _lib.PMOE_BF16, _lib.PMOE_F32
+    rows = lambda kind, P, E, H, I, dt=bf: lib.pmoe_expert_gemm_tile_rows(kind, P, E, H, I, dt, cus)  # noqa: E731
+    for P, E, H, I in ((65536, 128, 2048, 768), (131072, 128, 4096, 1536)):  # configs 2 / 4 and 3
+        assert [rows(k, P, E, H, I) for k in _KINDS] == [256] * 6
+    assert [rows(k, 8326, 16, 2048, 768) for k in _KINDS] == ep_share
+    assert [rows(k, 512, 128, 2048, 768) for k in _KINDS] == [32, 32, 256, 256, 256, 256]
+    assert rows(0, 4096, 8, 512, 1024, f32) == 64
+    assert lib.pmoe_expert_gemm_tile_rows(7, 100, 8, 64, 64, bf, cus) == -1
