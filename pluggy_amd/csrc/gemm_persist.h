@@ -109,8 +109,10 @@ __device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI
   static_assert(8 * CPR == kWave, "one chunk per lane per 8-row slab (64-column wave tiles)");
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
-  const int row0 = ti.m0 + wm * WM;
-  const int rows = min(max(ti.m_end - row0, 0), WM);
+  // uniform by construction; said so, or the descriptor lives in VGPRs and
+  // every buffer access becomes a readfirstlane loop
+  const int row0 = __builtin_amdgcn_readfirstlane(ti.m0 + wm * WM);
+  const int rows = __builtin_amdgcn_readfirstlane(min(max(ti.m_end - row0, 0), WM));
   Tout* base = C + (int64_t)row0 * p.ldc + ti.n0 + wn * WN;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       base, (short)0, rows > 0 ? (int)(((int64_t)(rows - 1) * p.ldc + WN) * (int64_t)sizeof(Tout)) : 0, 0x00020000);
@@ -141,6 +143,98 @@ __device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI
   }
 }
 
+// Epilogue of the SwiGLU backward (down dgrad, EPI_SWIGLU_BWD) for a tile
+// whose columns all lie inside N. Each output needs its row's saved gate and
+// up pre-activations and routing weight, which live in HBM. They are loaded
+// PF slabs ahead through bounded raw buffer loads (rows past the tile's end
+// read zero), the slabs go through the wave's fp32 LDS rows as in
+// store_tile_full_cols, and the outputs and routing-weight partials leave
+// through bounded buffer stores (rows past the end dropped). The descriptors
+// must be wave-uniform (else each access becomes a readfirstlane loop) and
+// the per-slab row offsets go in the SGPR offset (else the unrolled slabs
+// hold one VGPR offset each and the 256x256 kernel spills). Measured on
+// MI355X at config 2: 0.300 ms against 0.321 ms for the slab loop in
+// store_slabs, with PF = 1, 2 and 3 alike. The arithmetic and its order are
+// those of that slab loop.
+template <class Cfg, bool NT>
+__device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
+                                                      const TileInfo& ti, const GemmParams& p, int wm, int wn,
+                                                      int lane) {
+  constexpr int MI = Cfg::MI, NI = Cfg::NI, WM = Cfg::WM, WN = Cfg::WN;
+  constexpr int LD = PersistLayout<Cfg>::EPI_LD;
+  constexpr int CPR = WN / 8;
+  static_assert(WN == 64 && 8 * CPR == kWave, "one 8-column chunk per lane per 8-row slab, 64-column partials");
+  constexpr int NSLAB = MI * 4, PF = 2;  // slabs per wave, slabs loaded ahead
+  const int row0 = __builtin_amdgcn_readfirstlane(ti.m0 + wm * WM);  // uniform: scalar descriptors
+  const int rows = __builtin_amdgcn_readfirstlane(min(max(ti.m_end - row0, 0), WM));
+  const int col0 = __builtin_amdgcn_readfirstlane(ti.n0 + wn * WN);
+  const int r = lane / CPR, c = (lane % CPR) * 8;
+  const int ldaux = (int)p.ldaux, ldc = (int)p.ldc;
+  const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row0 * p.ldaux;
+  bf16_t* DG = reinterpret_cast<bf16_t*>(p.C) + (int64_t)row0 * p.ldc;
+  const __amdgpu_buffer_rsrc_t rs_gu =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(GU), (short)0, rows * ldaux * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_dg = __builtin_amdgcn_make_buffer_rsrc(DG, (short)0, rows * ldc * 2, 0x00020000);
+  const bool has_w = p.row_w != nullptr, has_part = p.part != nullptr;
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(
+      has_w ? const_cast<float*>(p.row_w) + row0 : nullptr, (short)0, has_w ? rows * 4 : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_part = __builtin_amdgcn_make_buffer_rsrc(
+      has_part ? p.part + (int64_t)row0 * p.part_ld : nullptr, (short)0, has_part ? rows * p.part_ld * 4 : 0,
+      0x00020000);
+  constexpr int AUX = NT ? 2 : 0;
+  const int half = lane >> 5, col_l = lane & 31;
+  u32x4 pg[PF], pu[PF];
+  float pw[PF];
+  // slab s: rows 32 (s / 4) + 8 (s % 4) .. +7 of the wave; this lane's row in it is r
+  // per-lane offsets are fixed; the slab's first row and the column block go
+  // in the uniform (SGPR) offset, so the unrolled slabs share four VGPRs
+  const int vo_gu = (r * ldaux + c) * 2, vo_dg = (r * ldc + c) * 2, vo_w = r * 4, vo_part = r * p.part_ld * 4;
+  auto fetch = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    constexpr int R0 = (S / 4) * 32 + 8 * (S % 4);
+    const int so = (R0 * ldaux + col0) * 2;
+    pg[S % PF] = __builtin_amdgcn_raw_buffer_load_b128(rs_gu, vo_gu, so, 0);
+    pu[S % PF] = __builtin_amdgcn_raw_buffer_load_b128(rs_gu, vo_gu, so + (int)p.inter * 2, 0);
+    pw[S % PF] = has_w ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_w, vo_w, R0 * 4, 0)) : 1.0f;
+  };
+  static_for<0, PF>([&](auto sc) { fetch(sc); });
+  static_for<0, NSLAB>([&](auto sc) {
+    constexpr int S = decltype(sc)::value, i = S / 4, q = S % 4;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) stage[(4 * half + rr) * LD + j * 32 + col_l] = acc[i][j][4 * q + rr];
+    float v[8], g[8], u[8], dg[8], du[8];
+    Vec8<float>::load(stage + r * LD + c, v);
+    unpack8(pg[S % PF], g);
+    unpack8(pu[S % PF], u);
+    const float ws = pw[S % PF];
+    if constexpr (S + PF < NSLAB) fetch(std::integral_constant<int, S + PF>());
+    float pd = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float sg = fast_sigmoid(g[t]);
+      const float silu = g[t] * sg;
+      pd += v[t] * (silu * u[t]);
+      const float dm = v[t] * ws;
+      dg[t] = dm * u[t] * (sg + silu * (1.0f - sg));
+      du[t] = dm * silu;
+    }
+    constexpr int R0 = i * 32 + 8 * q;
+    const int so = (R0 * ldc + col0) * 2;
+    __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(dg), rs_dg, vo_dg, so, AUX);
+    __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(du), rs_dg, vo_dg, so + (int)p.inter * 2, AUX);
+    if (has_part) {  // the CPR = 8 lanes of a row are consecutive: sum them in a fixed order
+      pd += __shfl_xor(pd, 1);
+      pd += __shfl_xor(pd, 2);
+      pd += __shfl_xor(pd, 4);
+      if ((lane % CPR) == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pd), rs_part, vo_part,
+                                              (R0 * p.part_ld + col0 / 64) * 4, 0);
+    }
+  });
+}
+
 template <class Cfg, typename Tout, int GM, int EPI, bool PACK, int SLAB>
 __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                             const TileInfo& ti, const GemmParams& p, int wm, int wn, int lane) {
@@ -151,6 +245,13 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   constexpr bool NT = nt_epilogue<GM>();
+  if constexpr (EPI == EPI_SWIGLU_BWD && GM == GM_ROWS && Cfg::WN == 64 && kFastStoreEpilogue) {
+    if (ti.n0 + Cfg::BN <= p.N && (int64_t)Cfg::WM * p.ldaux * 2 < ((int64_t)1 << 31) &&
+        (int64_t)Cfg::WM * p.ldc * 2 < ((int64_t)1 << 31)) {
+      store_tile_swiglu_bwd<Cfg, NT>(acc, stage, ti, p, wm, wn, lane);
+      return;
+    }
+  }
   if constexpr (EPI == EPI_STORE && Cfg::WN == 64 && kFastStoreEpilogue) {
     if (ti.n0 + Cfg::BN <= p.N && (int64_t)Cfg::WM * p.ldc * (int64_t)sizeof(Tout) < ((int64_t)1 << 31)) {
       store_tile_full_cols<Cfg, Tout, GM, NT>(acc, stage, ti, p, wm, wn, lane);
