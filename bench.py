@@ -14,7 +14,8 @@ reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
 inputs, the MoE half-block with and without the fused RMSNorm / residual add
 (``neighbours``), the other BASELINE.json configurations' steps (``decode``:
 config 5, ``config4``: skewed routing, ``config3``: the Qwen3-235B-A22B layer;
-``ep8_share``: one GPU's share at EP=8), the forward expert GEMMs against
+``config2_fp16``: config 2 with fp16 tensors on the fp16 MFMAs; ``ep8_share``:
+one GPU's share at EP=8), the forward expert GEMMs against
 hipBLASLt's batched product on equal experts (``vendor_gemm``), and a CPU
 baseline (the restated reference CPU path) timed on this host.
 
@@ -324,24 +325,33 @@ def decode_leg(dev, steps: int = 50, warmup: int = 5):
             "stages_ms": {n: round(v["mean_ms"], 4) for n, v in sorted(st.items(), key=lambda kv: -kv[1]["total_ms"])}}
 
 
-def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=None):
+def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=None, dtype=None):
     """Another BASELINE.json configuration's whole layer step (router, experts,
     and the backward for fwd+bwd configs), timed like the headline line: HIP
     events around `steps` steps after `warmup`. Config 4 reuses config 2's
     tensors (`base_inp`: the same seeded draws) with its Zipf logit bias and
     reports the routing's per-expert counts and its step time relative to
-    config 2's (`base_ms`)."""
+    config 2's (`base_ms`). `dtype`: the configuration with its activations and
+    expert weights in that dtype instead (config 2 in fp16: the same draws
+    rounded to fp16)."""
+    import dataclasses
+
     import torch
 
     import pluggy_amd
     from pluggy_amd.workloads import CONFIGS, make_inputs, zipf_logit_bias
 
     cfg = CONFIGS[cfg_id]
+    if dtype is not None and dtype != cfg.dtype:
+        cfg = dataclasses.replace(cfg, name=f"{cfg.name}-{str(dtype).split('.')[-1]}", dtype=dtype)
     T, H, E, K, I = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
     if base_inp is not None:
         inp = dict(base_inp)
         if cfg.skew:
             inp["logit_bias"] = zipf_logit_bias(E, cfg.skew).to(dev)
+        for key in ("x", "gate_up_proj", "down_proj", "grad_out"):
+            if key in inp:
+                inp[key] = inp[key].to(cfg.dtype)
     else:
         inp = make_inputs(cfg, device=dev)
     mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
@@ -381,6 +391,7 @@ def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=
         out["expert_rows_min_max"] = [int(counts.min().item()), int(counts.max().item())]
     if base_ms:
         out["vs_config2_step"] = round(ms / base_ms, 3)
+    out["dtype"] = str(cfg.dtype).split(".")[-1]
     del mlp, inp
     torch.cuda.empty_cache()
     return out
@@ -621,7 +632,7 @@ def main() -> int:
     traffic = profiled_traffic(cfg.name)
     gemm_flops = cfg.gemm_flops()
     tflops = gemm_flops / (ms * 1e-3) / 1e12
-    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    es = cfg.dtype.itemsize
     # dominant kernel: the grouped-GEMM stage with the largest total time
     gemm = {n: s for n, s in stages.items() if n in GEMM_STAGES}
     dom = max(gemm, key=lambda n: gemm[n]["total_ms"])
@@ -678,7 +689,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "f32",
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "f16"}.get(cfg.dtype, "f32"),
         "data": "synthetic (seeded N(0,1) inputs and upstream grad, N(0,0.02) weights)",
         "config": {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if cfg.backward else 'fwd'}", "tokens": T,
                    "batch": B, "seq_len": T // B, "hidden": H, "experts": E, "top_k": K, "moe_intermediate": I,
@@ -716,6 +727,9 @@ def main() -> int:
         result["decode"] = decode_leg(dev)
         result["ep8_share"] = ep_share_leg(dev)
         result["config4"] = layer_leg(4, dev, args.steps, args.warmup, base_inp=inp, base_ms=ms)
+        # the same layer with fp16 tensors (the fp16 MFMA path), against the bf16 step
+        result["config2_fp16"] = layer_leg(2, dev, args.steps, args.warmup, base_inp=inp, base_ms=ms,
+                                           dtype=torch.float16)
         result["config3"] = layer_leg(3, dev, min(args.steps, 10), 3)
         result["vendor_gemm"] = vendor_gemm_leg(dev)
     if not args.no_cpu_baseline:

@@ -4,7 +4,12 @@
  * C ABI. Conventions shared by every entry point:
  *  - Pointers are device pointers (HBM) unless stated; tensors are dense
  *    row-major. Sizes are element counts.
- *  - dtype codes: PMOE_F32 (fp32) or PMOE_BF16 (bf16 stored as uint16).
+ *  - dtype codes: PMOE_F32 (fp32), PMOE_BF16 (bf16 stored as uint16) or
+ *    PMOE_F16 (IEEE fp16). fp16 is taken by the expert path (permutation row
+ *    tables, row movers, expert GEMMs, the whole-FFN entry points), which
+ *    computes it on the fp16 MFMAs with fp32 accumulation as the reference's
+ *    F.grouped_mm does for fp16 tensors; the router and the RMSNorm and
+ *    residual neighbours take fp32 or bf16.
  *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
  *    asynchronously; no entry point synchronises the host or allocates
  *    memory. Scratch memory comes from the caller through `workspace`, sized by
@@ -31,7 +36,7 @@ extern "C" {
 
 #define PMOE_API __attribute__((visibility("default")))
 
-enum { PMOE_F32 = 0, PMOE_BF16 = 1 };
+enum { PMOE_F32 = 0, PMOE_BF16 = 1, PMOE_F16 = 2 };
 enum {
   PMOE_OK = 0,
   PMOE_ERR_INVALID = -1,     /* bad shape, dtype or null pointer */
@@ -52,9 +57,12 @@ PMOE_API const char* pmoe_last_error_string(void);
  * (qwen3_moe.py:285-316) and the per-expert counts of _update_expert_counts
  * (qwen3_moe.py:417-426): expert_counts[e] (int32), prob_sum[e] = sum_t p[t,e],
  * lse_sq_sum = sum_t logsumexp(logits[t])^2. Any of the three may be NULL.
- * x: (T,H) x_dtype; weight: (E,H) w_dtype; logit_bias: (E,) fp32 or NULL;
- * logits: (T,E) fp32; top_weights: (T,K) tw_dtype; top_indices: (T,K) int64;
- * top_weights_f32: (T,K) fp32 (kept for the backward). */
+ * x: (T,H) x_dtype; weight: (E,H) w_dtype (both fp32 or bf16); logit_bias:
+ * (E,) fp32 or NULL; logits: (T,E) fp32; top_weights: (T,K) tw_dtype (fp32,
+ * bf16 or fp16: an fp16 block runs its router on fp32 x and rounds the weights
+ * to fp16 as the reference's .to(hidden_states.dtype), qwen3_moe.py:177);
+ * top_indices: (T,K) int64; top_weights_f32: (T,K) fp32 (kept for the
+ * backward). */
 PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E);
 PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight, int w_dtype,
                                  const float* logit_bias, int64_t T, int64_t H, int64_t E, int64_t K,
@@ -169,8 +177,8 @@ PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const vo
  *     gradient of its routing weight (pmoe_pair_weight_grad).
  *   grad_down_proj[e] = G_e^T . mid_e (zeros for an empty expert).
  * Either output may be NULL. grad_weight_dtype is grad_down_proj's dtype:
- * `dtype`, or PMOE_F32 with bf16 operands (the gradient of an fp32 master
- * weight that the forward cast to bf16, written without a separate cast). */
+ * `dtype`, or PMOE_F32 with 16-bit operands (the gradient of an fp32 master
+ * weight that the forward cast to 16 bits, written without a separate cast). */
 PMOE_API int pmoe_down_proj_backward(const void* grad, const int32_t* row_index, const float* row_weight,
                                      int64_t grad_rows, const void* mid, const void* gate_up_out,
                                      const void* down_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
@@ -287,7 +295,7 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
 /* Autograd of pmoe_expert_ffn_forward from grad_out (T,H) dtype. Any of
  * grad_hidden, grad_top_weights (T,K) w_dtype, grad_gate_up_proj,
  * grad_down_proj may be NULL. grad_weight_dtype is the dtype of the two weight
- * gradients: `dtype`, or PMOE_F32 with bf16 operands (fp32 master weights).
+ * gradients: `dtype`, or PMOE_F32 with 16-bit operands (fp32 master weights).
  * Workspace holds grad_gate_up_out, the sorted rows' input gradient and the
  * routing-weight partials. sorted_w (the forward's) is required when T > 0. */
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype);
@@ -302,7 +310,7 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
 /* ------------------------------------------------------- engine queries ---
  * No counterpart in the reference (which has no kernels of its own): which
  * tile the grouped-GEMM engine gives an expert GEMM, for tests and tuning.
- * kind: PMOE_GEMM_* below; dtype: the operands' (PMOE_BF16 takes the
+ * kind: PMOE_GEMM_* below; dtype: the operands' (PMOE_BF16 and PMOE_F16 take the
  * persistent DMA engine: 32-row tiles for the forward GEMMs of few-token
  * batches, 128 or 256 otherwise; PMOE_F32 the register-staged one: 64 rows);
  * num_cus <= 0: the current device's compute units. Returns the tile's rows,

@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libpmoe.so")
 
 PMOE_F32 = 0
 PMOE_BF16 = 1
+PMOE_F16 = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -106,7 +107,9 @@ def dtype_code(dt: torch.dtype) -> int:
         return PMOE_BF16
     if dt == torch.float32:
         return PMOE_F32
-    raise TypeError(f"pmoe supports bf16 and fp32 tensors, got {dt}")
+    if dt == torch.float16:
+        return PMOE_F16
+    raise TypeError(f"pmoe supports bf16, fp16 and fp32 tensors, got {dt}")
 
 
 def ptr(t: torch.Tensor | None):

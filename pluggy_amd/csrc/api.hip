@@ -56,7 +56,11 @@ struct Carver {
   }
 };
 
+// The router, the RMSNorm neighbours and the residual combine take fp32 and
+// bf16; the expert path (row tables, row movers, expert GEMMs) also fp16.
 bool dtype_ok(int d) { return d == PMOE_F32 || d == PMOE_BF16; }
+bool dtype16_ok(int d) { return dtype_ok(d) || d == PMOE_F16; }
+size_t elem_bytes(int d) { return d == PMOE_F32 ? 4 : 2; }
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Tokens per split-K chunk of the router weight-gradient GEMM (fp32 partials
@@ -96,11 +100,17 @@ int check_moe_dims(int64_t T, int64_t K, int64_t E, int64_t H, int64_t I) {
   return PMOE_OK;
 }
 
-// Calls f with a null pointer of the element type of a dtype code.
+// Calls f with a null pointer of the element type of a dtype code (fp32 or
+// bf16; by_dtype16 also fp16).
 template <class F>
 hipError_t by_dtype(int code, F&& f) {
   if (code == PMOE_BF16) return f(static_cast<bf16_t*>(nullptr));
   return f(static_cast<float*>(nullptr));
+}
+template <class F>
+hipError_t by_dtype16(int code, F&& f) {
+  if (code == PMOE_F16) return f(static_cast<f16_t*>(nullptr));
+  return by_dtype(code, f);
 }
 #define PMOE_ELEM(p) std::remove_pointer_t<decltype(p)>
 
@@ -128,7 +138,8 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
                                  float* prob_sum, float* lse_sq_sum, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(tw_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype16_ok(tw_dtype),
+               "router_forward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_weights && top_indices && top_weights_f32),
                "router_forward: null tensor");
   const size_t need = pmoe_router_forward_workspace_size(T, H, E);
@@ -174,14 +185,11 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
                                                               s);
       PMOE_TRY(st, "router logits GEMM");
     }
-    hipError_t st =
-        tw_dtype == PMOE_BF16
-            ? router_topk<bf16_t>(lparts, nsplit, sstride, E, logits, logit_bias, t, e, k, norm_topk_prob,
-                                  (bf16_t*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
-                                  router_rows(T), s)
-            : router_topk<float>(lparts, nsplit, sstride, E, logits, logit_bias, t, e, k, norm_topk_prob,
-                                 (float*)top_weights, top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt,
-                                 router_rows(T), s);
+    hipError_t st = by_dtype16(tw_dtype, [&](auto wp) {
+      typedef PMOE_ELEM(wp) W;
+      return router_topk<W>(lparts, nsplit, sstride, E, logits, logit_bias, t, e, k, norm_topk_prob, (W*)top_weights,
+                            top_indices, top_weights_f32, blk_psum, blk_lse2, blk_cnt, router_rows(T), s);
+    });
     PMOE_TRY(st, "router top-k");
   }
   if (expert_counts || prob_sum || lse_sq_sum)
@@ -204,7 +212,8 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
                                   int64_t H, int64_t E, int64_t K, int norm_topk_prob, void* grad_x,
                                   void* grad_weight, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(gw_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(gw_dtype),
+               "router_backward: dtype codes must be PMOE_F32 or PMOE_BF16");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_indices && top_weights_f32),
                "router_backward: null tensor");
   const size_t need = pmoe_router_backward_workspace_size(T, H, E);
@@ -301,7 +310,7 @@ PMOE_API int pmoe_permute_rows(const int64_t* top_indices, const void* top_weigh
                                int32_t* inv_pos, int32_t* sorted_token, float* sorted_w, void* workspace,
                                size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, 8, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(w_dtype), "unknown dtype code");
   PMOE_REQUIRE(counts && offs &&
                    (T == 0 || (top_indices && sorted_pair && inv_pos && sorted_token && (!sorted_w || top_weights))),
                "permute_rows: null tensor");
@@ -310,7 +319,7 @@ PMOE_API int pmoe_permute_rows(const int64_t* top_indices, const void* top_weigh
     return fail(PMOE_ERR_WORKSPACE, "permute_rows: workspace %zu < %zu bytes", workspace_bytes, need);
   PMOE_TRY(permute_pairs(top_indices, (int)T, (int)K, (int)E, counts, offs, sorted_pair, inv_pos,
                          static_cast<int32_t*>(workspace), kPermuteChunk, as_stream(stream), sorted_token, sorted_w,
-                         top_weights, w_dtype == PMOE_BF16),
+                         top_weights, w_dtype == PMOE_BF16 ? 1 : w_dtype == PMOE_F16 ? 2 : 0),
            "permute_rows");
   return PMOE_OK;
 }
@@ -326,28 +335,27 @@ PMOE_API int pmoe_count_invalid_ids(const int64_t* top_indices, int64_t n, int64
 PMOE_API int pmoe_dispatch(const void* hidden, int dtype, const int32_t* inv_pos, int64_t T, int64_t K, int64_t H,
                            void* x_perm, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(hidden && inv_pos && x_perm, "dispatch: null tensor");
-  hipError_t st = dtype == PMOE_BF16
-                      ? dispatch_rows<bf16_t>((const bf16_t*)hidden, inv_pos, (int)T, (int)K, (int)H, (bf16_t*)x_perm,
-                                              as_stream(stream))
-                      : dispatch_rows<float>((const float*)hidden, inv_pos, (int)T, (int)K, (int)H, (float*)x_perm,
-                                             as_stream(stream));
+  hipError_t st = by_dtype16(dtype, [&](auto tp) {
+    typedef PMOE_ELEM(tp) E;
+    return dispatch_rows<E>((const E*)hidden, inv_pos, (int)T, (int)K, (int)H, (E*)x_perm, as_stream(stream));
+  });
   return hip_status(st, "dispatch");
 }
 
 PMOE_API int pmoe_dispatch_backward(const void* grad_x_perm, const int32_t* inv_pos, const void* grad_hidden_add,
                                     int dtype, int64_t T, int64_t K, int64_t H, void* grad_hidden, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(grad_x_perm && inv_pos && grad_hidden, "dispatch_backward: null tensor");
-  hipError_t st = dtype == PMOE_BF16
-                      ? dispatch_rows_bwd<bf16_t>((const bf16_t*)grad_x_perm, inv_pos, (const bf16_t*)grad_hidden_add,
-                                                  (int)T, (int)K, (int)H, (bf16_t*)grad_hidden, as_stream(stream))
-                      : dispatch_rows_bwd<float>((const float*)grad_x_perm, inv_pos, (const float*)grad_hidden_add,
-                                                 (int)T, (int)K, (int)H, (float*)grad_hidden, as_stream(stream));
+  hipError_t st = by_dtype16(dtype, [&](auto tp) {
+    typedef PMOE_ELEM(tp) E;
+    return dispatch_rows_bwd<E>((const E*)grad_x_perm, inv_pos, (const E*)grad_hidden_add, (int)T, (int)K, (int)H,
+                                (E*)grad_hidden, as_stream(stream));
+  });
   return hip_status(st, "dispatch_backward");
 }
 
@@ -365,7 +373,7 @@ int check_gather(const int32_t* index, int64_t rows, int64_t cols, int dtype, in
     return PMOE_OK;
   }
   PMOE_REQUIRE(rows > 0, "%s: a gathered operand needs rows > 0", what);
-  const int64_t bytes = rows * cols * (dtype == PMOE_BF16 ? 2 : 4);
+  const int64_t bytes = rows * cols * (int64_t)elem_bytes(dtype);
   if (bytes >= ((int64_t)1 << 31) - 16)
     return fail(PMOE_ERR_UNSUPPORTED, "%s: gathered operand of %lld bytes exceeds the 2 GiB a descriptor addresses",
                 what, (long long)bytes);
@@ -385,6 +393,10 @@ hipError_t dispatch_expert(int kind, int dtype, int wdt, const void* A, const vo
                            void* C2, void* Cw, const int32_t* offs, int64_t P, int64_t E, int64_t H, int64_t I,
                            const ExpertGather& xg, hipStream_t s) {
   if (dtype == PMOE_F32) return run_expert<float, float>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+  if (dtype == PMOE_F16) {
+    if (wdt == PMOE_F32) return run_expert<f16_t, float>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+    return run_expert<f16_t, f16_t>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
+  }
   if (wdt == PMOE_F32) return run_expert<bf16_t, float>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
   return run_expert<bf16_t, bf16_t>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, s);
 }
@@ -395,15 +407,14 @@ hipError_t dispatch_expert(int kind, int dtype, int wdt, const void* A, const vo
 PMOE_API int pmoe_sort_rows(const int32_t* sorted_pair, const void* top_weights, int w_dtype, int64_t T, int64_t K,
                             int32_t* sorted_token, float* sorted_w, void* stream) {
   PMOE_REQUIRE(T >= 0 && K > 0 && T * K <= kMaxIndex, "sort_rows: bad sizes");
-  PMOE_REQUIRE(dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(w_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(sorted_pair && sorted_token && (sorted_w == nullptr || top_weights), "sort_rows: null tensor");
   const int P = (int)(T * K);
-  hipError_t st = w_dtype == PMOE_BF16
-                      ? sort_rows<bf16_t>(sorted_pair, (const bf16_t*)top_weights, P, (int)K, sorted_token, sorted_w,
-                                          as_stream(stream))
-                      : sort_rows<float>(sorted_pair, (const float*)top_weights, P, (int)K, sorted_token, sorted_w,
-                                         as_stream(stream));
+  hipError_t st = by_dtype16(w_dtype, [&](auto wp) {
+    typedef PMOE_ELEM(wp) W;
+    return sort_rows<W>(sorted_pair, (const W*)top_weights, P, (int)K, sorted_token, sorted_w, as_stream(stream));
+  });
   return hip_status(st, "sort_rows");
 }
 
@@ -411,7 +422,7 @@ PMOE_API int pmoe_gate_up_swiglu(const void* x, const int32_t* row_index, const 
                                  const void* gate_up_proj, const int32_t* offs, int dtype, int64_t P, int64_t E,
                                  int64_t H, int64_t I, void* gate_up_out, void* mid, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_swiglu: bad dtype or I");
+  PMOE_REQUIRE(dtype16_ok(dtype) && I > 0, "gate_up_swiglu: bad dtype or I");
   if (int rc = check_gather(row_index, x_rows, H, dtype, P, "gate_up_swiglu")) return rc;
   if (P == 0) return PMOE_OK;
   PMOE_REQUIRE(x && gate_up_proj && offs && gate_up_out && mid, "gate_up_swiglu: null tensor");
@@ -428,7 +439,7 @@ PMOE_API int pmoe_gate_up_swiglu(const void* x, const int32_t* row_index, const 
 PMOE_API int pmoe_down_proj(const void* mid, const void* down_proj, const int32_t* offs, int dtype, int64_t P,
                             int64_t E, int64_t H, int64_t I, void* y, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj: bad dtype or I");
+  PMOE_REQUIRE(dtype16_ok(dtype) && I > 0, "down_proj: bad dtype or I");
   if (P == 0) return PMOE_OK;
   PMOE_REQUIRE(mid && down_proj && offs && y, "down_proj: null tensor");
   PMOE_TRY(dispatch_expert(EG_DOWN_FWD, dtype, dtype, mid, down_proj, nullptr, y, nullptr, nullptr, offs, P, E, H, I,
@@ -443,8 +454,8 @@ PMOE_API int pmoe_down_proj_backward(const void* grad, const int32_t* row_index,
                                      int64_t H, int64_t I, void* grad_gate_up_out, void* grad_down_proj,
                                      int grad_weight_dtype, float* part, int64_t part_ld, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "down_proj_backward: bad dtype or I");
-  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+  PMOE_REQUIRE(dtype16_ok(dtype) && I > 0, "down_proj_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype != PMOE_F32 && grad_weight_dtype == PMOE_F32),
                "down_proj_backward: grad_down_proj dtype must be the operands' or fp32");
   if (int rc = check_gather(row_index, grad_rows, H, dtype, P, "down_proj_backward")) return rc;
   PMOE_REQUIRE(part == nullptr || (row_weight != nullptr && part_ld >= (I + 63) / 64),
@@ -480,8 +491,8 @@ PMOE_API int pmoe_gate_up_backward(const void* grad_gate_up_out, const void* x, 
                                    int64_t E, int64_t H, int64_t I, void* grad_x_perm, void* grad_gate_up_proj,
                                    int grad_weight_dtype, void* stream) {
   if (int rc = check_moe_dims(P, 1, E, H, I)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && I > 0, "gate_up_backward: bad dtype or I");
-  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+  PMOE_REQUIRE(dtype16_ok(dtype) && I > 0, "gate_up_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype != PMOE_F32 && grad_weight_dtype == PMOE_F32),
                "gate_up_backward: grad_gate_up_proj dtype must be the operands' or fp32");
   if (int rc = check_gather(row_index, x_rows, H, dtype, P, "gate_up_backward")) return rc;
   PMOE_REQUIRE(offs && (P == 0 || grad_gate_up_out), "gate_up_backward: null tensor");
@@ -508,15 +519,14 @@ PMOE_API int pmoe_pair_weight_grad(const float* part, int64_t part_ld, int64_t n
                                    int64_t T, int64_t K, void* grad_top_weights, int gw_dtype, void* stream) {
   PMOE_REQUIRE(T >= 0 && K > 0 && T * K <= kMaxIndex && nparts >= 0 && part_ld >= nparts && part_ld < (1 << 20),
                "pair_weight_grad: bad sizes");
-  PMOE_REQUIRE(dtype_ok(gw_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(gw_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(part && inv_pos && grad_top_weights, "pair_weight_grad: null tensor");
   const int P = (int)(T * K);
-  hipError_t st = gw_dtype == PMOE_BF16
-                      ? pair_weight_grad<bf16_t>(part, (int)part_ld, (int)nparts, inv_pos, P, (bf16_t*)grad_top_weights,
-                                                 as_stream(stream))
-                      : pair_weight_grad<float>(part, (int)part_ld, (int)nparts, inv_pos, P, (float*)grad_top_weights,
-                                                as_stream(stream));
+  hipError_t st = by_dtype16(gw_dtype, [&](auto gp) {
+    typedef PMOE_ELEM(gp) G;
+    return pair_weight_grad<G>(part, (int)part_ld, (int)nparts, inv_pos, P, (G*)grad_top_weights, as_stream(stream));
+  });
   return hip_status(st, "pair_weight_grad");
 }
 
@@ -525,23 +535,18 @@ PMOE_API int pmoe_pair_weight_grad(const float* part, int64_t part_ld, int64_t n
 PMOE_API int pmoe_combine(const void* y, const void* top_weights, int w_dtype, const int32_t* inv_pos, int dtype,
                           int64_t T, int64_t K, int64_t H, void* out, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(dtype) && dtype16_ok(w_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(y && inv_pos && out, "combine: null tensor");  // top_weights NULL: unit weights
   hipStream_t s = as_stream(stream);
   const int t = (int)T, k = (int)K, h = (int)H;
-  hipError_t st;
-  if (dtype == PMOE_BF16)
-    st = w_dtype == PMOE_BF16
-             ? combine_rows<bf16_t, bf16_t>((const bf16_t*)y, (const bf16_t*)top_weights, inv_pos, t, k, h,
-                                            (bf16_t*)out, s)
-             : combine_rows<bf16_t, float>((const bf16_t*)y, (const float*)top_weights, inv_pos, t, k, h,
-                                           (bf16_t*)out, s);
-  else
-    st = w_dtype == PMOE_BF16 ? combine_rows<float, bf16_t>((const float*)y, (const bf16_t*)top_weights, inv_pos, t,
-                                                            k, h, (float*)out, s)
-                              : combine_rows<float, float>((const float*)y, (const float*)top_weights, inv_pos, t, k,
-                                                           h, (float*)out, s);
+  hipError_t st = by_dtype16(dtype, [&](auto yp) {
+    return by_dtype16(w_dtype, [&](auto wp) {
+      typedef PMOE_ELEM(yp) Y;
+      typedef PMOE_ELEM(wp) W;
+      return combine_rows<Y, W>((const Y*)y, (const W*)top_weights, inv_pos, t, k, h, (Y*)out, s);
+    });
+  });
   return hip_status(st, "combine");
 }
 
@@ -549,26 +554,20 @@ PMOE_API int pmoe_combine_backward(const void* grad_out, const void* y, const vo
                                    const int32_t* inv_pos, int dtype, int64_t T, int64_t K, int64_t H,
                                    void* grad_y, void* grad_top_weights, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(dtype) && dtype16_ok(w_dtype), "unknown dtype code");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(grad_out && y && top_weights && inv_pos && grad_y && grad_top_weights,
                "combine_backward: null tensor");
   hipStream_t s = as_stream(stream);
   const int t = (int)T, k = (int)K, h = (int)H;
-  hipError_t st;
-  if (dtype == PMOE_BF16)
-    st = w_dtype == PMOE_BF16
-             ? combine_rows_bwd<bf16_t, bf16_t>((const bf16_t*)grad_out, (const bf16_t*)y,
-                                                (const bf16_t*)top_weights, inv_pos, t, k, h, (bf16_t*)grad_y,
-                                                (bf16_t*)grad_top_weights, s)
-             : combine_rows_bwd<bf16_t, float>((const bf16_t*)grad_out, (const bf16_t*)y, (const float*)top_weights,
-                                               inv_pos, t, k, h, (bf16_t*)grad_y, (float*)grad_top_weights, s);
-  else
-    st = w_dtype == PMOE_BF16
-             ? combine_rows_bwd<float, bf16_t>((const float*)grad_out, (const float*)y, (const bf16_t*)top_weights,
-                                               inv_pos, t, k, h, (float*)grad_y, (bf16_t*)grad_top_weights, s)
-             : combine_rows_bwd<float, float>((const float*)grad_out, (const float*)y, (const float*)top_weights,
-                                              inv_pos, t, k, h, (float*)grad_y, (float*)grad_top_weights, s);
+  hipError_t st = by_dtype16(dtype, [&](auto yp) {
+    return by_dtype16(w_dtype, [&](auto wp) {
+      typedef PMOE_ELEM(yp) Y;
+      typedef PMOE_ELEM(wp) W;
+      return combine_rows_bwd<Y, W>((const Y*)grad_out, (const Y*)y, (const W*)top_weights, inv_pos, t, k, h,
+                                    (Y*)grad_y, (W*)grad_top_weights, s);
+    });
+  });
   return hip_status(st, "combine_backward");
 }
 
@@ -585,7 +584,7 @@ PMOE_API int pmoe_expert_ffn_forward(const void* hidden, const int64_t* top_indi
                                      int32_t* sorted_token, float* sorted_w, void* gate_up_out, void* mid, void* y,
                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
-  PMOE_REQUIRE(I > 0 && dtype_ok(dtype) && dtype_ok(w_dtype), "expert_ffn_forward: bad dtype or I");
+  PMOE_REQUIRE(I > 0 && dtype16_ok(dtype) && dtype16_ok(w_dtype), "expert_ffn_forward: bad dtype or I");
   // The routing weights reach the output only through sorted_w (the SwiGLU
   // epilogue scales each sorted row by it; the combine is unweighted), so both
   // are required: without them the sum would silently be unweighted.
@@ -669,7 +668,7 @@ PMOE_API int pmoe_expert_ffn_forward_noalloc(const void* hidden, const int64_t* 
 }
 
 PMOE_API size_t pmoe_expert_ffn_backward_workspace_size(int64_t T, int64_t K, int64_t H, int64_t I, int dtype) {
-  const size_t es = dtype == PMOE_BF16 ? 2 : 4;
+  const size_t es = elem_bytes(dtype);
   const int64_t P = T * K;
   return align_up((size_t)P * 2 * I * es) + align_up((size_t)P * H * es) +
          align_up((size_t)P * ((I + 63) / 64) * sizeof(float));
@@ -683,8 +682,8 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
                                       void* grad_gate_up_proj, void* grad_down_proj, int grad_weight_dtype,
                                       void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, I)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
-  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype == PMOE_BF16 && grad_weight_dtype == PMOE_F32),
+  PMOE_REQUIRE(dtype16_ok(dtype) && dtype16_ok(w_dtype) && I > 0, "expert_ffn_backward: bad dtype or I");
+  PMOE_REQUIRE(grad_weight_dtype == dtype || (dtype != PMOE_F32 && grad_weight_dtype == PMOE_F32),
                "expert_ffn_backward: weight gradient dtype must be the operands' or fp32");
   // sorted_w scales the gradient of every sorted row (the forward's weighted
   // rows); without it every gradient would be that of the unweighted sum
@@ -693,7 +692,7 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(PMOE_ERR_WORKSPACE, "expert_ffn_backward: workspace %zu < %zu bytes", workspace_bytes, need);
   const int64_t P = T * K;
-  const size_t es = dtype == PMOE_BF16 ? 2 : 4;
+  const size_t es = elem_bytes(dtype);
   Carver c(workspace);
   void* g_gu = c.take<char>((size_t)P * 2 * I * es);
   void* g_xp = c.take<char>((size_t)P * H * es);
@@ -737,10 +736,10 @@ PMOE_API int pmoe_expert_ffn_backward(const void* grad_out, const void* hidden, 
 PMOE_API int pmoe_expert_gemm_tile_rows(int kind, int64_t P, int64_t E, int64_t H, int64_t I, int dtype,
                                         int num_cus) {
   PMOE_REQUIRE(kind >= EG_GATE_UP_FWD && kind <= EG_GATE_UP_WGRAD, "expert_gemm_tile_rows: unknown kind %d", kind);
-  PMOE_REQUIRE(dtype_ok(dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype16_ok(dtype), "unknown dtype code");
   PMOE_REQUIRE(P >= 0 && P <= kMaxIndex && E >= 1 && E <= 1024 && H > 0 && I > 0 && H <= INT32_MAX && I <= INT32_MAX,
                "expert_gemm_tile_rows: bad sizes");
-  return expert_gemm_tile_rows(kind, (int)P, (int)E, (int)H, (int)I, dtype == PMOE_BF16, num_cus);
+  return expert_gemm_tile_rows(kind, (int)P, (int)E, (int)H, (int)I, dtype != PMOE_F32, num_cus);
 }
 
 // ------------------------------------------------------- block neighbours
@@ -749,7 +748,8 @@ PMOE_API int pmoe_rmsnorm_forward(const void* x, int x_dtype, const float* weigh
                                   void* out, int out_dtype, float* rstd, void* stream) {
   PMOE_REQUIRE(T >= 0 && H > 0 && H % 8 == 0 && T <= kMaxIndex, "rmsnorm_forward: bad sizes T=%lld H=%lld",
                (long long)T, (long long)H);
-  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype),
+               "rmsnorm_forward: dtype codes must be PMOE_F32 or PMOE_BF16");
   PMOE_REQUIRE(eps >= 0.0f, "rmsnorm_forward: eps must be non-negative");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(x && weight && out && rstd, "rmsnorm_forward: null tensor");
@@ -767,7 +767,8 @@ PMOE_API int pmoe_combine_residual(const void* y, const void* top_weights, int w
                                    int dtype, const void* residual, int res_dtype, int64_t T, int64_t K, int64_t H,
                                    void* out, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype),
+               "combine_residual: dtype codes must be PMOE_F32 or PMOE_BF16");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(y && inv_pos && residual && out, "combine_residual: null tensor");  // top_weights NULL: unit weights
   hipError_t st = by_dtype(dtype, [&](auto yp) {
@@ -788,7 +789,8 @@ PMOE_API int pmoe_combine_residual_backward(const void* grad_out, int res_dtype,
                                             int64_t T, int64_t K, int64_t H, void* grad_y, void* grad_top_weights,
                                             void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(w_dtype) && dtype_ok(res_dtype),
+               "combine_residual_backward: dtype codes must be PMOE_F32 or PMOE_BF16");
   if (T == 0) return PMOE_OK;
   PMOE_REQUIRE(grad_out && y && top_weights && inv_pos && grad_y && grad_top_weights,
                "combine_residual_backward: null tensor");
@@ -817,7 +819,8 @@ PMOE_API int pmoe_dispatch_rmsnorm_backward(const void* grad_x_perm, const int32
                                             int64_t T, int64_t K, int64_t H, void* grad_x, void* grad_weight,
                                             int w_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, K, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(x_dtype) && dtype_ok(w_dtype), "unknown dtype code");
+  PMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(x_dtype) && dtype_ok(w_dtype),
+               "dispatch_rmsnorm_backward: dtype codes must be PMOE_F32 or PMOE_BF16");
   if (H > kRmsnormMaxH)
     return fail(PMOE_ERR_UNSUPPORTED, "dispatch_rmsnorm_backward: hidden size %lld > %d", (long long)H,
                 kRmsnormMaxH);

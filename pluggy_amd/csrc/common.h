@@ -8,7 +8,9 @@
 namespace pmoe {
 
 typedef uint16_t bf16_t;  // bf16 storage: the upper 16 bits of an fp32
+typedef _Float16 f16_t;   // IEEE binary16 (fp16)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -96,13 +98,45 @@ template <> struct Vec8<float> {
   }
 };
 
+// ---------------------------------------------------------------- fp16 ----
+// Conversions follow IEEE rules: fp16 -> fp32 is exact, fp32 -> fp16 rounds to
+// nearest even (overflow to +-inf, NaN stays NaN), in the hardware converters.
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float f16lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
+__device__ __forceinline__ float f16hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
+
+// Two fp32 -> packed fp16 (lo in bits 0-15).
+__device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+}
+
+template <> struct Vec8<f16_t> {
+  __device__ static __forceinline__ void load(const f16_t* p, float* v) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = f16lo(w[i]); v[2 * i + 1] = f16hi(w[i]); }
+  }
+  __device__ static __forceinline__ void store(f16_t* p, const float* v) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = cvt_pk_f16(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = w;
+  }
+};
+
 template <typename T> __device__ __forceinline__ float load_scalar(const T* p);
 template <> __device__ __forceinline__ float load_scalar<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float load_scalar<bf16_t>(const bf16_t* p) { return bf16_to_f32(*p); }
+template <> __device__ __forceinline__ float load_scalar<f16_t>(const f16_t* p) { return (float)*p; }
 
 template <typename T> __device__ __forceinline__ void store_scalar(T* p, float v);
 template <> __device__ __forceinline__ void store_scalar<float>(float* p, float v) { *p = v; }
 template <> __device__ __forceinline__ void store_scalar<bf16_t>(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+template <> __device__ __forceinline__ void store_scalar<f16_t>(f16_t* p, float v) { *p = (f16_t)v; }
 
 // ------------------------------------------------------------- wave ops ----
 
@@ -138,7 +172,6 @@ __device__ __forceinline__ float fast_sigmoid(float g) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two fp32 -> packed bf16 (lo in bits 0-15), round to nearest even, with the
@@ -147,6 +180,20 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   const f32x2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+// The 16-bit storage formats of the MFMA paths: packing of two rounded
+// values into a dword and the two halves of a dword back to fp32.
+template <typename T> struct Fmt16;
+template <> struct Fmt16<bf16_t> {
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
+  __device__ static __forceinline__ float lo(uint32_t w) { return bf16lo(w); }
+  __device__ static __forceinline__ float hi(uint32_t w) { return bf16hi(w); }
+};
+template <> struct Fmt16<f16_t> {
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return cvt_pk_f16(lo, hi); }
+  __device__ static __forceinline__ float lo(uint32_t w) { return f16lo(w); }
+  __device__ static __forceinline__ float hi(uint32_t w) { return f16hi(w); }
+};
 
 __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -50,6 +50,18 @@ typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaRouterDx;
 typedef DmaCfg<32, 128, 32, 32, 3, 128, 1> DmaDecode;
 constexpr int kDecodeRowsPerExpert = 32;
 
+// The same tile shapes for each 16-bit operand format (fp16 runs the same
+// kernels on v_mfma_f32_32x32x16_f16, with fp16 conversions in the epilogues).
+template <typename T16> struct PersistCfgs {
+  typedef DmaCfg<256, 256, 128, 64, 4, 32, 1, T16> Main;
+  typedef DmaCfg<128, 256, 64, 64, 4, 32, 1, T16> Rows128;
+  typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, T16> Decode;
+};
+static_assert(std::is_same<PersistCfgs<bf16_t>::Main, DmaExpert>::value &&
+                  std::is_same<PersistCfgs<bf16_t>::Rows128, DmaExpert128>::value &&
+                  std::is_same<PersistCfgs<bf16_t>::Decode, DmaDecode>::value,
+              "one set of tile shapes");
+
 // Compute units of the current device (the persistent kernels launch one
 // block per CU), queried once per device and cached.
 constexpr int kMaxDevices = 64;
@@ -90,8 +102,8 @@ bool use_rows128(int kind, int P, int E, int H, int I, int cus) {
 
 }  // namespace
 
-int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool bf16, int cus) {
-  if (!bf16) return CfgF32::BM;
+int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool half, int cus) {
+  if (!half) return CfgF32::BM;
   if (cus <= 0) cus = num_cus();
   if ((kind == EG_GATE_UP_FWD || kind == EG_DOWN_FWD) && (int64_t)P <= (int64_t)kDecodeRowsPerExpert * E)
     return DmaDecode::BM;
@@ -104,12 +116,14 @@ hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C,
                            int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s) {
   const bool wgrad = kind == EG_DOWN_WGRAD || kind == EG_GATE_UP_WGRAD;
   if constexpr (sizeof(T) == 2) {
+    typedef PersistCfgs<T> Cfgs;
     const int rows = expert_gemm_tile_rows(kind, P, E, H, I, true, num_cus());
-    if (rows == DmaDecode::BM)
-      return expert_gemm_persist_fwd<DmaDecode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
-    if (rows == DmaExpert128::BM)
-      return expert_gemm_persist_rows<DmaExpert128>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus(), s);
-    return expert_gemm_persist<DmaExpert, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
+    if (rows == Cfgs::Decode::BM)
+      return expert_gemm_persist_fwd<typename Cfgs::Decode>(kind, A, B, C, C2, offs, P, E, H, I, xg, num_cus(), s);
+    if (rows == Cfgs::Rows128::BM)
+      return expert_gemm_persist_rows<typename Cfgs::Rows128>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus(),
+                                                               s);
+    return expert_gemm_persist<typename Cfgs::Main, Tw>(kind, A, B, aux, C, C2, Cw, offs, P, E, H, I, xg, num_cus(), s);
   } else {
     static_assert(std::is_same<T, Tw>::value, "fp32 operands give fp32 weight gradients");
     return expert_gemm<typename CfgFor<T>::type, T>(kind, A, B, aux, wgrad ? Cw : C, C2, offs, P, E, H, I, xg, s);
@@ -122,6 +136,12 @@ template hipError_t expert_gemm_run<bf16_t, bf16_t>(int, const bf16_t*, const bf
 template hipError_t expert_gemm_run<bf16_t, float>(int, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, bf16_t*,
                                                    float*, const int32_t*, int, int, int, int, const ExpertGather&,
                                                    hipStream_t);
+template hipError_t expert_gemm_run<f16_t, f16_t>(int, const f16_t*, const f16_t*, const f16_t*, f16_t*, f16_t*,
+                                                  f16_t*, const int32_t*, int, int, int, int, const ExpertGather&,
+                                                  hipStream_t);
+template hipError_t expert_gemm_run<f16_t, float>(int, const f16_t*, const f16_t*, const f16_t*, f16_t*, f16_t*,
+                                                  float*, const int32_t*, int, int, int, int, const ExpertGather&,
+                                                  hipStream_t);
 template hipError_t expert_gemm_run<float, float>(int, const float*, const float*, const float*, float*, float*,
                                                   float*, const int32_t*, int, int, int, int, const ExpertGather&,
                                                   hipStream_t);

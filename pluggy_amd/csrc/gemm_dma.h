@@ -32,9 +32,12 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 
 // MINB: blocks per CU the register allocation must allow (launch bounds).
-template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1>
+// Tc: the 16-bit operand format (bf16_t or f16_t; the persistent engine
+// serves both, the kernel in this file bf16 only).
+template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1, typename Tc_ = bf16_t>
 struct DmaCfg {
-  typedef bf16_t Tc;
+  typedef Tc_ Tc;
+  static_assert(std::is_same<Tc_, bf16_t>::value || std::is_same<Tc_, f16_t>::value, "16-bit operand format");
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, BK = BK_, MINB = MINB_;
   static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
   static constexpr int NW = WAVES_M * WAVES_N;
@@ -287,13 +290,35 @@ template <> struct Out8<bf16_t> {
   }
   __device__ static __forceinline__ void store(bf16_t* p, const float* v) { *reinterpret_cast<u32x4*>(p) = pack(v); }
 };
+template <> struct Out8<f16_t> {
+  __device__ static __forceinline__ u32x4 pack(const float* v) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = cvt_pk_f16(v[2 * i], v[2 * i + 1]);
+    return w;
+  }
+  __device__ static __forceinline__ void store(f16_t* p, const float* v) { *reinterpret_cast<u32x4*>(p) = pack(v); }
+};
 template <> struct Out8<float> {
   __device__ static __forceinline__ void store(float* p, const float* v) { Vec8<float>::store(p, v); }
 };
 
+// 8 packed 16-bit values (format T16) to fp32.
+template <typename T16 = bf16_t>
 __device__ __forceinline__ void unpack8(const u32x4& w, float* v) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { v[2 * i] = bf16lo(w[i]); v[2 * i + 1] = bf16hi(w[i]); }
+  for (int i = 0; i < 4; ++i) { v[2 * i] = Fmt16<T16>::lo(w[i]); v[2 * i + 1] = Fmt16<T16>::hi(w[i]); }
+}
+
+// One 32x32x16 MFMA on 16-bit fragments of format T16 (the fragments travel
+// as bf16x8 bit patterns through LDS and registers).
+template <typename T16>
+__device__ __forceinline__ f32x16 mfma16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  if constexpr (std::is_same<T16, f16_t>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Epilogue of the DMA engine. Each wave moves its accumulators to HBM one
@@ -427,6 +452,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SUM3 || (B_KC && Cfg::WN == 96), "EPI_SUM3: three 32-row pieces per wave");
+  static_assert(std::is_same<typename Cfg::Tc, bf16_t>::value, "this kernel computes bf16 operands");
 
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::SMEM_BYTES];
   __shared__ int s_scan[1025];

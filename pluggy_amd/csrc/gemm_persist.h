@@ -74,6 +74,8 @@ __device__ __forceinline__ void st16(void* p, const u32x4& v) {
 template <bool NT>
 __device__ __forceinline__ void st_out8(bf16_t* p, const float* v) { st16<NT>(p, Out8<bf16_t>::pack(v)); }
 template <bool NT>
+__device__ __forceinline__ void st_out8(f16_t* p, const float* v) { st16<NT>(p, Out8<f16_t>::pack(v)); }
+template <bool NT>
 __device__ __forceinline__ void st_out8(float* p, const float* v) {
   st16<NT>(p, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
   st16<NT>(p + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
@@ -132,7 +134,7 @@ __device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI
       Vec8<float>::load(stage + r * LD + c, v);
       const int off = (i * 32 + 8 * q + r) * ld_bytes + c * (int)sizeof(Tout);
       if constexpr (sizeof(Tout) == 2) {
-        __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(v), rs, off, 0, AUX);
+        __builtin_amdgcn_raw_buffer_store_b128(Out8<Tout>::pack(v), rs, off, 0, AUX);
       } else {
         const u32x4 lo = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
         const u32x4 hi = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])};
@@ -163,6 +165,7 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
   constexpr int MI = Cfg::MI, NI = Cfg::NI, WM = Cfg::WM, WN = Cfg::WN;
   constexpr int LD = PersistLayout<Cfg>::EPI_LD;
   constexpr int CPR = WN / 8;
+  typedef typename Cfg::Tc T16;
   static_assert(WN == 64 && 8 * CPR == kWave, "one 8-column chunk per lane per 8-row slab, 64-column partials");
   constexpr int NSLAB = MI * 4, PF = 2;  // slabs per wave, slabs loaded ahead
   const int row0 = __builtin_amdgcn_readfirstlane(ti.m0 + wm * WM);  // uniform: scalar descriptors
@@ -170,10 +173,10 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
   const int col0 = __builtin_amdgcn_readfirstlane(ti.n0 + wn * WN);
   const int r = lane / CPR, c = (lane % CPR) * 8;
   const int ldaux = (int)p.ldaux, ldc = (int)p.ldc;
-  const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row0 * p.ldaux;
-  bf16_t* DG = reinterpret_cast<bf16_t*>(p.C) + (int64_t)row0 * p.ldc;
+  const T16* GU = reinterpret_cast<const T16*>(p.aux) + (int64_t)row0 * p.ldaux;
+  T16* DG = reinterpret_cast<T16*>(p.C) + (int64_t)row0 * p.ldc;
   const __amdgpu_buffer_rsrc_t rs_gu =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(GU), (short)0, rows * ldaux * 2, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T16*>(GU), (short)0, rows * ldaux * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_dg = __builtin_amdgcn_make_buffer_rsrc(DG, (short)0, rows * ldc * 2, 0x00020000);
   const bool has_w = p.row_w != nullptr, has_part = p.part != nullptr;
   const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(
@@ -206,8 +209,8 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
       for (int rr = 0; rr < 4; ++rr) stage[(4 * half + rr) * LD + j * 32 + col_l] = acc[i][j][4 * q + rr];
     float v[8], g[8], u[8], dg[8], du[8];
     Vec8<float>::load(stage + r * LD + c, v);
-    unpack8(pg[S % PF], g);
-    unpack8(pu[S % PF], u);
+    unpack8<T16>(pg[S % PF], g);
+    unpack8<T16>(pu[S % PF], u);
     const float ws = pw[S % PF];
     if constexpr (S + PF < NSLAB) fetch(std::integral_constant<int, S + PF>());
     float pd = 0.0f;
@@ -222,8 +225,8 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
     }
     constexpr int R0 = i * 32 + 8 * q;
     const int so = (R0 * ldc + col0) * 2;
-    __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(dg), rs_dg, vo_dg, so, AUX);
-    __builtin_amdgcn_raw_buffer_store_b128(Out8<bf16_t>::pack(du), rs_dg, vo_dg, so + (int)p.inter * 2, AUX);
+    __builtin_amdgcn_raw_buffer_store_b128(Out8<T16>::pack(dg), rs_dg, vo_dg, so, AUX);
+    __builtin_amdgcn_raw_buffer_store_b128(Out8<T16>::pack(du), rs_dg, vo_dg, so + (int)p.inter * 2, AUX);
     if (has_part) {  // the CPR = 8 lanes of a row are consecutive: sum them in a fixed order
       pd += __shfl_xor(pd, 1);
       pd += __shfl_xor(pd, 2);
@@ -275,8 +278,8 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             const int q0 = 4 * (QPS * hs + qq);
             const float v0 = acc[i][j][q0], v1 = acc[i][j][q0 + 1], v2 = acc[i][j][q0 + 2], v3 = acc[i][j][q0 + 3];
             const float r0 = swap_lane_pair(odd ? v0 : v2), r1 = swap_lane_pair(odd ? v1 : v3);
-            const uint32_t p0 = odd ? cvt_pk_bf16(r0, v2) : cvt_pk_bf16(v0, r0);
-            const uint32_t p1 = odd ? cvt_pk_bf16(r1, v3) : cvt_pk_bf16(v1, r1);
+            const uint32_t p0 = odd ? Fmt16<Tout>::pack2(r0, v2) : Fmt16<Tout>::pack2(v0, r0);
+            const uint32_t p1 = odd ? Fmt16<Tout>::pack2(r1, v3) : Fmt16<Tout>::pack2(v1, r1);
             const int row = 8 * qq + 4 * half + (odd ? 2 : 0);
             st32[row * LDW + j * 16 + (col_l >> 1)] = p0;
             st32[(row + 1) * LDW + j * 16 + (col_l >> 1)] = p1;
@@ -295,7 +298,7 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
       const int row_base = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * hs;
       if constexpr (EPI == EPI_SWIGLU) {
         constexpr int H2 = WN / 2, CPR = H2 / 8;
-        bf16_t* MID = reinterpret_cast<bf16_t*>(p.C2);
+        Tout* MID = reinterpret_cast<Tout*>(p.C2);
 #pragma unroll
         for (int e = lane; e < SLAB * CPR; e += 64) {
           const int r = e / CPR, c = (e % CPR) * 8;
@@ -307,8 +310,8 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             const u32x4 uw = *reinterpret_cast<const u32x4*>(st32 + r * LDW + H2 / 2 + c / 2);
             st16<NT>(C + (int64_t)row * p.ldc + col, gw);
             st16<NT>(C + (int64_t)row * p.ldc + p.inter + col, uw);
-            unpack8(gw, g);  // the activation uses the stored (rounded) pre-activations
-            unpack8(uw, u);
+            unpack8<Tout>(gw, g);  // the activation uses the stored (rounded) pre-activations
+            unpack8<Tout>(uw, u);
             const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;  // the routing weight
 #pragma unroll
             for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t] * ws;
@@ -331,16 +334,16 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
               if (col + 8 <= p.N) {
                 st16<NT>(C + (int64_t)row * p.ldc + col, w);
               } else {
-                unpack8(w, v);
+                unpack8<Tout>(w, v);
                 for (int t = 0; col + t < p.N; ++t) store_scalar<Tout>(C + (int64_t)row * p.ldc + col + t, v[t]);
               }
             } else if constexpr (EPI == EPI_SWIGLU_BWD) {
               // v = d(mid), or with row_w d(w * mid): then d(mid) = w v and d(w) += v . mid
               Vec8<float>::load(stage + r * LD + c, v);
-              const bf16_t* GU = reinterpret_cast<const bf16_t*>(p.aux) + (int64_t)row * p.ldaux;
+              const Tout* GU = reinterpret_cast<const Tout*>(p.aux) + (int64_t)row * p.ldaux;
               float g[8], u[8], dg[8], du[8];
-              Vec8<bf16_t>::load(GU + col, g);
-              Vec8<bf16_t>::load(GU + p.inter + col, u);
+              Vec8<Tout>::load(GU + col, g);
+              Vec8<Tout>::load(GU + p.inter + col, u);
               const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;
 #pragma unroll
               for (int t = 0; t < 8; ++t) {
@@ -351,8 +354,8 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
                 dg[t] = dm * u[t] * (sg + silu * (1.0f - sg));
                 du[t] = dm * silu;
               }
-              st_out8<NT>(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + col, dg);
-              st_out8<NT>(reinterpret_cast<bf16_t*>(C) + (int64_t)row * p.ldc + p.inter + col, du);
+              st_out8<NT>(C + (int64_t)row * p.ldc + col, dg);
+              st_out8<NT>(C + (int64_t)row * p.ldc + p.inter + col, du);
             } else {
               Vec8<float>::load(stage + r * LD + c, v);
               if (col + 8 <= p.N) {
@@ -502,6 +505,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // bf16 outputs stage packed (the SwiGLU backward reads its fp32 accumulators back)
   constexpr bool PACK = sizeof(Tout) == 2 && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
   static_assert(PACK || EPI != EPI_SWIGLU, "the SwiGLU forward stages packed bf16");
+  static_assert(sizeof(Tout) == 4 || std::is_same<Tout, typename Cfg::Tc>::value,
+                "16-bit outputs are in the operands' format");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");
@@ -802,8 +807,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     if constexpr (GM == GM_RED) __builtin_amdgcn_s_setprio(1);
     static_for<0, MI * NI>([&](auto mc) {
       constexpr int M = decltype(mc)::value;
-      acc[M / NI][M % NI] =
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
+      acc[M / NI][M % NI] = mfma16<typename Cfg::Tc>(af[M / NI], bfr[M % NI], acc[M / NI][M % NI]);
       if constexpr (kInterleaveFrags) {
         // the fragments left when this is the last MFMA (fewer MFMAs than fragments)
         constexpr int F1 = M + 1 < MI * NI ? M + 1 : MI + NI;
@@ -927,7 +931,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   wait_vmcnt<0>();  // the zero-reading DMAs past the last tile
 }
 
-template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = bf16_t, int GATH = G_NONE>
+// Tout defaults to the configuration's 16-bit operand format.
+template <class Cfg, bool A_KC, bool B_KC, int GM, int EPI, typename Tout = typename Cfg::Tc, int GATH = G_NONE>
 hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) {
   if (p.groups > 1024) return hipErrorInvalidValue;
   const int grid = num_cus > 0 ? num_cus : 256;
@@ -937,16 +942,16 @@ hipError_t launch_gemm_persist(const GemmParams& p, int num_cus, hipStream_t s) 
 }
 
 // The two forward expert GEMMs on the persistent kernel (the tile shapes used
-// for few-token batches serve the forward only).
-template <class Cfg>
-hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, bf16_t* C, bf16_t* C2,
-                                   const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
-                                   int num_cus, hipStream_t s) {
-  GemmParams p = expert_params<bf16_t>(kind, A, B, nullptr, C, C2, offs, P, E, H, I, xg);
+// for few-token batches serve the forward only). Operands and outputs are in
+// the configuration's 16-bit format T16.
+template <class Cfg, typename T16 = typename Cfg::Tc>
+hipError_t expert_gemm_persist_fwd(int kind, const T16* A, const T16* B, T16* C, T16* C2, const int32_t* offs, int P,
+                                   int E, int H, int I, const ExpertGather& xg, int num_cus, hipStream_t s) {
+  GemmParams p = expert_params<T16>(kind, A, B, nullptr, C, C2, offs, P, E, H, I, xg);
   switch (kind) {
     case EG_GATE_UP_FWD:
       if (p.a_index != nullptr)
-        return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+        return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, T16, GA_ROWS>(p, num_cus, s);
       return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
     case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
   }
@@ -956,19 +961,19 @@ hipError_t expert_gemm_persist_fwd(int kind, const bf16_t* A, const bf16_t* B, b
 // The row-grouped expert GEMMs (forward and dgrad) on the persistent kernel;
 // a tile shape that serves only them (the weight gradients' k-row gathers
 // take 256-row tiles) is instantiated through this alone.
-template <class Cfg>
-hipError_t expert_gemm_persist_rows(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C,
-                                    bf16_t* C2, const int32_t* offs, int P, int E, int H, int I,
-                                    const ExpertGather& xg, int num_cus, hipStream_t s) {
+template <class Cfg, typename T16 = typename Cfg::Tc>
+hipError_t expert_gemm_persist_rows(int kind, const T16* A, const T16* B, const T16* aux, T16* C, T16* C2,
+                                    const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
+                                    int num_cus, hipStream_t s) {
   GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);
   const bool gath = xg.index != nullptr;
   switch (kind) {
     case EG_GATE_UP_FWD:
-      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, bf16_t, GA_ROWS>(p, num_cus, s);
+      if (gath) return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU, T16, GA_ROWS>(p, num_cus, s);
       return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_SWIGLU>(p, num_cus, s);
     case EG_DOWN_FWD: return launch_gemm_persist<Cfg, true, true, GM_ROWS, EPI_STORE>(p, num_cus, s);
     case EG_DOWN_DGRAD:
-      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, bf16_t, GA_ROWS>(p, num_cus, s);
+      if (gath) return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD, T16, GA_ROWS>(p, num_cus, s);
       return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_SWIGLU_BWD>(p, num_cus, s);
     case EG_GATE_UP_DGRAD: return launch_gemm_persist<Cfg, true, false, GM_ROWS, EPI_STORE>(p, num_cus, s);
   }
@@ -976,12 +981,13 @@ hipError_t expert_gemm_persist_rows(int kind, const bf16_t* A, const bf16_t* B, 
 }
 
 // The six expert GEMMs on the persistent kernel; Tw is the weight gradients'
-// type (bf16, or fp32 for fp32 master weights: the accumulators stored
-// unrounded). A gathered operand takes the GATH instance of its GEMM.
-template <class Cfg, typename Tw = bf16_t>
-hipError_t expert_gemm_persist(int kind, const bf16_t* A, const bf16_t* B, const bf16_t* aux, bf16_t* C, bf16_t* C2,
-                               Tw* Cw, const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg,
-                               int num_cus, hipStream_t s) {
+// type (the operands' 16-bit format, or fp32 for fp32 master weights: the
+// accumulators stored unrounded). A gathered operand takes the GATH instance
+// of its GEMM.
+template <class Cfg, typename Tw = typename Cfg::Tc, typename T16 = typename Cfg::Tc>
+hipError_t expert_gemm_persist(int kind, const T16* A, const T16* B, const T16* aux, T16* C, T16* C2, Tw* Cw,
+                               const int32_t* offs, int P, int E, int H, int I, const ExpertGather& xg, int num_cus,
+                               hipStream_t s) {
   if (kind != EG_DOWN_WGRAD && kind != EG_GATE_UP_WGRAD)
     return expert_gemm_persist_rows<Cfg>(kind, A, B, aux, C, C2, offs, P, E, H, I, xg, num_cus, s);
   GemmParams p = expert_params(kind, A, B, aux, C, C2, offs, P, E, H, I, xg);

@@ -11,9 +11,9 @@
 
 namespace pmoe {
 
-// ---- grouped expert GEMMs (gemm.hip). T = bf16_t or float (activation
-// dtype); Tw: the weight gradients' type (EG_*_WGRAD; fp32 with bf16
-// operands for fp32 master weights). offs: (E,) int32 inclusive end row of each
+// ---- grouped expert GEMMs (gemm.hip). T = bf16_t, f16_t or float
+// (activation dtype); Tw: the weight gradients' type (EG_*_WGRAD; fp32 with
+// 16-bit operands for fp32 master weights). offs: (E,) int32 inclusive end row of each
 // expert in the sorted order. Operands per kind (see ExpertGemm): A, B, aux,
 // C, C2 (gate_up forward: mid), Cw (weight gradients); xg: gathers and
 // routing weights.
@@ -21,10 +21,10 @@ template <typename T, typename Tw>
 hipError_t expert_gemm_run(int kind, const T* A, const T* B, const T* aux, T* C, T* C2, Tw* Cw, const int32_t* offs,
                            int P, int E, int H, int I, const ExpertGather& xg, hipStream_t s);
 
-// Rows of the tiles expert_gemm_run gives GEMM `kind` (32, 128 or 256 for bf16
-// operands, the register-staged engine's for fp32) on `cus` compute units
-// (<= 0: the current device's).
-int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool bf16, int cus);
+// Rows of the tiles expert_gemm_run gives GEMM `kind` (32, 128 or 256 for
+// 16-bit operands, half = true; the register-staged engine's for fp32) on `cus`
+// compute units (<= 0: the current device's).
+int expert_gemm_tile_rows(int kind, int P, int E, int H, int I, bool half, int cus);
 
 // ---- router GEMMs in fp32 arithmetic (gemm.hip). TX: x dtype, TW: router weight dtype.
 template <typename TX, typename TW>
@@ -79,11 +79,11 @@ hipError_t count_invalid_ids(const int64_t* idx, int64_t n, int64_t E, int32_t* 
 // Stable counting-sort permutation of the T*K pairs by expert; with
 // sorted_token non-null it also writes the expert GEMMs' row tables
 // (sorted_token[p] = sorted_pair[p] / K, sorted_w[p] = float(w[sorted_pair[p]]),
-// w bf16 when w_bf16 else fp32; sorted_w may be null).
+// w fp32, bf16 or fp16 for w_code 0, 1, 2; sorted_w may be null).
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
                          int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s,
                          int32_t* sorted_token = nullptr, float* sorted_w = nullptr, const void* w = nullptr,
-                         int w_bf16 = 0);
+                         int w_code = 0);
 template <typename T>
 hipError_t dispatch_rows(const T* x, const int32_t* inv_pos, int T_, int K, int H, T* x_perm, hipStream_t s);
 template <typename T, typename TW>

@@ -461,13 +461,14 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int32_t* __restrict_
 }
 
 // The expert GEMMs' row tables of sorted row p (pair q): sorted_token[p] =
-// q / K and sorted_w[p] = float(w[q]) (w bf16 or fp32; sorted_w may be NULL).
+// q / K and sorted_w[p] = float(w[q]) (w fp32, bf16 or fp16 by w_code 0, 1, 2;
+// sorted_w may be NULL).
 // With sorted_token NULL the permutation writes no tables.
 struct RowTables {
   int32_t* sorted_token = nullptr;
   float* sorted_w = nullptr;
   const void* w = nullptr;
-  int w_bf16 = 0;
+  int w_code = 0;
   int K = 1;
 };
 
@@ -475,8 +476,9 @@ __device__ __forceinline__ void write_row_tables(const RowTables& rt, int pos, i
   if (rt.sorted_token != nullptr) {
     rt.sorted_token[pos] = q / rt.K;
     if (rt.sorted_w != nullptr)
-      rt.sorted_w[pos] = rt.w_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(rt.w)[q])
-                                   : static_cast<const float*>(rt.w)[q];
+      rt.sorted_w[pos] = rt.w_code == 1   ? bf16_to_f32(static_cast<const bf16_t*>(rt.w)[q])
+                         : rt.w_code == 2 ? (float)static_cast<const f16_t*>(rt.w)[q]
+                                          : static_cast<const float*>(rt.w)[q];
   }
 }
 
@@ -920,7 +922,7 @@ hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out,
 
 hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* counts, int32_t* offs,
                          int32_t* sorted_pair, int32_t* inv_pos, int32_t* chunk_hist, int chunk, hipStream_t s,
-                         int32_t* sorted_token, float* sorted_w, const void* w, int w_bf16) {
+                         int32_t* sorted_token, float* sorted_w, const void* w, int w_code) {
   const int P = T * K;
   const int nchunks = (P + chunk - 1) / chunk;
   if (E > 1024 || E < 1) return hipErrorInvalidValue;
@@ -930,7 +932,7 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   rt.sorted_token = sorted_token;
   rt.sorted_w = sorted_w;
   rt.w = w;
-  rt.w_bf16 = w_bf16;
+  rt.w_code = w_code;
   rt.K = K;
   if (nchunks <= 1) {
     hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits, counts,
@@ -1000,6 +1002,7 @@ hipError_t sort_rows(const int32_t* sorted_pair, const TW* w, int P, int K, int3
 }
 template hipError_t sort_rows<float>(const int32_t*, const float*, int, int, int32_t*, float*, hipStream_t);
 template hipError_t sort_rows<bf16_t>(const int32_t*, const bf16_t*, int, int, int32_t*, float*, hipStream_t);
+template hipError_t sort_rows<f16_t>(const int32_t*, const f16_t*, int, int, int32_t*, float*, hipStream_t);
 
 // The routing weights' gradient from the per-row partials of the down
 // backward: grad_w[q] = sum_j part[inv_pos[q] * ld + j] (j ascending, fp32).
@@ -1026,6 +1029,7 @@ hipError_t pair_weight_grad(const float* part, int ld, int nparts, const int32_t
 }
 template hipError_t pair_weight_grad<float>(const float*, int, int, const int32_t*, int, float*, hipStream_t);
 template hipError_t pair_weight_grad<bf16_t>(const float*, int, int, const int32_t*, int, bf16_t*, hipStream_t);
+template hipError_t pair_weight_grad<f16_t>(const float*, int, int, const int32_t*, int, f16_t*, hipStream_t);
 
 // Calls F with the compile-time top-k (the common values) or 0 (runtime K).
 template <class F>
@@ -1128,6 +1132,8 @@ template hipError_t router_topk<bf16_t>(const float*, int, int64_t, int64_t, flo
                                         bf16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_topk<float>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
                                        float*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
+template hipError_t router_topk<f16_t>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
+                                       f16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
                                            int, int, int, int, float*, bf16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
@@ -1135,19 +1141,17 @@ template hipError_t router_dlogits<float>(const float*, const int64_t*, const fl
 template hipError_t reduce_partials<float>(const float*, int, int64_t, float*, hipStream_t);
 template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*, hipStream_t);
 
+#define PMOE_INST_COMBINE(T, TW)                                                                                \
+  template hipError_t combine_rows<T, TW>(const T*, const TW*, const int32_t*, int, int, int, T*, hipStream_t);     \
+  template hipError_t combine_rows_bwd<T, TW>(const T*, const T*, const TW*, const int32_t*, int, int, int, T*, TW*, \
+                                              hipStream_t);
 #define PMOE_INST_ROWS(T)                                                                                      \
   template hipError_t dispatch_rows<T>(const T*, const int32_t*, int, int, int, T*, hipStream_t);              \
   template hipError_t dispatch_rows_bwd<T>(const T*, const int32_t*, const T*, int, int, int, T*, hipStream_t); \
-  template hipError_t combine_rows<T, bf16_t>(const T*, const bf16_t*, const int32_t*, int, int, int, T*,      \
-                                              hipStream_t);                                                    \
-  template hipError_t combine_rows<T, float>(const T*, const float*, const int32_t*, int, int, int, T*,        \
-                                             hipStream_t);                                                     \
-  template hipError_t combine_rows_bwd<T, bf16_t>(const T*, const T*, const bf16_t*, const int32_t*, int, int, \
-                                                  int, T*, bf16_t*, hipStream_t);                              \
-  template hipError_t combine_rows_bwd<T, float>(const T*, const T*, const float*, const int32_t*, int, int,   \
-                                                 int, T*, float*, hipStream_t);
+  PMOE_INST_COMBINE(T, bf16_t) PMOE_INST_COMBINE(T, f16_t) PMOE_INST_COMBINE(T, float)
 
 PMOE_INST_ROWS(bf16_t)
+PMOE_INST_ROWS(f16_t)
 PMOE_INST_ROWS(float)
 
 #define PMOE_INST_RES(T, TW, TR)                                                                                  \

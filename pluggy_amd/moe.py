@@ -119,32 +119,46 @@ def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
     returns its outputs in the input's dtype as the reference does. (torch's
     ``F.grouped_mm`` is not on autocast's bf16 list, so with an fp32 residual
     stream the reference's expert GEMMs actually run in fp32; this build keeps
-    the stated bf16 intent.) The kernels compute in bf16 or fp32 only: under
-    fp16 autocast they take fp32 operands (at least fp16's precision), and the
-    outputs keep the input's dtype.
+    the stated bf16 intent.) Under fp16 autocast the expert path takes fp16
+    operands likewise (fp16 MFMAs, fp32 accumulation); the router takes fp32
+    ones (``_router_x``, ``_router_operand``). Any other autocast dtype gives
+    fp32 operands.
     """
     if t.is_cuda and torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
-        return torch.bfloat16 if dt == torch.bfloat16 else torch.float32
+        return dt if dt in (torch.bfloat16, torch.float16) else torch.float32
     return None
 
 
 def _compute_dtype(t: torch.Tensor) -> torch.dtype:
-    """The dtype the kernels compute in for activations ``t``: autocast's (see
-    ``_amp_dtype``), else ``t``'s own when it is bf16 or fp32, else fp32 (an
-    fp16 tensor is computed in fp32 and the result cast back)."""
+    """The dtype the expert kernels compute in for activations ``t``:
+    autocast's (see ``_amp_dtype``), else ``t``'s own when it is bf16, fp16 or
+    fp32, else fp32 (e.g. an fp64 tensor, computed in fp32 and cast back).
+    bf16 and fp16 run on the 16-bit MFMAs with fp32 accumulation, as the
+    reference's ``F.grouped_mm`` runs them (moe.py:113-119)."""
     amp = _amp_dtype(t)
     if amp is not None:
         return amp
-    return t.dtype if t.dtype in (torch.bfloat16, torch.float32) else torch.float32
+    return t.dtype if t.dtype in (torch.bfloat16, torch.float16, torch.float32) else torch.float32
+
+
+def _router_x(x: torch.Tensor) -> torch.Tensor:
+    """The router's input as its kernels take it: fp32 or bf16 as given, and an
+    fp16 input in fp32 (exact). The router's logits are fp32 arithmetic in
+    every case; its input gradient comes back in fp32 and is rounded to fp16
+    where it joins the experts' fp16 input gradient."""
+    return x.float() if x.dtype == torch.float16 else x
 
 
 def _router_operand(w: torch.Tensor, amp: torch.dtype | None) -> torch.Tensor:
     """The router weight as the kernels take it: bf16 under bf16 autocast (as
-    the reference's ``F.linear`` there), else fp32 or bf16 as given (fp32 for
-    any other dtype)."""
+    the reference's ``F.linear`` there), its fp16 rounding in fp32 under fp16
+    autocast (the router's kernels take fp32 and bf16), else fp32 or bf16 as
+    given (fp32 for any other dtype, fp16 included)."""
     if amp == torch.bfloat16:
         w = w.to(torch.bfloat16)
+    elif amp == torch.float16:
+        w = w.to(torch.float16).float()
     elif w.dtype not in (torch.float32, torch.bfloat16):
         w = w.float()
     return w.contiguous()
@@ -172,15 +186,15 @@ def _pad_experts(gate_up_proj: torch.Tensor, down_proj: torch.Tensor, Hp: int, I
     return torch.cat([gate, up], dim=1), F.pad(down_proj, (0, Ip - I, 0, Hp - H))
 
 
-# bf16 copies of fp32 master weights kept across calls (see weight_cast_cache):
-# id(master) -> (weakref to the master, (version, data_ptr, shape, stride), copy)
+# 16-bit copies of fp32 master weights kept across calls (see weight_cast_cache):
+# (id(master), dtype) -> (weakref to the master, (version, data_ptr, shape, stride), copy)
 _cast_cache: dict[int, tuple] = {}
 _cast_cache_on = False
 
 
 @contextlib.contextmanager
 def weight_cast_cache(enabled: bool = True):
-    """Reuse the bf16 copies of fp32 master expert weights across calls.
+    """Reuse the bf16 (or fp16) copies of fp32 master expert weights across calls.
 
     Under bf16 autocast the kernels take bf16 copies of fp32 master weights,
     as the reference casts them on every call (moe.py:110-112); its trainer
@@ -206,14 +220,14 @@ def weight_cast_cache(enabled: bool = True):
             _cast_cache.clear()
 
 
-def _cached_bf16(w: torch.Tensor) -> torch.Tensor:
-    key = id(w)
+def _cached_copy(w: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    key = (id(w), dt)
     state = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()))
     hit = _cast_cache.get(key)
     if hit is not None and hit[0]() is w and hit[1] == state:
         return hit[2]
     with torch.no_grad():
-        copy = w.detach().to(torch.bfloat16).contiguous()
+        copy = w.detach().to(dt).contiguous()
     _cast_cache[key] = (weakref.ref(w, lambda _r, k=key: _cast_cache.pop(k, None)), state, copy)
     return copy
 
@@ -221,17 +235,19 @@ def _cached_bf16(w: torch.Tensor) -> torch.Tensor:
 def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, torch.Tensor | None]:
     """-> (the weight in the kernels' dtype, its fp32 master or None).
 
-    An fp32 master weight that feeds bf16 kernels (autocast training) is cast
-    outside autograd and passed to the op beside its bf16 copy. The op's
-    backward then writes the master's gradient in fp32 straight from the
-    weight-gradient GEMM, with no bf16 gradient and no cast kernel between.
+    An fp32 master weight that feeds 16-bit kernels (autocast training) is
+    cast outside autograd and passed to the op beside its bf16 (or fp16) copy.
+    The op's backward then writes the master's gradient in fp32 straight from
+    the weight-gradient GEMM, with no 16-bit gradient and no cast kernel
+    between.
     Inside ``weight_cast_cache`` the copy of a leaf master is reused while
     the master is unchanged. Otherwise the cast, if any, is an ordinary
     differentiable one.
     """
-    if w.dtype == torch.float32 and dt == torch.bfloat16 and w.requires_grad and torch.is_grad_enabled():
+    half = dt in (torch.bfloat16, torch.float16)
+    if w.dtype == torch.float32 and half and w.requires_grad and torch.is_grad_enabled():
         if _cast_cache_on and w.is_leaf and not torch.compiler.is_compiling():
-            return _cached_bf16(w), w
+            return _cached_copy(w, dt), w
         with torch.no_grad():
             return w.detach().to(dt).contiguous(), w
     return w.to(dtype=dt).contiguous(), None
@@ -351,7 +367,7 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     require_gpu(hidden, weight, logit_bias)
     amp = _amp_dtype(hidden)
     H = hidden.shape[1]
-    x = _pad_last(hidden.to(_compute_dtype(hidden)), _pad8(H)).contiguous()
+    x = _pad_last(_router_x(hidden.to(_compute_dtype(hidden))), _pad8(H)).contiguous()
     w = _pad_last(_router_operand(weight, amp), _pad8(H)).contiguous()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
@@ -575,7 +591,7 @@ def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_
     """
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-            x, router_weight, top_k, norm_topk_prob, logit_bias)
+            _router_x(x), router_weight, top_k, norm_topk_prob, logit_bias, tw_dtype=x.dtype)
     out, offs, inv_pos, stok, sw, gu, mid = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
     return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid
 
@@ -627,8 +643,9 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
         g_tw = _none_if_empty(g_tw)
     gx_router = None
     if need[0] or need[1]:
-        gx_router, g_rw = torch.ops.pmoe.router_bwd(x, rw, logits, top_i, top_w32, g_tw, g_logits,
+        gx_router, g_rw = torch.ops.pmoe.router_bwd(_router_x(x), rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
+        gx_router = gx_router.to(x.dtype)  # an fp16 block's router works in fp32
     if g_gu is not None and (need[0] or need_gu or need_dn):
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
             g_gu, g_out, x, gate_up, down, offs, inv_pos, stok, mid, gx_router if need[0] else None, K,
@@ -702,7 +719,7 @@ def moe_expert_ffn(
     I = gate_up_proj.shape[1] // 2
     Hp, Ip = _pad8(H), _pad8(I)
     gu, gu_master, dn, dn_master = _expert_weights(gate_up_proj, down_proj, dt, Hp, Ip)
-    tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16) else top_weights.float()
+    tw = top_weights if top_weights.dtype in (torch.float32, torch.bfloat16, torch.float16) else top_weights.float()
     out = torch.ops.pmoe.expert_ffn_fwd(_pad_last(hidden.to(dt), Hp).contiguous(),
                                         top_indices.to(torch.int64).contiguous(), tw.contiguous(), gu, dn,
                                         gu_master, dn_master)[0]
@@ -878,10 +895,12 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     require_gpu(x)
     assert isinstance(norm, torch.nn.RMSNorm) and tuple(norm.normalized_shape) == (H,) and norm.weight is not None
     I = mlp.experts.gate_up_proj.shape[1] // 2
-    if H > 16384 or H % 8 or I % 8 or x.dtype not in (torch.float32, torch.bfloat16):
+    if (H > 16384 or H % 8 or I % 8 or x.dtype not in (torch.float32, torch.bfloat16)
+            or _compute_dtype(x) == torch.float16):
         # the fused backward's row kernels take 16-byte rows of an fp32 or bf16
         # stream up to 16384 wide (beyond 4096 the rows are walked twice, with
-        # the norm-weight partials in LDS); other shapes take the unfused path
+        # the norm-weight partials in LDS) and bf16 or fp32 expert rows; other
+        # shapes and fp16 experts take the unfused path
         return x + mlp(norm(x))
     r = mlp.router
     flat = x.reshape(B * S, H).contiguous()

@@ -17,14 +17,16 @@ def _dims(gate_up_proj: torch.Tensor):
     return E, H, two_i // 2
 
 
-def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bias=None):
-    """-> logits, top_w (x.dtype), top_i (int64), top_w_f32, counts (int32), prob_sum, lse_sq_sum."""
+def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bias=None, tw_dtype=None):
+    """-> logits, top_w (tw_dtype, default x.dtype), top_i (int64), top_w_f32, counts (int32), prob_sum,
+    lse_sq_sum."""
     require_gpu(x, weight, logit_bias)
     T, H = x.shape
     E = weight.shape[0]
     dev = x.device
+    tw_dtype = x.dtype if tw_dtype is None else tw_dtype
     logits = torch.empty(T, E, dtype=torch.float32, device=dev)
-    top_w = torch.empty(T, top_k, dtype=x.dtype, device=dev)
+    top_w = torch.empty(T, top_k, dtype=tw_dtype, device=dev)
     top_i = torch.empty(T, top_k, dtype=torch.int64, device=dev)
     top_w32 = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     counts = torch.empty(E, dtype=torch.int32, device=dev)
@@ -32,7 +34,7 @@ def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bia
     lse2 = torch.empty(1, dtype=torch.float32, device=dev)
     ws = workspace(size("pmoe_router_forward_workspace_size", T, H, E), dev)
     call("pmoe_router_forward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype), ptr(logit_bias),
-         T, H, E, top_k, int(norm_topk_prob), ptr(logits), ptr(top_w), dtype_code(x.dtype), ptr(top_i),
+         T, H, E, top_k, int(norm_topk_prob), ptr(logits), ptr(top_w), dtype_code(tw_dtype), ptr(top_i),
          ptr(top_w32), ptr(counts), ptr(psum), ptr(lse2), ptr(ws), ws.numel(), stream_of(x))
     return logits, top_w, top_i, top_w32, counts, psum, lse2
 

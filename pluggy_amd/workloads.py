@@ -103,14 +103,14 @@ def mib(nbytes: float) -> float:
 
 def dispatch_bytes(cfg: MoEConfig) -> float:
     """Compulsory bytes of the row gather: read T*H, write P*H (+ int32 indices)."""
-    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    es = cfg.dtype.itemsize
     return cfg.tokens * cfg.hidden * es + cfg.pairs * cfg.hidden * es + cfg.pairs * 4
 
 
 def combine_bytes(cfg: MoEConfig) -> float:
     """Compulsory bytes of the combine: read the P weighted rows (P*H) and their
     positions (P int32), write T*H (the routing weight is already in the rows)."""
-    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    es = cfg.dtype.itemsize
     return cfg.pairs * cfg.hidden * es + cfg.pairs * 4 + cfg.tokens * cfg.hidden * es
 
 

@@ -395,7 +395,7 @@ def _run_config(cfg_id, tokens: int | None = None):
     ref = ref_layer_fp64(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"],
                          torch.from_numpy(idx), lg, cfg.norm_topk_prob,
                          gout=inp["grad_out"] if cfg.backward else None)
-    tol = 1e-2 if cfg.dtype == torch.bfloat16 else 1e-4
+    tol = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}[cfg.dtype]
     frac = MAX_ABS_FRAC[cfg.dtype]
     check_close("out", out, ref["out"], tol, frac)
     if cfg.backward:
@@ -443,6 +443,17 @@ def test_config2_qwen3_30b_a3b():
 
 def test_config4_skewed():
     _run_config(4)
+
+
+def test_config2_fp16():
+    """Config 2's layer with fp16 tensors (activations and expert weights): the
+    expert path on the fp16 MFMAs, the router on fp32 copies of x; every value
+    and gradient against fp64 at fp16's bar (rel-L2 2e-3)."""
+    import dataclasses
+
+    from pluggy_amd.workloads import CONFIGS
+
+    _run_config(dataclasses.replace(CONFIGS[2], name="qwen3-30b-a3b-fp16", dtype=torch.float16))
 
 
 def test_config_climbmix():

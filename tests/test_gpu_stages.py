@@ -2,7 +2,9 @@
 
 Integer work (permutation, selection, row gather) must be bit-exact. GEMM
 stages are compared with fp64 per-expert products: rel-L2 <= 1e-2 for bf16
-and <= 1e-5 for fp32 arithmetic; the max-abs error is
+<= 5e-4 for fp16 (its outputs are rounded to 11
+significant bits: RMS error about 1.4e-4, where a bf16 rounding by mistake
+would give about 1.1e-3) and <= 1e-5 for fp32 arithmetic; the max-abs error is
 printed next to each figure.
 """
 
@@ -18,7 +20,10 @@ from tests._gpu_helpers import (DEV, MAX_ABS_FRAC, check_close, gen, max_abs, re
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.bfloat16: 1e-2, torch.float32: 1e-5}
+TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-4, torch.float32: 1e-5}
+# row movers (one rounding of an fp32 sum) and the whole-operator comparisons
+ROW_TOL = {torch.bfloat16: 4e-3, torch.float16: 5e-4, torch.float32: 1e-6}
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
 
 
 def _ops():
@@ -47,8 +52,8 @@ def test_permute_bitexact(T, K, E, mode):
     assert np.array_equal(to_np(offs), ro)
     assert np.array_equal(to_np(sp), rsp)
     assert np.array_equal(to_np(inv), rinv)
-    # the one-pass form with the GEMMs' row tables (bf16 and fp32 weights, and none)
-    for wdt in (torch.bfloat16, torch.float32, None):
+    # the one-pass form with the GEMMs' row tables (bf16, fp16 and fp32 weights, and none)
+    for wdt in (torch.bfloat16, torch.float16, torch.float32, None):
         w = None if wdt is None else torch.rand(T, K, generator=gen(T)).to(wdt)
         c2, o2, sp2, inv2, tok, sw = _ops().permute_rows(idx.to(DEV), None if w is None else w.to(DEV), E)
         assert np.array_equal(to_np(c2), rc.astype(np.int32)) and np.array_equal(to_np(o2), ro)
@@ -71,7 +76,7 @@ def test_permute_deterministic():
 # ----------------------------------------------------------- row movement
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("T,K,E,H", [(300, 4, 16, 264), (64, 8, 128, 2048), (200, 3, 12, 520), (128, 8, 16, 4096)])
 def test_dispatch_combine(dtype, T, K, E, H):
     say(f"dispatch/combine T={T} K={K} E={E} H={H} {dtype}")
@@ -90,24 +95,24 @@ def test_dispatch_combine(dtype, T, K, E, H):
     inv_c = inv.cpu().long().view(T, K)
     ref = (w.double().unsqueeze(-1) * y.double()[inv_c]).sum(1)
     say(f"  combine rel={rel(out, ref):.2e} maxabs={max_abs(out, ref):.2e}")
-    assert rel(out, ref) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    assert rel(out, ref) < ROW_TOL[dtype]
     # combine backward
     go = torch.randn(T, H, generator=g).to(dtype)
     gy, gw = ops.combine_backward(go.to(DEV), y.to(DEV), w.to(DEV), inv)
     ref_gy = torch.zeros(T * K, H, dtype=torch.float64)
     ref_gy[inv_c.reshape(-1)] = (w.double().unsqueeze(-1) * go.double().unsqueeze(1)).reshape(T * K, H)
     ref_gw = (go.double().unsqueeze(1) * y.double()[inv_c]).sum(-1)
-    assert rel(gy, ref_gy) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
-    assert rel(gw, ref_gw) < (4e-3 if dtype == torch.bfloat16 else 1e-5)
+    assert rel(gy, ref_gy) < ROW_TOL[dtype]
+    assert rel(gw, ref_gw) < max(ROW_TOL[dtype], 1e-5)
     # dispatch backward: grad_x[t] = sum_k gxp[inv[t,k]]
     gxp = torch.randn(T * K, H, generator=g).to(dtype)
     gx = ops.dispatch_backward(gxp.to(DEV), inv, T, K)
     ref_gx = gxp.double()[inv_c].sum(1)
-    assert rel(gx, ref_gx) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    assert rel(gx, ref_gx) < ROW_TOL[dtype]
     # with an addend row (the router's share of the input gradient), summed first
     add = torch.randn(T, H, generator=g).to(dtype)
     gx2 = ops.dispatch_backward(gxp.to(DEV), inv, T, K, add=add.to(DEV))
-    assert rel(gx2, ref_gx + add.double()) < (4e-3 if dtype == torch.bfloat16 else 1e-6)
+    assert rel(gx2, ref_gx + add.double()) < ROW_TOL[dtype]
 
 
 # -------------------------------------------------------------- GEMMs
@@ -140,12 +145,13 @@ def test_gemm_cases_cover_both_row_tile_shapes():
     256-row tiles, so the stage tests below cover both shapes."""
     from pluggy_amd import _lib
 
-    q = lambda kind, T, K, E, H, I: _lib.load().pmoe_expert_gemm_tile_rows(  # noqa: E731
-        kind, T * K, E, H, I, _lib.PMOE_BF16, 0)
-    assert q(2, 8320, 1, 16, 2048, 768) == 128  # down dgrad at the EP=8 share
-    assert q(0, 8320, 1, 16, 2048, 768) == 256  # gate_up fwd there
-    assert q(0, 1024, 8, 8, 4096, 1536) == 256
-    assert q(0, 64, 8, 128, 2048, 768) == 32    # the decode shape's forward
+    for code in (_lib.PMOE_BF16, _lib.PMOE_F16):  # fp16 takes the same tiles
+        q = lambda kind, T, K, E, H, I: _lib.load().pmoe_expert_gemm_tile_rows(  # noqa: E731
+            kind, T * K, E, H, I, code, 0)
+        assert q(2, 8320, 1, 16, 2048, 768) == 128  # down dgrad at the EP=8 share
+        assert q(0, 8320, 1, 16, 2048, 768) == 256  # gate_up fwd there
+        assert q(0, 1024, 8, 8, 4096, 1536) == 256
+        assert q(0, 64, 8, 128, 2048, 768) == 32    # the decode shape's forward
 
 
 def _gemm_inputs(T, K, E, H, I, mode, dtype, seed=0):
@@ -160,7 +166,7 @@ def _gemm_inputs(T, K, E, H, I, mode, dtype, seed=0):
     return idx, x, wgu, wdn, offs, sp, inv, xp
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", GEMM_CASES)
 def test_gate_up_swiglu(dtype, case):
     T, K, E, H, I, mode = case
@@ -176,7 +182,7 @@ def test_gate_up_swiglu(dtype, case):
     check_close("mid", mid, ref_mid, TOL[dtype], MAX_ABS_FRAC[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", GEMM_CASES)
 def test_down_proj(dtype, case):
     T, K, E, H, I, mode = case
@@ -189,7 +195,7 @@ def test_down_proj(dtype, case):
     check_close("y", y, ref, TOL[dtype], MAX_ABS_FRAC[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", GEMM_CASES)
 def test_down_proj_backward(dtype, case):
     T, K, E, H, I, mode = case
@@ -215,7 +221,7 @@ def test_down_proj_backward(dtype, case):
         assert torch.count_nonzero(gdn[e]).item() == 0, "an empty expert has a zero weight gradient"
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", GEMM_CASES)
 def test_gate_up_backward(dtype, case):
     T, K, E, H, I, mode = case
@@ -232,16 +238,17 @@ def test_gate_up_backward(dtype, case):
     check_close("d gate_up_proj", gwgu, ref_gw, TOL[dtype], MAX_ABS_FRAC[dtype])
 
 
+@pytest.mark.parametrize("half", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", GEMM_CASES)
-def test_weight_gradients_in_fp32(case):
-    """bf16 operands, fp32 weight gradients (for fp32 master weights): the
-    unrounded accumulators of the same tiles, so rounding them gives the bf16
+def test_weight_gradients_in_fp32(case, half):
+    """16-bit operands, fp32 weight gradients (for fp32 master weights): the
+    unrounded accumulators of the same tiles, so rounding them gives the 16-bit
     entry point's output bit for bit, and they sit within fp32 summation error
     of the fp64 product."""
     T, K, E, H, I, mode = case
-    say(f"wgrad fp32 out {case}")
+    say(f"wgrad fp32 out {case} {half}")
     ops = _ops()
-    bf, f32 = torch.bfloat16, torch.float32
+    bf, f32 = half, torch.float32
     idx, x, wgu, wdn, offs, sp, inv, xp = _gemm_inputs(T, K, E, H, I, mode, bf)
     g = gen(8)
     P = T * K
@@ -262,7 +269,7 @@ def test_weight_gradients_in_fp32(case):
                 assert torch.count_nonzero(f32_out[e]).item() == 0, "an empty expert has a zero weight gradient"
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", GEMM_CASES)
 def test_gathered_rows_and_routing_weights(dtype, case):
     """The forward and backward GEMMs over rows gathered from token-major tensors
@@ -313,7 +320,7 @@ def test_gathered_rows_and_routing_weights(dtype, case):
     gxp, gwgu = ops.gate_up_backward(g2.to(DEV), x.to(DEV), wgu.to(DEV), offs, row_index=stok)
     check_close("d x_perm", gxp, ref_grouped(g2, wgu, o, trans_w=False), TOL[dtype], MAX_ABS_FRAC[dtype])
     check_close("d gate_up_proj (gathered)", gwgu, ref_wgrad(g2, x[tok], o), TOL[dtype], MAX_ABS_FRAC[dtype])
-    if dtype == torch.bfloat16:
+    if dtype != torch.float32:
         # fp32 weight gradients over gathered rows: the same tiles unrounded
         f32 = torch.float32
         gw32 = ops.gate_up_wgrad(g2.to(DEV), x.to(DEV), offs, E, f32, row_index=stok)
@@ -481,7 +488,7 @@ def test_router_backward(norm, x_dtype, T, H, E, K):
 # ------------------------------------------------- fused C entry points
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_fused_expert_ffn_entry_points(dtype):
     """pmoe_expert_ffn_forward/backward (the whole-operator C ABI) == the per-stage path, bitwise."""
     from pluggy_amd._lib import call, dtype_code, ptr, size, workspace
@@ -533,7 +540,7 @@ def test_fused_expert_ffn_entry_points(dtype):
     assert torch.equal(out, out_s)
     assert torch.equal(gx, xs.grad) and torch.equal(gw, ws_.grad)
     assert torch.equal(ggu, a.grad) and torch.equal(gdn, b.grad)
-    if dtype == torch.bfloat16:
+    if dtype != torch.float32:
         # weight gradients of fp32 masters: the unrounded accumulators of the same tiles
         ggu32 = torch.empty(wgu.shape, dtype=torch.float32, device=DEV)
         gdn32 = torch.empty(wdn.shape, dtype=torch.float32, device=DEV)
