@@ -545,7 +545,8 @@ def test_weight_cast_cache_reuses_copies_until_the_master_changes():
         with torch.no_grad():  # an optimizer-style in-place update bumps the version
             mlp.experts.gate_up_proj.mul_(0.5)
         third = step()
-        assert M._cast_cache[id(mlp.experts.gate_up_proj)][2] is not copies[id(mlp.experts.gate_up_proj)]
+        key = (id(mlp.experts.gate_up_proj), torch.bfloat16)  # copies are kept per master and dtype
+        assert M._cast_cache[key][2] is not copies[key]
     assert not M._cast_cache
     fresh = step()
     for a, b in zip(third, fresh):
