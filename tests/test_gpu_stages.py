@@ -328,6 +328,58 @@ def test_gathered_rows_and_routing_weights(dtype, case):
         assert torch.equal(gw32.to(dtype), gwgu) and torch.equal(gd32.to(dtype), gdn)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_epilogue_stores_stay_inside_the_rows(dtype):
+    """The epilogues write through buffer descriptors sized to a tile's valid
+    rows, with a slab's first row in the instruction's scalar offset: rows past
+    the last one must be dropped. One expert of 100 rows (one partial 256-row
+    tile) writes into buffers that hold 256 sentinel rows after the 100 the
+    call sees: the forward (gate_up pre-activations, the weighted SwiGLU, the
+    down rows) and the down dgrad with its routing-weight partials leave every
+    sentinel row as it was, and the 100 rows match fp64."""
+    from pluggy_amd._lib import call, dtype_code, ptr, stream_of
+
+    P, E, H, I, X = 100, 1, 256, 256, 256
+    say(f"epilogue bounds P={P} H={H} I={I} {dtype}")
+    g = gen(23)
+    dt = dtype_code(dtype)
+    nan = float("nan")
+    x = torch.randn(P + X, H, generator=g).to(dtype).to(DEV)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype).to(DEV)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype).to(DEV)
+    sw = torch.rand(P + X, generator=g).to(DEV)
+    offs = torch.tensor([P], dtype=torch.int32, device=DEV)
+    gu = torch.full((P + X, 2 * I), nan, dtype=dtype, device=DEV)
+    mid = torch.full((P + X, I), nan, dtype=dtype, device=DEV)
+    y = torch.full((P + X, H), nan, dtype=dtype, device=DEV)
+    call("pmoe_gate_up_swiglu", ptr(x), None, ptr(sw), P, ptr(wgu), ptr(offs), dt, P, E, H, I, ptr(gu), ptr(mid),
+         stream_of(x))
+    call("pmoe_down_proj", ptr(mid), ptr(wdn), ptr(offs), dt, P, E, H, I, ptr(y), stream_of(x))
+    gout = torch.randn(P + X, H, generator=g).to(dtype).to(DEV)
+    gu_in = gu.clone()
+    gu_in[P:] = torch.randn(X, 2 * I, generator=g).to(dtype).to(DEV)  # finite past the rows
+    ggu = torch.full((P + X, 2 * I), nan, dtype=dtype, device=DEV)
+    part = torch.full((P + X, 4), nan, device=DEV)
+    call("pmoe_down_proj_backward", ptr(gout), None, ptr(sw), P, None, ptr(gu_in), ptr(wdn), ptr(offs), dt, P, E, H,
+         I, ptr(ggu), None, dt, ptr(part), 4, stream_of(x))
+    torch.cuda.synchronize()
+    for name, t in (("gate_up_out", gu), ("mid", mid), ("y", y), ("d gate_up_out", ggu), ("partials", part)):
+        assert torch.isnan(t[P:]).all(), f"{name}: rows past the tile's last were written"
+        assert not torch.isnan(t[:P]).any(), f"{name}: a row was not written"
+    # the visible rows against fp64
+    x64, w64 = x[:P].double().cpu(), sw[:P].double().cpu().unsqueeze(1)
+    ref_gu = x64 @ wgu[0].double().cpu().T
+    check_close("gate_up_out", gu[:P], ref_gu, TOL[dtype], MAX_ABS_FRAC[dtype])
+    gq = gu[:P].double().cpu()
+    check_close("mid", mid[:P], w64 * silu64(gq[:, :I]) * gq[:, I:], TOL[dtype], MAX_ABS_FRAC[dtype])
+    check_close("y", y[:P], mid[:P].double().cpu() @ wdn[0].double().cpu().T, TOL[dtype], MAX_ABS_FRAC[dtype])
+    acc = gout[:P].double().cpu() @ wdn[0].double().cpu()
+    gate, up = gu_in[:P].double().cpu()[:, :I], gu_in[:P].double().cpu()[:, I:]
+    s_ = torch.sigmoid(gate)
+    ref_ggu = torch.cat([w64 * acc * up * s_ * (1 + gate * (1 - s_)), w64 * acc * gate * s_], dim=1)
+    check_close("d gate_up_out", ggu[:P], ref_ggu, TOL[dtype], MAX_ABS_FRAC[dtype])
+
+
 # Rows per expert with every kind of short last m-tile (1, 127, 128, 129 and
 # 255 rows of a 256-row tile), experts of under 128 rows (nothing but a short
 # tile), full experts (no last tile) and an empty expert.
