@@ -14,7 +14,7 @@ reference's own torch GPU path (F.grouped_mm) timed on the same GPU and
 inputs, the MoE half-block with and without the fused RMSNorm / residual add
 (``neighbours``), the other BASELINE.json configurations' steps (``decode``:
 config 5, ``config4``: skewed routing, ``config3``: the Qwen3-235B-A22B layer;
-``config2_fp16``: config 2 with fp16 tensors on the fp16 MFMAs; ``ep8_share``:
+``config2_fp16``: config 2 with fp16 tensors, router weight included, on the fp16 MFMAs; ``ep8_share``:
 one GPU's share at EP=8), the forward expert GEMMs against
 hipBLASLt's batched product on equal experts (``vendor_gemm``), and a CPU
 baseline (the restated reference CPU path) timed on this host.
@@ -333,7 +333,9 @@ def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=
     reports the routing's per-expert counts and its step time relative to
     config 2's (`base_ms`). `dtype`: the configuration with its activations and
     expert weights in that dtype instead (config 2 in fp16: the same draws
-    rounded to fp16)."""
+    rounded to fp16, the router weight included, as a module in fp16 holds
+    them: the reference's F.linear takes fp16 input only beside an fp16
+    weight)."""
     import dataclasses
 
     import torch
@@ -355,6 +357,8 @@ def layer_leg(cfg_id: int, dev, steps: int, warmup: int, base_inp=None, base_ms=
     else:
         inp = make_inputs(cfg, device=dev)
     mlp = pluggy_amd.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(dev)
+    if cfg.dtype == torch.float16:
+        mlp.router.to(torch.float16)
     with torch.no_grad():
         mlp.router.weight.copy_(inp["router_weight"])
     mlp.experts.gate_up_proj.data = inp["gate_up_proj"]

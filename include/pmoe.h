@@ -8,8 +8,9 @@
  *    PMOE_F16 (IEEE fp16). fp16 is taken by the expert path (permutation row
  *    tables, row movers, expert GEMMs, the whole-FFN entry points), which
  *    computes it on the fp16 MFMAs with fp32 accumulation as the reference's
- *    F.grouped_mm does for fp16 tensors; the router and the RMSNorm and
- *    residual neighbours take fp32 or bf16.
+ *    F.grouped_mm does for fp16 tensors; so is the router when its x and
+ *    weight are both fp16. The RMSNorm and residual neighbours take fp32 or
+ *    bf16.
  *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
  *    asynchronously; no entry point synchronises the host or allocates
  *    memory. Scratch memory comes from the caller through `workspace`, sized by
@@ -50,17 +51,19 @@ PMOE_API const char* pmoe_last_error_string(void);
 /* ---------------------------------------------------------------- router ---
  * Replaces Qwen3MoeTopKRouter.forward (pluggy/models/qwen3_moe/qwen3_moe.py:168-178):
  *   logits = x . W^T (+ logit_bias)  [fp32 arithmetic; for bf16 x the fp32 W is
- *   split into three bf16 pieces whose products with x are exact]
+ *   split into three bf16 pieces whose products with x are exact; fp16 x and
+ *   fp16 W multiply exactly on the fp16 MFMAs]
  *   p = softmax(logits) (fp32); top-k of logits (ties -> lower expert id)
  *   w = p[top] (/ sum p[top] when norm_topk_prob), written as tw_dtype and fp32.
  * Also emits the additive aux statistics of load_balancing_loss / router_z_loss
  * (qwen3_moe.py:285-316) and the per-expert counts of _update_expert_counts
  * (qwen3_moe.py:417-426): expert_counts[e] (int32), prob_sum[e] = sum_t p[t,e],
  * lse_sq_sum = sum_t logsumexp(logits[t])^2. Any of the three may be NULL.
- * x: (T,H) x_dtype; weight: (E,H) w_dtype (both fp32 or bf16); logit_bias:
- * (E,) fp32 or NULL; logits: (T,E) fp32; top_weights: (T,K) tw_dtype (fp32,
- * bf16 or fp16: an fp16 block runs its router on fp32 x and rounds the weights
- * to fp16 as the reference's .to(hidden_states.dtype), qwen3_moe.py:177);
+ * x: (T,H) x_dtype; weight: (E,H) w_dtype (each fp32 or bf16, or both fp16:
+ * the reference's F.linear under fp16 takes fp16 x and W, qwen3_moe.py:172);
+ * logit_bias: (E,) fp32 or NULL; logits: (T,E) fp32; top_weights: (T,K)
+ * tw_dtype (fp32, bf16 or fp16, rounded as the reference's
+ * .to(hidden_states.dtype), qwen3_moe.py:177);
  * top_indices: (T,K) int64; top_weights_f32: (T,K) fp32 (kept for the
  * backward). */
 PMOE_API size_t pmoe_router_forward_workspace_size(int64_t T, int64_t H, int64_t E);
@@ -74,8 +77,11 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
 /* Autograd of pmoe_router_forward (torch derivatives of qwen3_moe.py:172-177):
  *   dl = d(top_weights) through renorm/softmax/top-k (+ grad_logits)
  *   grad_x = dl . W  (x_dtype, overwritten),  grad_weight = dl^T . x (w_dtype).
- * grad_top_weights (T,K) gw_dtype and grad_logits (T,E) fp32 may be NULL
- * (zero); grad_x / grad_weight may be NULL (not needed). */
+ * dl is fp32; its products with x and W are formed exactly from 16-bit
+ * pieces of dl (two bf16 pieces; for fp16 x and W, grad_weight from two fp16
+ * pieces, which carry fp16's exponent range as the reference's fp16 dl does).
+ * grad_top_weights (T,K) gw_dtype (fp32, bf16 or fp16) and grad_logits (T,E)
+ * fp32 may be NULL (zero); grad_x / grad_weight may be NULL (not needed). */
 PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E);
 PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
                                   const float* logits, const int64_t* top_indices, const float* top_weights_f32,

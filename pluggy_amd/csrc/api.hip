@@ -138,8 +138,9 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
                                  float* prob_sum, float* lse_sq_sum, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype16_ok(tw_dtype),
-               "router_forward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16");
+  PMOE_REQUIRE(((dtype_ok(x_dtype) && dtype_ok(w_dtype)) || (x_dtype == PMOE_F16 && w_dtype == PMOE_F16)) &&
+                   dtype16_ok(tw_dtype),
+               "router_forward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, or both PMOE_F16");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_weights && top_indices && top_weights_f32),
                "router_forward: null tensor");
   const size_t need = pmoe_router_forward_workspace_size(T, H, E);
@@ -159,12 +160,19 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   // Logits in fp32 arithmetic. bf16 x: x is exact in bf16, so splitting an fp32
   // weight into three bf16 pieces makes every MFMA product exact; the GEMM's
   // epilogue adds the three pieces' fp32 accumulators in a fixed order, and the
-  // top-k kernel sums the split-K planes in order.
+  // top-k kernel sums the split-K planes in order. fp16 x and weight: fp16
+  // products are exact in fp32, one piece on the fp16 MFMAs.
   const float* lparts = logits;
   int nsplit = 1;
   int64_t sstride = 0;
   if (T > 0) {
-    if (x_dtype == PMOE_BF16) {
+    if (x_dtype == PMOE_F16) {
+      PMOE_TRY(router_logits_f16((const f16_t*)x, (const f16_t*)weight, t, h, e, splits, parts, s),
+               "router logits GEMM");
+      lparts = parts;
+      nsplit = splits;
+      sstride = (int64_t)T * E;
+    } else if (x_dtype == PMOE_BF16) {
       const bf16_t* wb = (const bf16_t*)weight;
       int npieces = 1;
       if (w_dtype == PMOE_F32) {
@@ -203,7 +211,8 @@ PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_
   const size_t fp32_path = align_up(T * ldl * sizeof(float)) + align_up(router_splits(T) * E * H * sizeof(float));
   const size_t bf16_path = align_up(T * 3 * ldl * sizeof(bf16_t)) + align_up(3 * ldl * H * sizeof(bf16_t)) +
                            align_up(2 * router_splits(T) * E * H * sizeof(float));
-  return std::max(fp32_path, bf16_path);
+  const size_t f16_path = bf16_path + align_up(T * 2 * ldl * sizeof(f16_t));
+  return std::max(fp32_path, f16_path);
 }
 
 PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
@@ -212,8 +221,9 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
                                   int64_t H, int64_t E, int64_t K, int norm_topk_prob, void* grad_x,
                                   void* grad_weight, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(dtype_ok(x_dtype) && dtype_ok(w_dtype) && dtype_ok(gw_dtype),
-               "router_backward: dtype codes must be PMOE_F32 or PMOE_BF16");
+  PMOE_REQUIRE(((dtype_ok(x_dtype) && dtype_ok(w_dtype)) || (x_dtype == PMOE_F16 && w_dtype == PMOE_F16)) &&
+                   dtype16_ok(gw_dtype),
+               "router_backward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, or both PMOE_F16");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_indices && top_weights_f32),
                "router_backward: null tensor");
   const size_t need = pmoe_router_backward_workspace_size(T, H, E);
@@ -228,9 +238,37 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
     // no tokens: dW = 0, written by the reduction kernel over zero partial
     // planes (a kernel write, not hipMemsetAsync, so a captured graph replays it)
     if (grad_weight) {
-      hipError_t st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(nullptr, 0, E * H, (bf16_t*)grad_weight, s)
-                                           : reduce_partials<float>(nullptr, 0, E * H, (float*)grad_weight, s);
+      hipError_t st = by_dtype16(w_dtype, [&](auto wp) {
+        typedef PMOE_ELEM(wp) W;
+        return reduce_partials<W>(nullptr, 0, E * H, (W*)grad_weight, s);
+      });
       PMOE_TRY(st, "router dW zero");
+    }
+    return PMOE_OK;
+  }
+  auto dlogits = [&](float* dl, bf16_t* dl3, f16_t* dl2) {
+    return by_dtype16(gw_dtype, [&](auto gp) {
+      typedef PMOE_ELEM(gp) G;
+      return router_dlogits<G>(logits, top_indices, top_weights_f32, (const G*)grad_top_weights, grad_logits, t, e,
+                               k, norm_topk_prob, dl, dl3, dl2, ldl, s);
+    });
+  };
+  if (x_dtype == PMOE_F16) {
+    // fp16 x and weight: dx from the bf16 planes of dl and the weight's bf16
+    // pieces W = W_hi + W_lo (exact for fp16), as below; dW from fp16 planes
+    // dl = dl_hi + dl_lo and the fp16 x on the fp16 MFMAs, every product exact.
+    bf16_t* dl3 = cv.take<bf16_t>((size_t)T * 3 * ldl);
+    bf16_t* w3t = cv.take<bf16_t>((size_t)3 * ldl * H);
+    float* partial = cv.take<float>((size_t)2 * splits * E * H);
+    f16_t* dl2 = cv.take<f16_t>((size_t)T * 2 * ldl);
+    PMOE_TRY(dlogits(nullptr, dl3, grad_weight ? dl2 : nullptr), "router dlogits");
+    if (grad_x) {
+      PMOE_TRY(split_router_weight_bwd<f16_t>((const f16_t*)weight, e, h, ldl, w3t, s), "router weight split");
+      PMOE_TRY(router_dx_bf16<f16_t>(dl3, ldl, w3t, t, h, (f16_t*)grad_x, s), "router dx GEMM");
+    }
+    if (grad_weight) {
+      PMOE_TRY(router_dw_f16(dl2, ldl, (const f16_t*)x, t, h, e, kRouterSplitChunk, partial, s), "router dW GEMM");
+      PMOE_TRY(reduce_partials<f16_t>(partial, 2 * splits, E * H, (f16_t*)grad_weight, s), "router dW reduce");
     }
     return PMOE_OK;
   }
@@ -240,17 +278,13 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
     bf16_t* dl3 = cv.take<bf16_t>((size_t)T * 3 * ldl);
     bf16_t* w3t = cv.take<bf16_t>((size_t)3 * ldl * H);
     float* partial = cv.take<float>((size_t)2 * splits * E * H);
-    hipError_t st = gw_dtype == PMOE_BF16
-                        ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32, (const bf16_t*)grad_top_weights,
-                                                 grad_logits, t, e, k, norm_topk_prob, nullptr, dl3, ldl, s)
-                        : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
-                                                grad_logits, t, e, k, norm_topk_prob, nullptr, dl3, ldl, s);
-    PMOE_TRY(st, "router dlogits");
+    PMOE_TRY(dlogits(nullptr, dl3, nullptr), "router dlogits");
+    hipError_t st;
     if (grad_x) {
       st = w_dtype == PMOE_F32 ? split_router_weight_bwd<float>((const float*)weight, e, h, ldl, w3t, s)
                                : split_router_weight_bwd<bf16_t>((const bf16_t*)weight, e, h, ldl, w3t, s);
       PMOE_TRY(st, "router weight split");
-      PMOE_TRY(router_dx_bf16(dl3, ldl, w3t, t, h, (bf16_t*)grad_x, s), "router dx GEMM");
+      PMOE_TRY(router_dx_bf16<bf16_t>(dl3, ldl, w3t, t, h, (bf16_t*)grad_x, s), "router dx GEMM");
     }
     if (grad_weight) {
       PMOE_TRY(router_dw_bf16(dl3, ldl, (const bf16_t*)x, t, h, e, kRouterSplitChunk, partial, s), "router dW GEMM");
@@ -263,12 +297,8 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
   // fp32 x: fp32 MFMA GEMMs on the fp32 dl
   float* dl = cv.take<float>((size_t)T * ldl);
   float* partial = cv.take<float>((size_t)splits * E * H);
-  hipError_t st = gw_dtype == PMOE_BF16
-                      ? router_dlogits<bf16_t>(logits, top_indices, top_weights_f32, (const bf16_t*)grad_top_weights,
-                                               grad_logits, t, e, k, norm_topk_prob, dl, nullptr, ldl, s)
-                      : router_dlogits<float>(logits, top_indices, top_weights_f32, (const float*)grad_top_weights,
-                                              grad_logits, t, e, k, norm_topk_prob, dl, nullptr, ldl, s);
-  PMOE_TRY(st, "router dlogits");
+  PMOE_TRY(dlogits(dl, nullptr, nullptr), "router dlogits");
+  hipError_t st;
   if (grad_x) {
     st = w_dtype == PMOE_F32
              ? router_dx_gemm<float, float>(dl, ldl, (const float*)weight, t, h, e, (float*)grad_x, s)

@@ -166,6 +166,9 @@ hipError_t router_logits_gemm(const TX* x, const TW* w, int T, int H, int E, flo
 typedef DmaCfg<128, 384, 64, 96, 2, 64> DmaRouterLogits3;
 typedef DmaCfg<64, 64, 32, 32, 2> DmaRouterLogits;
 typedef DmaCfg<128, 128, 64, 64, 4> DmaRouterDw;
+// The same one-piece logits and weight-gradient tiles on fp16 operands.
+typedef DmaCfg<64, 64, 32, 32, 2, 64, 1, f16_t> DmaRouterLogitsF16;
+typedef DmaCfg<128, 128, 64, 64, 4, 64, 1, f16_t> DmaRouterDwF16;
 
 // Router logits x . W^T in fp32 from bf16 x and npieces bf16 pieces of W
 // stacked along rows (w3 = [piece 0; piece 1; piece 2], each (E, H); npieces
@@ -195,19 +198,43 @@ hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npie
   return launch_gemm_dma<DmaRouterLogits, true, true, GM_BATCH, EPI_STORE, float>(p, s);
 }
 
+// Router logits x . W^T in fp32 from fp16 x and an fp16 W. A product of two
+// fp16 values (11-bit significands) is exact in fp32, so one piece on the fp16
+// MFMAs gives fp32-accumulated logits of exact products, as the bf16 pieces do.
+// The split-K planes are as in router_logits_bf16_pieces with one piece.
+hipError_t router_logits_f16(const f16_t* x, const f16_t* w, int T, int H, int E, int splits, float* parts,
+                             hipStream_t s) {
+  GemmParams p = zero_params();
+  p.A = x; p.lda = H;
+  p.B = w; p.ldb = H;
+  p.C = parts; p.ldc = E;
+  p.M = T; p.N = E; p.K = H;
+  p.a_bytes = (uint64_t)T * H * 2; p.b_bytes = (uint64_t)E * H * 2;
+  p.groups = splits;
+  p.strideC = (int64_t)T * E;
+  constexpr int BK = DmaRouterLogitsF16::BK;
+  p.split_chunk = splits > 1 ? ((H + splits - 1) / splits + BK - 1) / BK * BK : 0;
+  return launch_gemm_dma<DmaRouterLogitsF16, true, true, GM_BATCH, EPI_STORE, float>(p, s);
+}
+
 // Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
 // (T, 3*ldl), w3t = [W_hi; W_hi; W_lo] (3*ldl, H). dx = dl3 . w3t has the
 // expert input-gradient GEMM's form (k-contiguous A, [k][n] B), so it runs on
 // the persistent engine as one group of T rows with reduction 3*ldl: its 256 x
 // 256 tiles move half the operand bytes of 128 x 128 ones (measured at config
 // 2: 24 -> 21.5 us; with one tile per CU the loads, MFMAs and the 33.5 MB of
-// stores follow each other rather than overlap).
-hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s) {
+// stores follow each other rather than overlap). dx is written in TO: bf16,
+// or fp16 for an fp16 router (whose weight's bf16 pieces are exact).
+template <typename TO>
+hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, TO* dx, hipStream_t s) {
+  static_assert(sizeof(TO) == 2, "16-bit input gradient");
   if ((3 * ldl) % 2) return hipErrorInvalidValue;
-  const GemmParams p = expert_params<bf16_t>(EG_GATE_UP_DGRAD, dl3, w3t, nullptr, dx, nullptr, nullptr, T, 1, H,
-                                             3 * ldl / 2);
-  return launch_gemm_persist<DmaRouterDx, true, false, GM_ROWS, EPI_STORE>(p, num_cus(), s);
+  const GemmParams p = expert_params<bf16_t>(EG_GATE_UP_DGRAD, dl3, w3t, nullptr, reinterpret_cast<bf16_t*>(dx),
+                                             nullptr, nullptr, T, 1, H, 3 * ldl / 2);
+  return launch_gemm_persist<DmaRouterDx, true, false, GM_ROWS, EPI_STORE, TO>(p, num_cus(), s);
 }
+template hipError_t router_dx_bf16<bf16_t>(const bf16_t*, int, const bf16_t*, int, int, bf16_t*, hipStream_t);
+template hipError_t router_dx_bf16<f16_t>(const bf16_t*, int, const bf16_t*, int, int, f16_t*, hipStream_t);
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and
 // lo planes of dl3 -> (2 * splits, E, H) fp32.
@@ -222,6 +249,22 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
   p.M = E; p.N = H; p.K = T;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
   return launch_gemm_dma<DmaRouterDw, false, false, GM_RED, EPI_STORE, float>(p, s);
+}
+
+// The fp16 router's weight gradient: dl2 = [dl_hi | dl_lo] (T, 2*ldl) fp16
+// planes of the fp32 dl and fp16 x, on the fp16 MFMAs (every product exact).
+// partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] -> (2 * splits, E, H) fp32.
+hipError_t router_dw_f16(const f16_t* dl2, int ldl, const f16_t* x, int T, int H, int E, int split_chunk,
+                         float* partial, hipStream_t s) {
+  GemmParams p = zero_params();
+  p.A = dl2; p.lda = 2 * ldl;  // A[m=e][k=t] = dl_plane[t][e]
+  p.B = x; p.ldb = H;          // B[k=t][n=h]
+  p.C = partial; p.ldc = H; p.strideC = (int64_t)E * H;
+  const int splits = (T + split_chunk - 1) / split_chunk;
+  p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
+  p.M = E; p.N = H; p.K = T;
+  p.a_bytes = (uint64_t)T * 2 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
+  return launch_gemm_dma<DmaRouterDwF16, false, false, GM_RED, EPI_STORE, float>(p, s);
 }
 
 template <typename TX, typename TW>

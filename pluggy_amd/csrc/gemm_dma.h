@@ -452,7 +452,6 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
   constexpr int MI = Cfg::MI, NI = Cfg::NI;
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SUM3 || (B_KC && Cfg::WN == 96), "EPI_SUM3: three 32-row pieces per wave");
-  static_assert(std::is_same<typename Cfg::Tc, bf16_t>::value, "this kernel computes bf16 operands");
 
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::SMEM_BYTES];
   __shared__ int s_scan[1025];
@@ -630,8 +629,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void grouped_gemm_dma_kernel(Ge
     constexpr int KSI = decltype(ksc)::value;
     static_for<0, MI * NI>([&](auto mc) {
       constexpr int M = decltype(mc)::value;
-      acc[M / NI][M % NI] =
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[M / NI], bfr[M % NI], acc[M / NI][M % NI], 0, 0, 0);
+      acc[M / NI][M % NI] = mfma16<typename Cfg::Tc>(af[M / NI], bfr[M % NI], acc[M / NI][M % NI]);
       constexpr int G = KSI * MI * NI + M;  // MFMA index within the stage
       static_for<0, D>([&](auto dc) {
         constexpr int DI = decltype(dc)::value;

@@ -505,8 +505,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // bf16 outputs stage packed (the SwiGLU backward reads its fp32 accumulators back)
   constexpr bool PACK = sizeof(Tout) == 2 && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
   static_assert(PACK || EPI != EPI_SWIGLU, "the SwiGLU forward stages packed bf16");
-  static_assert(sizeof(Tout) == 4 || std::is_same<Tout, typename Cfg::Tc>::value,
-                "16-bit outputs are in the operands' format");
+  // (a plain store may round to the other 16-bit format: the router's input
+  // gradient from bf16 pieces of an fp16 weight)
+  static_assert(sizeof(Tout) == 4 || std::is_same<Tout, typename Cfg::Tc>::value || EPI == EPI_STORE,
+                "16-bit outputs of the fused epilogues are in the operands' format");
   static_assert(GM == GM_ROWS || GM == GM_RED, "persistent kernel serves the expert GEMMs");
   static_assert(!(GM == GM_RED && (A_KC || B_KC)), "GM_RED expects [k][m] and [k][n] operands");
   static_assert(EPI != EPI_SWIGLU || (B_KC && GM == GM_ROWS && Cfg::WN % 32 == 0), "SwiGLU epilogue layout");

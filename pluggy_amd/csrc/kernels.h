@@ -53,17 +53,24 @@ hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s);
 // into `splits` planes of (T, npieces*E) each.
 hipError_t router_logits_bf16_pieces(const bf16_t* x, const bf16_t* w3, int npieces, int T, int H, int E,
                                      int splits, float* parts, hipStream_t s);
+// parts (T, E) planes fp32 = x . w^T from fp16 x (T,H) and fp16 w (E,H), split-K as above.
+hipError_t router_logits_f16(const f16_t* x, const f16_t* w, int T, int H, int E, int splits, float* parts,
+                             hipStream_t s);
 hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
                                float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s);
-// dl (T, ldl) fp32, or with dl3 != nullptr the bf16 planes [dl_hi | dl_lo | dl_hi] (T, 3*ldl).
+// dl (T, ldl) fp32, or with dl3 != nullptr the bf16 planes [dl_hi | dl_lo | dl_hi] (T, 3*ldl),
+// and with dl2 != nullptr also the fp16 planes [dl_hi | dl_lo] (T, 2*ldl).
 template <typename TG>
 hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
                           const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, bf16_t* dl3,
-                          int ldl, hipStream_t s);
+                          f16_t* dl2, int ldl, hipStream_t s);
 // w3t = [W_hi; W_hi; W_lo] with rows E..ldl-1 of each plane zero (3*ldl, H)
 template <typename TW>
 hipError_t split_router_weight_bwd(const TW* w, int E, int H, int ldl, bf16_t* w3t, hipStream_t s);
-hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, bf16_t* dx, hipStream_t s);
+template <typename TO>
+hipError_t router_dx_bf16(const bf16_t* dl3, int ldl, const bf16_t* w3t, int T, int H, TO* dx, hipStream_t s);
+hipError_t router_dw_f16(const f16_t* dl2, int ldl, const f16_t* x, int T, int H, int E, int split_chunk,
+                         float* partial, hipStream_t s);
 hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, int H, int E, int split_chunk,
                           float* partial, hipStream_t s);
 template <typename TO>

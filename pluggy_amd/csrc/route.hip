@@ -250,7 +250,8 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
                                                              const TG* __restrict__ grad_w,
                                                              const float* __restrict__ grad_logits, int T, int E,
                                                              int K, int norm_topk, float* __restrict__ dl,
-                                                             bf16_t* __restrict__ dl3, int ldl) {
+                                                             bf16_t* __restrict__ dl3, f16_t* __restrict__ dl2,
+                                                             int ldl) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
@@ -336,6 +337,17 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
         o[ldl + e] = lo;
         o[2 * ldl + e] = hi;
       }
+      if (dl2 != nullptr) {
+        // fp16 planes for the fp16 weight gradient: val = hi + lo to 2^-22
+        // relative for |val| >= 2^-3 (lo normal) and to 2^-25 absolute below;
+        // fp16's range, as the fp16 dl of an fp16 linear layer has (an
+        // overflow gives hi = inf and lo = 0, not inf - inf)
+        const f16_t hi = (f16_t)val;
+        const float hf = (float)hi;
+        f16_t* o = dl2 + (int64_t)row * 2 * ldl;
+        o[e] = hi;
+        o[ldl + e] = (f16_t)(__builtin_isinf(hf) ? 0.0f : val - hf);
+      }
     }
   }
   for (int e = 64 * EPL + lane; e < ldl; e += 64) {
@@ -344,6 +356,10 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
     } else {
       bf16_t* o = dl3 + (int64_t)row * 3 * ldl;
       o[e] = o[ldl + e] = o[2 * ldl + e] = 0;
+    }
+    if (dl2 != nullptr) {
+      f16_t* o = dl2 + (int64_t)row * 2 * ldl;
+      o[e] = o[ldl + e] = (f16_t)0.0f;
     }
   }
 }
@@ -892,16 +908,17 @@ hipError_t split_router_weight_bwd(const TW* w, int E, int H, int ldl, bf16_t* w
 }
 template hipError_t split_router_weight_bwd<float>(const float*, int, int, int, bf16_t*, hipStream_t);
 template hipError_t split_router_weight_bwd<bf16_t>(const bf16_t*, int, int, int, bf16_t*, hipStream_t);
+template hipError_t split_router_weight_bwd<f16_t>(const f16_t*, int, int, int, bf16_t*, hipStream_t);
 
 template <typename TG>
 hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
                           const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, bf16_t* dl3,
-                          int ldl, hipStream_t s) {
+                          f16_t* dl2, int ldl, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const unsigned grid = blocks_for(T, 4);
 #define PMOE_DL_CASE(EPL)                                                                                        \
   hipLaunchKernelGGL((router_dlogits_kernel<EPL, TG>), dim3(grid), dim3(256), 0, s, logits, top_idx, top_w_f32, \
-                     grad_w, grad_logits, T, E, K, norm_topk, dl, dl3, ldl)
+                     grad_w, grad_logits, T, E, K, norm_topk, dl, dl3, dl2, ldl)
   if (E <= 64) PMOE_DL_CASE(1);
   else if (E <= 128) PMOE_DL_CASE(2);
   else if (E <= 256) PMOE_DL_CASE(4);
@@ -1135,11 +1152,14 @@ template hipError_t router_topk<float>(const float*, int, int64_t, int64_t, floa
 template hipError_t router_topk<f16_t>(const float*, int, int64_t, int64_t, float*, const float*, int, int, int, int,
                                        f16_t*, int64_t*, float*, float*, float*, int*, int, hipStream_t);
 template hipError_t router_dlogits<bf16_t>(const float*, const int64_t*, const float*, const bf16_t*, const float*,
-                                           int, int, int, int, float*, bf16_t*, int, hipStream_t);
+                                           int, int, int, int, float*, bf16_t*, f16_t*, int, hipStream_t);
+template hipError_t router_dlogits<f16_t>(const float*, const int64_t*, const float*, const f16_t*, const float*,
+                                          int, int, int, int, float*, bf16_t*, f16_t*, int, hipStream_t);
 template hipError_t router_dlogits<float>(const float*, const int64_t*, const float*, const float*, const float*, int,
-                                          int, int, int, float*, bf16_t*, int, hipStream_t);
+                                          int, int, int, float*, bf16_t*, f16_t*, int, hipStream_t);
 template hipError_t reduce_partials<float>(const float*, int, int64_t, float*, hipStream_t);
 template hipError_t reduce_partials<bf16_t>(const float*, int, int64_t, bf16_t*, hipStream_t);
+template hipError_t reduce_partials<f16_t>(const float*, int, int64_t, f16_t*, hipStream_t);
 
 #define PMOE_INST_COMBINE(T, TW)                                                                                \
   template hipError_t combine_rows<T, TW>(const T*, const TW*, const int32_t*, int, int, int, T*, hipStream_t);     \

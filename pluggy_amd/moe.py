@@ -119,10 +119,10 @@ def _amp_dtype(t: torch.Tensor) -> torch.dtype | None:
     returns its outputs in the input's dtype as the reference does. (torch's
     ``F.grouped_mm`` is not on autocast's bf16 list, so with an fp32 residual
     stream the reference's expert GEMMs actually run in fp32; this build keeps
-    the stated bf16 intent.) Under fp16 autocast the expert path takes fp16
-    operands likewise (fp16 MFMAs, fp32 accumulation); the router takes fp32
-    ones (``_router_x``, ``_router_operand``). Any other autocast dtype gives
-    fp32 operands.
+    the stated bf16 intent.) Under fp16 autocast the expert path and the
+    router take fp16 operands likewise (fp16 MFMAs, fp32 accumulation; see
+    ``_router_x``, ``_router_operand``). Any other autocast dtype gives fp32
+    operands.
     """
     if t.is_cuda and torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
@@ -142,24 +142,28 @@ def _compute_dtype(t: torch.Tensor) -> torch.dtype:
     return t.dtype if t.dtype in (torch.bfloat16, torch.float16, torch.float32) else torch.float32
 
 
-def _router_x(x: torch.Tensor) -> torch.Tensor:
-    """The router's input as its kernels take it: fp32 or bf16 as given, and an
-    fp16 input in fp32 (exact). The router's logits are fp32 arithmetic in
-    every case; its input gradient comes back in fp32 and is rounded to fp16
-    where it joins the experts' fp16 input gradient."""
-    return x.float() if x.dtype == torch.float16 else x
+def _router_x(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The router's input as its kernels take it beside the weight operand
+    ``w`` (from ``_router_operand``): fp32 or bf16 as given, fp16 when the
+    weight is fp16 too (the fp16 MFMAs, as the reference's ``F.linear`` on
+    fp16 tensors), else an fp16 input in fp32 (exact). The logits are fp32
+    arithmetic in every case."""
+    return x.float() if x.dtype == torch.float16 and w.dtype != torch.float16 else x
 
 
-def _router_operand(w: torch.Tensor, amp: torch.dtype | None) -> torch.Tensor:
-    """The router weight as the kernels take it: bf16 under bf16 autocast (as
-    the reference's ``F.linear`` there), its fp16 rounding in fp32 under fp16
-    autocast (the router's kernels take fp32 and bf16), else fp32 or bf16 as
-    given (fp32 for any other dtype, fp16 included)."""
+def _router_operand(w: torch.Tensor, amp: torch.dtype | None, x_dtype: torch.dtype) -> torch.Tensor:
+    """The router weight as the kernels take it beside activations of
+    ``x_dtype``: bf16 under bf16 autocast and fp16 under fp16 autocast (as the
+    reference's ``F.linear`` there), else fp32, bf16 or fp16 as given, except
+    that an fp16 weight beside non-fp16 activations (a pairing the kernels do
+    not take) and any other dtype are taken in fp32 (exact)."""
     if amp == torch.bfloat16:
         w = w.to(torch.bfloat16)
     elif amp == torch.float16:
-        w = w.to(torch.float16).float()
-    elif w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.to(torch.float16)
+    elif w.dtype == torch.float16 and x_dtype != torch.float16:
+        w = w.float()
+    elif w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         w = w.float()
     return w.contiguous()
 
@@ -367,8 +371,9 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     require_gpu(hidden, weight, logit_bias)
     amp = _amp_dtype(hidden)
     H = hidden.shape[1]
-    x = _pad_last(_router_x(hidden.to(_compute_dtype(hidden))), _pad8(H)).contiguous()
-    w = _pad_last(_router_operand(weight, amp), _pad8(H)).contiguous()
+    cdt = _compute_dtype(hidden)
+    w = _pad_last(_router_operand(weight, amp, cdt), _pad8(H)).contiguous()
+    x = _pad_last(_router_x(hidden.to(cdt), w), _pad8(H)).contiguous()
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     logits, top_w, top_i, _w32, counts, psum, lse2 = torch.ops.pmoe.router_fwd(
@@ -591,7 +596,7 @@ def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_
     """
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-            _router_x(x), router_weight, top_k, norm_topk_prob, logit_bias, tw_dtype=x.dtype)
+            _router_x(x, router_weight), router_weight, top_k, norm_topk_prob, logit_bias, tw_dtype=x.dtype)
     out, offs, inv_pos, stok, sw, gu, mid = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
     return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid
 
@@ -643,9 +648,9 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
         g_tw = _none_if_empty(g_tw)
     gx_router = None
     if need[0] or need[1]:
-        gx_router, g_rw = torch.ops.pmoe.router_bwd(_router_x(x), rw, logits, top_i, top_w32, g_tw, g_logits,
+        gx_router, g_rw = torch.ops.pmoe.router_bwd(_router_x(x, rw), rw, logits, top_i, top_w32, g_tw, g_logits,
                                                     ctx.norm_topk_prob)
-        gx_router = gx_router.to(x.dtype)  # an fp16 block's router works in fp32
+        gx_router = gx_router.to(x.dtype)  # fp32 when fp16 x met a non-fp16 weight
     if g_gu is not None and (need[0] or need_gu or need_dn):
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
             g_gu, g_out, x, gate_up, down, offs, inv_pos, stok, mid, gx_router if need[0] else None, K,
@@ -682,7 +687,7 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     I = gate_up_proj.shape[1] // 2
     Hp, Ip = _pad8(H), _pad8(I)
     x = _pad_last(hidden.to(dt), Hp).contiguous()
-    rw = _pad_last(_router_operand(router_weight, amp), Hp).contiguous()
+    rw = _pad_last(_router_operand(router_weight, amp, dt), Hp).contiguous()
     gu, gu_master, dn, dn_master = _expert_weights(gate_up_proj, down_proj, dt, Hp, Ip)
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
@@ -908,7 +913,7 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     cdt = _compute_dtype(flat)
     eps = norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
     nw = norm.weight if norm.weight.dtype == torch.float32 else norm.weight.float()
-    rw = _router_operand(r.weight, amp)
+    rw = _router_operand(r.weight, amp, cdt)
     gu, gu_master = _compute_weight(mlp.experts.gate_up_proj, cdt)
     dn, dn_master = _compute_weight(mlp.experts.down_proj, cdt)
     bias = r.logit_bias.float().contiguous() if r.logit_bias is not None else None

@@ -338,12 +338,13 @@ def _check_routing_vs_cpu(x, Wr, gpu_logits, K, bias=None):
     return len(bad)
 
 
-def _run_config(cfg_id, tokens: int | None = None):
+def _run_config(cfg_id, tokens: int | None = None, router_dtype=None):
     """One configuration at full size: routing, counts and permutation bit-exact;
     the router statistics against the oracle; every output row, the whole input
     gradient, every expert's weight gradients and the full router weight gradient
     against fp64 truth (``ref_layer_fp64``) with rel-L2 and max-abs bounds;
-    bitwise run-to-run determinism."""
+    bitwise run-to-run determinism. ``router_dtype``: the router weight in that
+    dtype (its rounding is the truth's weight too), else fp32."""
     from pluggy_amd.workloads import CONFIGS, MoEConfig, make_inputs
 
     pa = _mod()
@@ -353,6 +354,9 @@ def _run_config(cfg_id, tokens: int | None = None):
     H, E, K, I = cfg.hidden, cfg.experts, cfg.top_k, cfg.inter
     say(f"config {cfg_id if isinstance(cfg_id, int) else '-'} ({cfg.name}) T={T} H={H} E={E} K={K} I={I} {cfg.dtype} backward={cfg.backward}")
     mlp = pa.Qwen3MoeSparseMLP(H, I, E, K, cfg.norm_topk_prob).to(DEV)
+    if router_dtype is not None:
+        inp["router_weight"] = inp["router_weight"].to(router_dtype)
+        mlp.router.to(router_dtype)
     with torch.no_grad():
         mlp.router.weight.copy_(inp["router_weight"])
         mlp.experts.gate_up_proj.data = inp["gate_up_proj"].to(DEV)
@@ -377,7 +381,7 @@ def _run_config(cfg_id, tokens: int | None = None):
     lg = logits.detach().cpu()
     idx = O.select_topk(lg, K)
     # 1. routing: bit-exact on the GPU logits; near-tie-only differences on CPU logits
-    n_tie = _check_routing_vs_cpu(inp["x"], inp["router_weight"], lg, K, bias)
+    n_tie = _check_routing_vs_cpu(inp["x"], inp["router_weight"].float(), lg, K, bias)
     say(f"  routing ok (near-tie rows vs CPU logits: {n_tie})")
     counts = to_np(stats.expert_counts)
     assert np.array_equal(counts, np.bincount(idx.reshape(-1), minlength=E))
@@ -392,7 +396,7 @@ def _run_config(cfg_id, tokens: int | None = None):
     rc, ro, rsp, rinv = O.permute(idx, E)
     assert np.array_equal(to_np(offs), ro) and np.array_equal(to_np(sp), rsp) and np.array_equal(to_np(inv), rinv)
     # 3. every value against fp64 truth given the GPU's routing
-    ref = ref_layer_fp64(inp["x"], inp["router_weight"], inp["gate_up_proj"], inp["down_proj"],
+    ref = ref_layer_fp64(inp["x"], inp["router_weight"].float(), inp["gate_up_proj"], inp["down_proj"],
                          torch.from_numpy(idx), lg, cfg.norm_topk_prob,
                          gout=inp["grad_out"] if cfg.backward else None)
     tol = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}[cfg.dtype]
@@ -445,15 +449,19 @@ def test_config4_skewed():
     _run_config(4)
 
 
-def test_config2_fp16():
-    """Config 2's layer with fp16 tensors (activations and expert weights): the
-    expert path on the fp16 MFMAs, the router on fp32 copies of x; every value
-    and gradient against fp64 at fp16's bar (rel-L2 2e-3)."""
+@pytest.mark.parametrize("router_dtype", [torch.float16, torch.float32])
+def test_config2_fp16(router_dtype):
+    """Config 2's layer with fp16 tensors (activations and expert weights), the
+    expert path on the fp16 MFMAs. With an fp16 router weight (a module in
+    fp16, the only pairing the reference's F.linear takes for fp16 input) the
+    router runs on the fp16 MFMAs too; with an fp32 one, on fp32 copies of x.
+    Every value and gradient against fp64 at fp16's bar (rel-L2 2e-3)."""
     import dataclasses
 
     from pluggy_amd.workloads import CONFIGS
 
-    _run_config(dataclasses.replace(CONFIGS[2], name="qwen3-30b-a3b-fp16", dtype=torch.float16))
+    _run_config(dataclasses.replace(CONFIGS[2], name="qwen3-30b-a3b-fp16", dtype=torch.float16),
+                router_dtype=router_dtype)
 
 
 def test_config_climbmix():

@@ -90,8 +90,8 @@ def test_autocast_sparse_mlp(x_dtype):
 
 def test_fp16_autocast_takes_fp16_operands():
     """Under fp16 autocast the expert path takes fp16 operands (fp16 MFMAs,
-    fp32 masters' copies) and the router the fp16-rounded input and weight in
-    fp32: the module over fp32 parameters gives, bit for bit, what the same
+    fp32 masters' copies) and so does the router (the fp16-rounded input and
+    weight): the module over fp32 parameters gives, bit for bit, what the same
     module in fp16 gives on the fp16-rounded input (values cast to fp32, and
     the fp32 masters' gradients rounded to fp16 equal the fp16 module's)."""
     pa = _pa()
