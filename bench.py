@@ -678,8 +678,12 @@ def main() -> int:
                          # x, W, logits, ids, fp32 weights and their gradient in; dx, dW out
                          ("router_bwd", 2 * T * H * es + 2 * E * H * 4 + T * E * 4 + T * K * (8 + 4 + 4))):
         if name in stages:
-            gbs = nbytes / (stages[name]["mean_ms"] * 1e-3) / 1e9
-            hbm[name] = {"bytes": nbytes, "mean_ms": round(stages[name]["mean_ms"], 4), "GB/s": round(gbs, 1),
+            t_ms = stages[name]["mean_ms"]
+            if name == "router_fwd" and "router_split" in stages:
+                # the fp32 weight's bf16 pieces, made before the router op (its backward reuses them)
+                t_ms += stages["router_split"]["mean_ms"]
+            gbs = nbytes / (t_ms * 1e-3) / 1e9
+            hbm[name] = {"bytes": nbytes, "mean_ms": round(t_ms, 4), "GB/s": round(gbs, 1),
                          "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
     result = {

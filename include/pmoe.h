@@ -37,7 +37,9 @@ extern "C" {
 
 #define PMOE_API __attribute__((visibility("default")))
 
-enum { PMOE_F32 = 0, PMOE_BF16 = 1, PMOE_F16 = 2 };
+/* PMOE_BF16X3: a router weight that is fp32, given as the bf16 pieces
+ * pmoe_router_split_weight writes (router entry points only, beside bf16 x). */
+enum { PMOE_F32 = 0, PMOE_BF16 = 1, PMOE_F16 = 2, PMOE_BF16X3 = 3 };
 enum {
   PMOE_OK = 0,
   PMOE_ERR_INVALID = -1,     /* bad shape, dtype or null pointer */
@@ -60,7 +62,9 @@ PMOE_API const char* pmoe_last_error_string(void);
  * (qwen3_moe.py:417-426): expert_counts[e] (int32), prob_sum[e] = sum_t p[t,e],
  * lse_sq_sum = sum_t logsumexp(logits[t])^2. Any of the three may be NULL.
  * x: (T,H) x_dtype; weight: (E,H) w_dtype (each fp32 or bf16, or both fp16:
- * the reference's F.linear under fp16 takes fp16 x and W, qwen3_moe.py:172);
+ * the reference's F.linear under fp16 takes fp16 x and W, qwen3_moe.py:172;
+ * or, beside bf16 x, PMOE_BF16X3: the pieces of an fp32 weight from
+ * pmoe_router_split_weight, which spare the call its own split);
  * logit_bias: (E,) fp32 or NULL; logits: (T,E) fp32; top_weights: (T,K)
  * tw_dtype (fp32, bf16 or fp16, rounded as the reference's
  * .to(hidden_states.dtype), qwen3_moe.py:177);
@@ -81,8 +85,19 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
  * pieces of dl (two bf16 pieces; for fp16 x and W, grad_weight from two fp16
  * pieces, which carry fp16's exponent range as the reference's fp16 dl does).
  * grad_top_weights (T,K) gw_dtype (fp32, bf16 or fp16) and grad_logits (T,E)
- * fp32 may be NULL (zero); grad_x / grad_weight may be NULL (not needed). */
+ * fp32 may be NULL (zero); grad_x / grad_weight may be NULL (not needed).
+ * A weight given as PMOE_BF16X3 pieces (E a multiple of 8) gets its gradient
+ * in fp32. */
 PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E);
+/* The bf16 pieces of an fp32 router weight (E,H) that pmoe_router_forward and
+ * pmoe_router_backward take as w_dtype PMOE_BF16X3, so that a forward and its
+ * backward (or the micro-batches of one optimizer step) split the weight once
+ * instead of on every call: pieces (4,E,H) bf16 = [lo; hi; mid; hi], hi =
+ * bf16(W), mid = bf16(W - hi), lo = bf16(W - hi - mid); hi + mid + lo = W to
+ * 2^-24 relative. Part of the split inside pmoe_router_forward (the per-call
+ * copy of qwen3_moe.py:172's weight operand), exposed; no reference
+ * counterpart of its own. */
+PMOE_API int pmoe_router_split_weight(const float* weight, int64_t E, int64_t H, void* pieces, void* stream);
 PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight, int w_dtype,
                                   const float* logits, const int64_t* top_indices, const float* top_weights_f32,
                                   const void* grad_top_weights, int gw_dtype, const float* grad_logits, int64_t T,

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libpmoe.so")
 PMOE_F32 = 0
 PMOE_BF16 = 1
 PMOE_F16 = 2
+PMOE_BF16X3 = 3  # an fp32 router weight given as its bf16 pieces (pmoe_router_split_weight)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -32,6 +33,7 @@ SIGNATURES = {
     "pmoe_router_forward": (_INT, [_P, _INT, _P, _INT, _P, _I64, _I64, _I64, _I64, _INT, _P, _P, _INT, _P, _P, _P,
                                    _P, _P, _P, _SZ, _P]),
     "pmoe_router_backward_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "pmoe_router_split_weight": (_INT, [_P, _I64, _I64, _P, _P]),
     "pmoe_router_backward": (_INT, [_P, _INT, _P, _INT, _P, _P, _P, _P, _INT, _P, _I64, _I64, _I64, _I64, _INT, _P,
                                     _P, _P, _SZ, _P]),
     "pmoe_permute_workspace_size": (_SZ, [_I64, _I64, _I64]),

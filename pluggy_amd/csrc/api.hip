@@ -60,6 +60,11 @@ struct Carver {
 // bf16; the expert path (row tables, row movers, expert GEMMs) also fp16.
 bool dtype_ok(int d) { return d == PMOE_F32 || d == PMOE_BF16; }
 bool dtype16_ok(int d) { return dtype_ok(d) || d == PMOE_F16; }
+// The router's (x, weight) pairings: each fp32 or bf16, both fp16, or bf16 x
+// beside an fp32 weight given as its bf16 pieces (pmoe_router_split_weight).
+bool router_pair_ok(int x, int w) {
+  return (dtype_ok(x) && dtype_ok(w)) || (x == PMOE_F16 && w == PMOE_F16) || (x == PMOE_BF16 && w == PMOE_BF16X3);
+}
 size_t elem_bytes(int d) { return d == PMOE_F32 ? 4 : 2; }
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -68,8 +73,8 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 constexpr int kRouterSplitChunk = 1024;
 constexpr int64_t kMaxIndex = 0x7fffffffLL;
 
-// Rows per block of the router top-k kernel (4 waves, one row at a time per
-// wave): 16 when there are enough rows to fill the GPU, else one row per wave.
+// Rows per block of the router top-k kernel: 16 when there are enough rows to
+// fill the GPU, else 4 (a wave takes four rows for E <= 256, else one).
 int router_rows(int64_t T) { return T >= 2048 ? 16 : 4; }
 int64_t router_blocks(int64_t T) { return (T + router_rows(T) - 1) / router_rows(T); }
 // Split-K planes of the router logits GEMM: its output tiles (128 x 128 for
@@ -138,9 +143,9 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
                                  float* prob_sum, float* lse_sq_sum, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(((dtype_ok(x_dtype) && dtype_ok(w_dtype)) || (x_dtype == PMOE_F16 && w_dtype == PMOE_F16)) &&
-                   dtype16_ok(tw_dtype),
-               "router_forward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, or both PMOE_F16");
+  PMOE_REQUIRE(router_pair_ok(x_dtype, w_dtype) && dtype16_ok(tw_dtype),
+               "router_forward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, both PMOE_F16, or "
+               "PMOE_BF16 and PMOE_BF16X3");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_weights && top_indices && top_weights_f32),
                "router_forward: null tensor");
   const size_t need = pmoe_router_forward_workspace_size(T, H, E);
@@ -154,7 +159,7 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   int* blk_cnt = cv.take<int>(nb * E);
   float* blk_lse2 = cv.take<float>(nb);
   bf16_t* w3 = cv.take<bf16_t>(3 * E * H);
-  const bool pieces = x_dtype == PMOE_BF16 && w_dtype == PMOE_F32;
+  const bool pieces = x_dtype == PMOE_BF16 && (w_dtype == PMOE_F32 || w_dtype == PMOE_BF16X3);
   const int splits = router_logit_splits(T, H, E, pieces);
   float* parts = cv.take<float>(splits * T * E);
   // Logits in fp32 arithmetic. bf16 x: x is exact in bf16, so splitting an fp32
@@ -176,9 +181,11 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
       const bf16_t* wb = (const bf16_t*)weight;
       int npieces = 1;
       if (w_dtype == PMOE_F32) {
-        PMOE_TRY(split_bf16x3((const float*)weight, E * H, w3, s), "router weight split");
+        PMOE_TRY(split_bf16x3((const float*)weight, E * H, 3, w3, s), "router weight split");
         wb = w3;
         npieces = 3;
+      } else if (w_dtype == PMOE_BF16X3) {
+        npieces = 3;  // planes 0..2 of the caller's pieces
       }
       // the pieces are summed in the GEMM's epilogue: one (T, E) plane per split
       PMOE_TRY(router_logits_bf16_pieces((const bf16_t*)x, wb, npieces, t, h, e, splits, parts, s),
@@ -206,6 +213,13 @@ PMOE_API int pmoe_router_forward(const void* x, int x_dtype, const void* weight,
   return PMOE_OK;
 }
 
+PMOE_API int pmoe_router_split_weight(const float* weight, int64_t E, int64_t H, void* pieces, void* stream) {
+  if (int rc = check_moe_dims(1, 1, E, H, 0)) return rc;
+  PMOE_REQUIRE(weight && pieces, "router_split_weight: null tensor");
+  PMOE_TRY(split_bf16x3(weight, E * H, 4, (bf16_t*)pieces, as_stream(stream)), "router weight split");
+  return PMOE_OK;
+}
+
 PMOE_API size_t pmoe_router_backward_workspace_size(int64_t T, int64_t H, int64_t E) {
   const int64_t ldl = ldl_of(E);
   const size_t fp32_path = align_up(T * ldl * sizeof(float)) + align_up(router_splits(T) * E * H * sizeof(float));
@@ -221,9 +235,11 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
                                   int64_t H, int64_t E, int64_t K, int norm_topk_prob, void* grad_x,
                                   void* grad_weight, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_moe_dims(T, K, E, H, 0)) return rc;
-  PMOE_REQUIRE(((dtype_ok(x_dtype) && dtype_ok(w_dtype)) || (x_dtype == PMOE_F16 && w_dtype == PMOE_F16)) &&
-                   dtype16_ok(gw_dtype),
-               "router_backward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, or both PMOE_F16");
+  PMOE_REQUIRE(router_pair_ok(x_dtype, w_dtype) && dtype16_ok(gw_dtype),
+               "router_backward: x and weight dtype codes must be PMOE_F32 or PMOE_BF16, both PMOE_F16, or "
+               "PMOE_BF16 and PMOE_BF16X3");
+  PMOE_REQUIRE(w_dtype != PMOE_BF16X3 || E % 8 == 0,
+               "router_backward: a weight given as pieces needs E a multiple of 8");
   PMOE_REQUIRE(T == 0 || (x && weight && logits && top_indices && top_weights_f32),
                "router_backward: null tensor");
   const size_t need = pmoe_router_backward_workspace_size(T, H, E);
@@ -238,7 +254,7 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
     // no tokens: dW = 0, written by the reduction kernel over zero partial
     // planes (a kernel write, not hipMemsetAsync, so a captured graph replays it)
     if (grad_weight) {
-      hipError_t st = by_dtype16(w_dtype, [&](auto wp) {
+      hipError_t st = by_dtype16(w_dtype == PMOE_BF16X3 ? PMOE_F32 : w_dtype, [&](auto wp) {
         typedef PMOE_ELEM(wp) W;
         return reduce_partials<W>(nullptr, 0, E * H, (W*)grad_weight, s);
       });
@@ -281,13 +297,19 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
     PMOE_TRY(dlogits(nullptr, dl3, nullptr), "router dlogits");
     hipError_t st;
     if (grad_x) {
-      st = w_dtype == PMOE_F32 ? split_router_weight_bwd<float>((const float*)weight, e, h, ldl, w3t, s)
-                               : split_router_weight_bwd<bf16_t>((const bf16_t*)weight, e, h, ldl, w3t, s);
-      PMOE_TRY(st, "router weight split");
-      PMOE_TRY(router_dx_bf16<bf16_t>(dl3, ldl, w3t, t, h, (bf16_t*)grad_x, s), "router dx GEMM");
+      const bf16_t* wt = w3t;
+      if (w_dtype == PMOE_BF16X3) {
+        wt = (const bf16_t*)weight + (size_t)E * H;  // planes 1..3 = [hi; mid; hi] (ldl == E)
+      } else {
+        st = w_dtype == PMOE_F32 ? split_router_weight_bwd<float>((const float*)weight, e, h, ldl, w3t, s)
+                                 : split_router_weight_bwd<bf16_t>((const bf16_t*)weight, e, h, ldl, w3t, s);
+        PMOE_TRY(st, "router weight split");
+      }
+      PMOE_TRY(router_dx_bf16<bf16_t>(dl3, ldl, wt, t, h, (bf16_t*)grad_x, s), "router dx GEMM");
     }
     if (grad_weight) {
       PMOE_TRY(router_dw_bf16(dl3, ldl, (const bf16_t*)x, t, h, e, kRouterSplitChunk, partial, s), "router dW GEMM");
+      // an fp32 weight, whole or as pieces, gets its gradient in fp32
       st = w_dtype == PMOE_BF16 ? reduce_partials<bf16_t>(partial, 2 * splits, E * H, (bf16_t*)grad_weight, s)
                                 : reduce_partials<float>(partial, 2 * splits, E * H, (float*)grad_weight, s);
       PMOE_TRY(st, "router dW reduce");

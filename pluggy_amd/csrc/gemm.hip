@@ -171,9 +171,9 @@ typedef DmaCfg<64, 64, 32, 32, 2, 64, 1, f16_t> DmaRouterLogitsF16;
 typedef DmaCfg<128, 128, 64, 64, 4, 64, 1, f16_t> DmaRouterDwF16;
 
 // Router logits x . W^T in fp32 from bf16 x and npieces bf16 pieces of W
-// stacked along rows (w3 = [piece 0; piece 1; piece 2], each (E, H); npieces
-// is 1 or 3). Each piece is accumulated over the block's k range on its own;
-// the epilogue adds them as (piece 0 + piece 1) + piece 2. With splits > 1 the
+// stacked along rows (w3 = [lo; hi; mid], each (E, H), as split_bf16x3 writes
+// them; npieces is 1 or 3). Each piece is accumulated over the block's k range
+// on its own; the epilogue adds them as (hi + mid) + lo. With splits > 1 the
 // reduction over H is split into that many chunks (a multiple of the k tile),
 // each writing its own (T, E) plane at parts + s * T * E, which the caller
 // sums in order; few tokens give too few blocks to fill the GPU otherwise.
@@ -217,8 +217,8 @@ hipError_t router_logits_f16(const f16_t* x, const f16_t* w, int T, int H, int E
   return launch_gemm_dma<DmaRouterLogitsF16, true, true, GM_BATCH, EPI_STORE, float>(p, s);
 }
 
-// Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_lo | dl_hi]
-// (T, 3*ldl), w3t = [W_hi; W_hi; W_lo] (3*ldl, H). dx = dl3 . w3t has the
+// Router backward from bf16 planes (see api.hip): dl3 = [dl_hi | dl_hi | dl_lo]
+// (T, 3*ldl), w3t = [W_hi; W_mid; W_hi] (3*ldl, H). dx = dl3 . w3t has the
 // expert input-gradient GEMM's form (k-contiguous A, [k][n] B), so it runs on
 // the persistent engine as one group of T rows with reduction 3*ldl: its 256 x
 // 256 tiles move half the operand bytes of 128 x 128 ones (measured at config
@@ -237,7 +237,7 @@ template hipError_t router_dx_bf16<bf16_t>(const bf16_t*, int, const bf16_t*, in
 template hipError_t router_dx_bf16<f16_t>(const bf16_t*, int, const bf16_t*, int, int, f16_t*, hipStream_t);
 
 // partial[plane * splits + c] = dl_plane[chunk c]^T . x[chunk c] for the hi and
-// lo planes of dl3 -> (2 * splits, E, H) fp32.
+// lo planes of dl3 (columns 0 and 2*ldl of its rows) -> (2 * splits, E, H) fp32.
 hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, int H, int E, int split_chunk,
                           float* partial, hipStream_t s) {
   GemmParams p = zero_params();
@@ -245,7 +245,7 @@ hipError_t router_dw_bf16(const bf16_t* dl3, int ldl, const bf16_t* x, int T, in
   p.B = x; p.ldb = H;          // B[k=t][n=h]
   p.C = partial; p.ldc = H; p.strideC = (int64_t)E * H;
   const int splits = (T + split_chunk - 1) / split_chunk;
-  p.planes = 2; p.strideA = ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
+  p.planes = 2; p.strideA = 2 * ldl; p.groups = 2 * splits; p.split_chunk = split_chunk;
   p.M = E; p.N = H; p.K = T;
   p.a_bytes = (uint64_t)T * 3 * ldl * 2; p.b_bytes = (uint64_t)T * H * 2;
   return launch_gemm_dma<DmaRouterDw, false, false, GM_RED, EPI_STORE, float>(p, s);

@@ -333,7 +333,7 @@ __device__ __forceinline__ void store_tile_dma(const f32x16 (&acc)[Cfg::MI][Cfg:
                                                int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI, LD = Cfg::EPI_LD;
   // EPI_SUM3: the wave's three 32-column blocks are the three weight pieces of
-  // the same 32 output columns; they are summed (piece 0 + piece 1) + piece 2.
+  // the same 32 output columns, [lo; hi; mid]; they are summed (hi + mid) + lo.
   constexpr int WN = EPI == EPI_SUM3 ? 32 : Cfg::WN;
   static_assert(LD % 4 == 0, "16-byte aligned staging rows");
   static_assert(EPI == EPI_STORE || EPI == EPI_SUM3, "the router GEMMs store plainly or sum weight pieces");
@@ -350,7 +350,7 @@ __device__ __forceinline__ void store_tile_dma(const f32x16 (&acc)[Cfg::MI][Cfg:
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           stage[(8 * q + 4 * half + r) * LD + col_l] =
-              (acc[i][0][4 * q + r] + acc[i][1][4 * q + r]) + acc[i][2][4 * q + r];
+              (acc[i][1][4 * q + r] + acc[i][2][4 * q + r]) + acc[i][0][4 * q + r];
     } else {
 #pragma unroll
       for (int j = 0; j < NI; ++j)

@@ -40,14 +40,16 @@ hipError_t router_dw_gemm(const float* dl, int ldl, const TX* x, int T, int H, i
 // ---- routing, permutation and row movement (route.hip).
 // logits = the fixed-order sum of nsplit split-K planes (plane s of (t, e) at
 // parts[s*split_stride + t*ldp + e]) plus the optional bias, then softmax /
-// top-k / renormalisation and the per-block statistics; one wave per row,
-// rows_per_block (<= 16) rows per block.
+// top-k / renormalisation and the per-block statistics of rows_per_block
+// (<= 16) rows per block: four rows per wave when E <= 256 and rows_per_block
+// is a multiple of 4, else one wave per row.
 template <typename TW>
 hipError_t router_topk(const float* parts, int nsplit, int64_t split_stride, int64_t ldp, float* logits,
                        const float* logit_bias, int T, int E, int K, int norm_topk, TW* top_w, int64_t* top_idx,
                        float* top_w_f32, float* blk_psum, float* blk_lse2, int* blk_counts, int rows_per_block,
                        hipStream_t s);
-hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s);
+// fp32 w (n values) -> bf16 planes [lo; hi; mid] (planes 3) or [lo; hi; mid; hi] (planes 4).
+hipError_t split_bf16x3(const float* w, int64_t n, int planes, bf16_t* out, hipStream_t s);
 // parts (T, npieces*E) fp32 = x . [w3[0]; w3[1]; ...]^T: one GEMM over the stacked pieces, so x is
 // read once; x (T,H) bf16, w3 (npieces,E,H) bf16. splits > 1: split-K over H
 // into `splits` planes of (T, npieces*E) each.
@@ -58,13 +60,13 @@ hipError_t router_logits_f16(const f16_t* x, const f16_t* w, int T, int H, int E
                              hipStream_t s);
 hipError_t router_stats_reduce(const float* blk_psum, const float* blk_lse2, const int* blk_counts, int nblk, int E,
                                float* prob_sum, float* lse_sq_sum, int32_t* counts, hipStream_t s);
-// dl (T, ldl) fp32, or with dl3 != nullptr the bf16 planes [dl_hi | dl_lo | dl_hi] (T, 3*ldl),
+// dl (T, ldl) fp32, or with dl3 != nullptr the bf16 planes [dl_hi | dl_hi | dl_lo] (T, 3*ldl),
 // and with dl2 != nullptr also the fp16 planes [dl_hi | dl_lo] (T, 2*ldl).
 template <typename TG>
 hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const float* top_w_f32, const TG* grad_w,
                           const float* grad_logits, int T, int E, int K, int norm_topk, float* dl, bf16_t* dl3,
                           f16_t* dl2, int ldl, hipStream_t s);
-// w3t = [W_hi; W_hi; W_lo] with rows E..ldl-1 of each plane zero (3*ldl, H)
+// w3t = [W_hi; W_mid; W_hi] with rows E..ldl-1 of each plane zero (3*ldl, H)
 template <typename TW>
 hipError_t split_router_weight_bwd(const TW* w, int E, int H, int ldl, bf16_t* w3t, hipStream_t s);
 template <typename TO>

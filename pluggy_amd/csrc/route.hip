@@ -58,18 +58,22 @@ __device__ __forceinline__ float wave_fmax_dpp(float v) {
 }
 
 // One wave per row. EPL = experts per lane (E <= 64 * EPL).
-// W (E*H fp32) -> three bf16 planes hi, mid, lo with hi + mid + lo == W to
-// within 2^-24 relative (each residual is exact in fp32).
-__global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, bf16_t* __restrict__ out) {
+// W (E*H fp32) -> bf16 planes [lo; hi; mid] (and with planes == 4 a second
+// hi after them) with hi + mid + lo == W to within 2^-24 relative (each
+// residual is exact in fp32). The logits GEMM reads planes 0..2; the input
+// gradient's GEMM reads planes 1..3 = [hi; mid; hi] against dl's bf16 planes
+// [dl_hi | dl_hi | dl_lo].
+__global__ void split_bf16x3_kernel(const float* __restrict__ w, int64_t n, int planes, bf16_t* __restrict__ out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const float v = w[i];
     const bf16_t hi = f32_to_bf16(v);
     const float r1 = v - bf16_to_f32(hi);
     const bf16_t mid = f32_to_bf16(r1);
     const float r2 = r1 - bf16_to_f32(mid);
-    out[i] = hi;
-    out[n + i] = mid;
-    out[2 * n + i] = f32_to_bf16(r2);
+    out[i] = f32_to_bf16(r2);
+    out[n + i] = hi;
+    out[2 * n + i] = mid;
+    if (planes == 4) out[3 * n + i] = hi;
   }
 }
 
@@ -210,6 +214,218 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restri
   }
 }
 
+// Reductions over one 16-lane DPP row (every lane of the row ends with the
+// result; each step pairs lanes symmetrically, so all lanes hold the same
+// bits): pairs, quads, half rows (row_half_mirror), the row (row_mirror).
+__device__ __forceinline__ int row16_max(int v) {
+  v = dpp_max<0xB1, 0xf>(v);
+  v = dpp_max<0x4E, 0xf>(v);
+  v = dpp_max<0x141, 0xf>(v);
+  return dpp_max<0x140, 0xf>(v);
+}
+__device__ __forceinline__ float row16_fmax(float v) {
+  v = dpp_fmax<0xB1, 0xf>(v);
+  v = dpp_fmax<0x4E, 0xf>(v);
+  v = dpp_fmax<0x141, 0xf>(v);
+  return dpp_fmax<0x140, 0xf>(v);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_fadd(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_fadd<0xB1>(v);
+  v = dpp_fadd<0x4E>(v);
+  v = dpp_fadd<0x141>(v);
+  return dpp_fadd<0x140>(v);
+}
+
+// Router top-k with four rows per wave: each 16-lane DPP row of the wave takes
+// one token row, lane li holding experts li*V .. li*V+V-1 (E <= 16 V). The
+// same results as router_topk_kernel (logits, ids, top weights, statistics),
+// with the row reductions in 4 DPP steps instead of 6 and one ballot per pick:
+// lower lanes hold lower ids, so the lowest lane of the row whose local
+// maximum equals the row's maximum owns the pick (its lowest slot holding that
+// key). Blocks of NWB waves take 4 NWB consecutive rows. VEC: E, ldp and
+// split_stride multiples of 4 and V of 4, so a lane's loads and logit stores
+// are 16-byte vectors. The sums of the softmax run in the DPP butterfly's
+// fixed order.
+template <int V, bool VEC, typename TW>
+__global__ __launch_bounds__(256) void router_topk16_kernel(const float* __restrict__ parts, int nsplit,
+                                                            int64_t split_stride, int64_t ldp, float* logits,
+                                                            const float* __restrict__ bias, int T, int E, int K,
+                                                            int norm_topk, TW* __restrict__ top_w,
+                                                            int64_t* __restrict__ top_idx,
+                                                            float* __restrict__ top_w_f32,
+                                                            float* __restrict__ blk_psum,
+                                                            float* __restrict__ blk_lse2,
+                                                            int* __restrict__ blk_counts) {
+  static_assert(!VEC || V % 4 == 0, "16-byte lane slices");
+  // LDS: [R][E] psum partials, [E] counts, [R] lse2, then per row K picks (id, p)
+  extern __shared__ float sh[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwb = blockDim.x >> 6;
+  const int R = 4 * nwb;  // rows of the block
+  const int li = lane & 15, rg = lane >> 4;
+  const int rb = wave * 4 + rg;  // row within the block
+  float* s_psum = sh;
+  int* s_cnt = reinterpret_cast<int*>(sh + R * E);
+  float* s_lse2 = sh + (R + 1) * E;
+  int* s_pid = reinterpret_cast<int*>(sh + (R + 1) * E + R);
+  float* s_pp = sh + (R + 1) * E + R + R * K;
+  for (int e = tid; e < E; e += blockDim.x) s_cnt[e] = 0;
+  __syncthreads();
+
+  const int row = blockIdx.x * R + rb;
+  const bool live = row < T;
+  const int64_t rowc = live ? row : T - 1;  // dead rows read a live row and write nothing
+  const bool write_logits = nsplit > 1 || bias != nullptr || parts != logits;
+  const int e0 = li * V;
+
+  // ---- logits of the lane's V experts: every plane's loads, then the in-order sums
+  float v[V];
+  {
+    float acc[V];
+    if constexpr (VEC) {
+      // chunks past E read the row's last chunk (E >= 4), whose values are masked below
+      float4 pl[kMaxSplits][V / 4];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < nsplit) {
+#pragma unroll
+          for (int c = 0; c < V / 4; ++c) {
+            const int ec = min(e0 + 4 * c, E - 4);
+            pl[sp][c] = *reinterpret_cast<const float4*>(parts + sp * split_stride + rowc * ldp + ec);
+          }
+        }
+#pragma unroll
+      for (int c = 0; c < V / 4; ++c) {
+        float4 x = pl[0][c];
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplits; ++sp)
+          if (sp < nsplit) {
+            x.x += pl[sp][c].x; x.y += pl[sp][c].y; x.z += pl[sp][c].z; x.w += pl[sp][c].w;
+          }
+        acc[4 * c] = x.x; acc[4 * c + 1] = x.y; acc[4 * c + 2] = x.z; acc[4 * c + 3] = x.w;
+      }
+    } else {
+      float pl[kMaxSplits][V];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < nsplit) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) pl[sp][j] = parts[sp * split_stride + rowc * ldp + min(e0 + j, E - 1)];
+        }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float x = pl[0][j];
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplits; ++sp)
+          if (sp < nsplit) x += pl[sp][j];
+        acc[j] = x;
+      }
+    }
+    if (bias != nullptr) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] += bias[min(e0 + j, E - 1)];
+    }
+    if (live && write_logits && e0 < E) {
+      float* lrow = logits + (int64_t)row * E;
+      if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < V / 4; ++c)
+          if (e0 + 4 * c < E)
+            *reinterpret_cast<float4*>(lrow + e0 + 4 * c) =
+                make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if (e0 + j < E) lrow[e0 + j] = acc[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = e0 + j < E ? acc[j] : -INFINITY;
+  }
+
+  // ---- softmax statistics of the row
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < V; ++j) m = fmaxf(m, v[j]);
+  m = row16_fmax(m);
+  float ex[V];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    ex[j] = e0 + j < E ? expf(v[j] - m) : 0.0f;
+    s += ex[j];
+  }
+  s = row16_sum(s);
+  const float inv_s = 1.0f / s;
+  const float lse = m + logf(s);
+
+  // ---- top-k by (logit desc, id asc); NaN ranks as -inf, picked and padding
+  // slots hold INT_MIN (below every logit's key), so K <= E picks find valid ids
+  int key[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) key[j] = e0 + j < E ? rank_key(nan_to_neg_inf(v[j])) : INT_MIN;
+  int* pid = s_pid + rb * K;
+  float* pp = s_pp + rb * K;
+  for (int k = 0; k < K; ++k) {
+    int lm = key[0];
+#pragma unroll
+    for (int j = 1; j < V; ++j) lm = max(lm, key[j]);
+    const int km = row16_max(lm);
+    const unsigned long long hit = __ballot(lm == km);
+    const unsigned mrow = (unsigned)(hit >> (16 * rg)) & 0xffffu;
+    const bool owner = li == __builtin_ctz(mrow);
+    // the owner's lowest slot holding the key
+    int jsel = V - 1;
+#pragma unroll
+    for (int j = V - 2; j >= 0; --j)
+      if (key[j] == km) jsel = j;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (owner && j == jsel) key[j] = INT_MIN;
+    if (owner) {
+      pid[k] = e0 + jsel;
+      pp[k] = expf(key_value(km) - m) * inv_s;
+    }
+  }
+  // the picks' probabilities summed in pick order (every lane of the row alike)
+  __syncthreads();
+  float psum_sel = 0.0f;
+  for (int k = 0; k < K; ++k) psum_sel += pp[k];
+  if (live) {
+    for (int k = li; k < K; k += 16) {
+      const int e = pid[k];
+      const float p = pp[k];
+      const float w = norm_topk ? p / psum_sel : p;
+      const int64_t o = (int64_t)row * K + k;
+      top_idx[o] = e;
+      top_w_f32[o] = w;
+      store_scalar<TW>(top_w + o, w);
+      atomicAdd(&s_cnt[e], 1);
+    }
+  }
+  // ---- fixed-order block reduction of the statistics (deterministic)
+#pragma unroll
+  for (int j = 0; j < V; ++j)
+    if (e0 + j < E) s_psum[rb * E + e0 + j] = live ? ex[j] * inv_s : 0.0f;
+  if (li == 0) s_lse2[rb] = live ? lse * lse : 0.0f;
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {
+    float t = s_psum[e];
+    for (int r = 1; r < R; ++r) t += s_psum[r * E + e];
+    blk_psum[(int64_t)blockIdx.x * E + e] = t;
+    blk_counts[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+  }
+  if (tid == 0) {
+    float t = s_lse2[0];
+    for (int r = 1; r < R; ++r) t += s_lse2[r];
+    blk_lse2[blockIdx.x] = t;
+  }
+}
+
 // One wave per expert (and one more for the lse^2 total): lane l sums the
 // partials b = l, l + 64, ... in order, then a fixed butterfly combines lanes,
 // so the result is the same on every run.
@@ -329,13 +545,13 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
         dl[(int64_t)row * ldl + e] = val;
       } else {
         // val = hi + lo to 2^-16 relative; hi appears twice so that
-        // [hi | lo | hi] . [W_hi; W_hi; W_lo] = dl . W to that precision.
+        // [hi | hi | lo] . [W_hi; W_mid; W_hi] = dl . W to that precision.
         const bf16_t hi = f32_to_bf16(val);
         const bf16_t lo = f32_to_bf16(val - bf16_to_f32(hi));
         bf16_t* o = dl3 + (int64_t)row * 3 * ldl;
         o[e] = hi;
-        o[ldl + e] = lo;
-        o[2 * ldl + e] = hi;
+        o[ldl + e] = hi;
+        o[2 * ldl + e] = lo;
       }
       if (dl2 != nullptr) {
         // fp16 planes for the fp16 weight gradient: val = hi + lo to 2^-22
@@ -364,6 +580,9 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
   }
 }
 
+// w3t = [W_hi; W_mid; W_hi] (3*ldl, H), W_mid = bf16(W - W_hi), rows E..ldl-1
+// of each plane zero: the input gradient's GEMM operand against dl's planes
+// [dl_hi | dl_hi | dl_lo] (planes 1..3 of split_bf16x3's four-plane form).
 template <typename TW>
 __global__ void split_router_weight_bwd_kernel(const TW* __restrict__ w, int E, int H, int ldl,
                                                bf16_t* __restrict__ w3t) {
@@ -373,8 +592,8 @@ __global__ void split_router_weight_bwd_kernel(const TW* __restrict__ w, int E, 
     const float v = e < E ? load_scalar<TW>(w + i) : 0.0f;
     const bf16_t hi = f32_to_bf16(v);
     w3t[i] = hi;
-    w3t[n + i] = hi;
-    w3t[2 * n + i] = f32_to_bf16(v - bf16_to_f32(hi));
+    w3t[n + i] = f32_to_bf16(v - bf16_to_f32(hi));
+    w3t[2 * n + i] = hi;
   }
 }
 
@@ -859,10 +1078,11 @@ unsigned blocks_for(int64_t rows, int per_block) { return (unsigned)((rows + per
 
 }  // namespace
 
-hipError_t split_bf16x3(const float* w, int64_t n, bf16_t* out, hipStream_t s) {
+hipError_t split_bf16x3(const float* w, int64_t n, int planes, bf16_t* out, hipStream_t s) {
   if (n == 0) return hipSuccess;
+  if (planes != 3 && planes != 4) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 2048);
-  hipLaunchKernelGGL(split_bf16x3_kernel, dim3(grid), dim3(256), 0, s, w, n, out);
+  hipLaunchKernelGGL(split_bf16x3_kernel, dim3(grid), dim3(256), 0, s, w, n, planes, out);
   return hipGetLastError();
 }
 
@@ -873,9 +1093,27 @@ hipError_t router_topk(const float* parts, int nsplit, int64_t split_stride, int
                        hipStream_t s) {
   if (T == 0) return hipSuccess;
   if (nsplit < 1 || nsplit > kMaxSplits) return hipErrorInvalidValue;
-  // one wave per row of the block
   if (rows_per_block < 1 || rows_per_block > 16) return hipErrorInvalidValue;
   const unsigned grid = blocks_for(T, rows_per_block);
+  if (E <= 256 && rows_per_block % 4 == 0) {
+    // four rows per wave: the same blocks of rows, a quarter of the waves
+    const unsigned threads16 = 16u * (unsigned)rows_per_block;
+    const size_t shmem16 =
+        (size_t)((rows_per_block + 1) * E + rows_per_block + 2 * rows_per_block * K) * sizeof(float);
+    const bool vec = E % 4 == 0 && ldp % 4 == 0 && split_stride % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(parts) & 15) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+#define PMOE_TOPK16(V, VEC)                                                                                        \
+  hipLaunchKernelGGL((router_topk16_kernel<V, VEC, TW>), dim3(grid), dim3(threads16), shmem16, s, parts, nsplit,   \
+                     split_stride, ldp, logits, logit_bias, T, E, K, norm_topk, top_w, top_idx, top_w_f32, blk_psum, \
+                     blk_lse2, blk_counts)
+    if (E <= 16) PMOE_TOPK16(1, false);
+    else if (E <= 32) PMOE_TOPK16(2, false);
+    else if (E <= 64) { if (vec) PMOE_TOPK16(4, true); else PMOE_TOPK16(4, false); }
+    else if (E <= 128) { if (vec) PMOE_TOPK16(8, true); else PMOE_TOPK16(8, false); }
+    else { if (vec) PMOE_TOPK16(16, true); else PMOE_TOPK16(16, false); }
+#undef PMOE_TOPK16
+    return hipGetLastError();
+  }
   const unsigned threads = 64u * (unsigned)rows_per_block;
   const size_t shmem = (size_t)((rows_per_block + 1) * E + rows_per_block) * sizeof(float);
 #define PMOE_TOPK_CASE(EPL)                                                                                        \

@@ -191,7 +191,8 @@ def _pad_experts(gate_up_proj: torch.Tensor, down_proj: torch.Tensor, Hp: int, I
 
 
 # 16-bit copies of fp32 master weights kept across calls (see weight_cast_cache):
-# (id(master), dtype) -> (weakref to the master, (version, data_ptr, shape, stride), copy)
+# (id(master), tag) -> (weakref to the master, (version, data_ptr, shape, stride), copy);
+# the tag is the copy's dtype, or "router_pieces" for a router weight's bf16 pieces
 _cast_cache: dict[int, tuple] = {}
 _cast_cache_on = False
 
@@ -212,7 +213,8 @@ def weight_cast_cache(enabled: bool = True):
     seen: inside the context, change masters through the tensor itself (or
     leave the context). The copies stay alive as long as their masters (half
     the masters' bytes). Eager mode only: under ``torch.compile`` every call
-    casts, as without the context.
+    casts, as without the context. The bf16 pieces of an fp32 router weight
+    beside bf16 activations (``_router_pieces``) are kept the same way.
     """
     global _cast_cache_on
     prev, _cast_cache_on = _cast_cache_on, bool(enabled)
@@ -224,16 +226,44 @@ def weight_cast_cache(enabled: bool = True):
             _cast_cache.clear()
 
 
-def _cached_copy(w: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
-    key = (id(w), dt)
+def _cached(w: torch.Tensor, tag, make) -> torch.Tensor:
+    """``make(w)`` (a tensor derived from ``w``), kept under ``(id(w), tag)``
+    while ``w`` is unchanged (version counter, storage and layout)."""
+    key = (id(w), tag)
     state = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()))
     hit = _cast_cache.get(key)
     if hit is not None and hit[0]() is w and hit[1] == state:
         return hit[2]
     with torch.no_grad():
-        copy = w.detach().to(dt).contiguous()
-    _cast_cache[key] = (weakref.ref(w, lambda _r, k=key: _cast_cache.pop(k, None)), state, copy)
-    return copy
+        val = make(w.detach())
+    _cast_cache[key] = (weakref.ref(w, lambda _r, k=key: _cast_cache.pop(k, None)), state, val)
+    return val
+
+
+def _cached_copy(w: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    return _cached(w, dt, lambda t: t.to(dt).contiguous())
+
+
+def _router_pieces(x_dtype: torch.dtype, rw: torch.Tensor, source: torch.Tensor | None = None):
+    """The bf16 pieces (``ops.split_router_weight``) of the fp32 router weight
+    operand ``rw`` beside bf16 activations, the three-piece logits GEMM's
+    operand: the forward splits the weight once and its backward reuses the
+    pieces instead of splitting it again. Inside ``weight_cast_cache`` they are
+    kept across calls while ``rw`` is unchanged, when ``rw`` is the parameter
+    ``source`` itself. None for other pairings, for E not a multiple of 8 and
+    under ``torch.compile``; the kernels then split the weight inside each call,
+    with the same bits."""
+    if (x_dtype != torch.bfloat16 or rw.dtype != torch.float32 or rw.shape[0] % 8 or not rw.is_cuda
+            or torch.compiler.is_compiling()):
+        return None
+    def split(w):
+        with _stage("router_split"):
+            return ops.split_router_weight(w)
+
+    if _cast_cache_on and source is rw and rw.is_leaf:
+        return _cached(rw, "router_pieces", split)
+    with torch.no_grad():
+        return split(rw.detach().contiguous())
 
 
 def _compute_weight(w: torch.Tensor, dt: torch.dtype) -> tuple[torch.Tensor, torch.Tensor | None]:
@@ -300,15 +330,16 @@ def _empty_like_none(ref: torch.Tensor) -> torch.Tensor:
 
 
 @torch.library.custom_op("pmoe::router_fwd", mutates_args=(),
-                         schema="(Tensor x, Tensor weight, int top_k, bool norm_topk_prob, Tensor? logit_bias) -> "
-                                "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
-def _router_fwd(x, weight, top_k, norm_topk_prob, logit_bias):
+                         schema="(Tensor x, Tensor weight, int top_k, bool norm_topk_prob, Tensor? logit_bias, "
+                                "Tensor? pieces=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _router_fwd(x, weight, top_k, norm_topk_prob, logit_bias, pieces=None):
+    """``pieces``: the fp32 weight's bf16 pieces (``_router_pieces``) or None."""
     with _stage("router_fwd"):
-        return ops.router_forward(x, weight, top_k, norm_topk_prob, logit_bias)
+        return ops.router_forward(x, weight, top_k, norm_topk_prob, logit_bias, pieces=pieces)
 
 
 @_router_fwd.register_fake
-def _(x, weight, top_k, norm_topk_prob, logit_bias):
+def _(x, weight, top_k, norm_topk_prob, logit_bias, pieces=None):
     T, E, K = x.shape[0], weight.shape[0], top_k
     f32 = torch.float32
     return (x.new_empty(T, E, dtype=f32), x.new_empty(T, K), x.new_empty(T, K, dtype=torch.int64),
@@ -318,38 +349,40 @@ def _(x, weight, top_k, norm_topk_prob, logit_bias):
 
 @torch.library.custom_op("pmoe::router_bwd", mutates_args=(),
                          schema="(Tensor x, Tensor weight, Tensor logits, Tensor top_i, Tensor top_w32, "
-                                "Tensor? grad_top_w, Tensor? grad_logits, bool norm_topk_prob) -> (Tensor, Tensor)")
-def _router_bwd(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob):
+                                "Tensor? grad_top_w, Tensor? grad_logits, bool norm_topk_prob, Tensor? pieces=None) "
+                                "-> (Tensor, Tensor)")
+def _router_bwd(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob, pieces=None):
     _refuse_capture("router_bwd")
     with _stage("router_bwd"):
-        return ops.router_backward(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob)
+        return ops.router_backward(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob,
+                                   pieces=pieces)
 
 
 @_router_bwd.register_fake
-def _(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob):
+def _(x, weight, logits, top_i, top_w32, grad_top_w, grad_logits, norm_topk_prob, pieces=None):
     return torch.empty_like(x), torch.empty_like(weight)
 
 
 def _router_setup(ctx, inputs, output):
-    x, weight, top_k, norm_topk_prob, logit_bias = inputs
+    x, weight, top_k, norm_topk_prob, logit_bias, pieces = inputs
     logits, top_w, top_i, top_w32, counts, psum, lse2 = output
-    ctx.save_for_backward(x, weight, logits, top_i, top_w32)
+    ctx.save_for_backward(x, weight, logits, top_i, top_w32, pieces)
     ctx.norm_topk_prob = bool(norm_topk_prob)
     ctx.mark_non_differentiable(top_i, top_w32, counts, psum, lse2)
     ctx.set_materialize_grads(False)  # absent gradients stay None (no zero-filled tensors)
 
 
 def _router_backward(ctx, g_logits, g_w, _gi, _gw32, _gc, _gp, _gl):
-    x, weight, logits, top_i, top_w32 = ctx.saved_tensors
+    x, weight, logits, top_i, top_w32, pieces = ctx.saved_tensors
     need = ctx.needs_input_grad
     if not (need[0] or need[1]) or (g_logits is None and g_w is None):
-        return None, None, None, None, None
+        return None, None, None, None, None, None
     if g_logits is not None:
         g_logits = g_logits.float().contiguous()
     if g_w is not None:
         g_w = g_w.contiguous()
-    gx, gW = torch.ops.pmoe.router_bwd(x, weight, logits, top_i, top_w32, g_w, g_logits, ctx.norm_topk_prob)
-    return (gx if need[0] else None), (gW if need[1] else None), None, None, None
+    gx, gW = torch.ops.pmoe.router_bwd(x, weight, logits, top_i, top_w32, g_w, g_logits, ctx.norm_topk_prob, pieces)
+    return (gx if need[0] else None), (gW if need[1] else None), None, None, None, None
 
 
 _router_fwd.register_autograd(_router_backward, setup_context=_router_setup)
@@ -377,7 +410,7 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int, norm_top
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
     logits, top_w, top_i, _w32, counts, psum, lse2 = torch.ops.pmoe.router_fwd(
-        x, w, int(top_k), bool(norm_topk_prob), logit_bias)
+        x, w, int(top_k), bool(norm_topk_prob), logit_bias, _router_pieces(x.dtype, w, weight))
     top_w = top_w.to(hidden.dtype)  # the reference returns them in x.dtype (qwen3_moe.py:177)
     if return_stats:
         return logits, top_w, top_i, RouterStats(counts, psum, lse2, x.shape[0])
@@ -582,28 +615,31 @@ _expert_ffn_fwd.register_autograd(_ffn_backward, setup_context=_ffn_setup)
 @torch.library.custom_op("pmoe::sparse_moe_fwd", mutates_args=(),
                          schema="(Tensor x, Tensor router_weight, Tensor gate_up_proj, Tensor down_proj, int top_k, "
                                 "bool norm_topk_prob, Tensor? logit_bias, Tensor? gate_up_master=None, "
-                                "Tensor? down_master=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, "
-                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+                                "Tensor? down_master=None, Tensor? router_pieces=None) -> (Tensor, Tensor, Tensor, "
+                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+                                "Tensor)")
 def _sparse_moe_fwd(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias,
-                    gate_up_master=None, down_master=None):
+                    gate_up_master=None, down_master=None, router_pieces=None):
     """Router + dropless experts (Qwen3MoeSparseMLP.forward) as one op.
 
     -> out, router_logits, counts, prob_sum, lse_sq_sum, then what the backward
     reads: top_i, top_w32, top_w, offs, inv_pos, sorted_token, sorted_w, gu,
     mid. The masters, when given, are the differentiable fp32 weights whose
     bf16 copies gate_up_proj / down_proj are (their gradients are written in
-    fp32).
+    fp32). router_pieces: the router weight's bf16 pieces (``_router_pieces``),
+    reused by the backward, or None.
     """
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-            _router_x(x, router_weight), router_weight, top_k, norm_topk_prob, logit_bias, tw_dtype=x.dtype)
+            _router_x(x, router_weight), router_weight, top_k, norm_topk_prob, logit_bias, tw_dtype=x.dtype,
+            pieces=router_pieces)
     out, offs, inv_pos, stok, sw, gu, mid = _ffn_forward(x, top_i, top_w, gate_up_proj, down_proj)
     return out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid
 
 
 @_sparse_moe_fwd.register_fake
 def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gate_up_master=None,
-      down_master=None):
+      down_master=None, router_pieces=None):
     T, E, K = x.shape[0], router_weight.shape[0], top_k
     I = gate_up_proj.shape[1] // 2
     f32 = torch.float32
@@ -614,11 +650,12 @@ def _(x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bi
 
 
 def _sparse_setup(ctx, inputs, output):
-    x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master, dn_master = inputs
+    (x, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master, dn_master,
+     router_pieces) = inputs
     (out, logits, counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid) = output
     ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
     ctx.save_for_backward(x, router_weight, logits, top_i, top_w32, gate_up_proj, down_proj, offs, inv_pos, stok,
-                          sw, gu, mid)
+                          sw, gu, mid, router_pieces)
     ctx.norm_topk_prob = bool(norm_topk_prob)
     ctx.dims = (x.shape[0], int(top_k))
     ctx.mark_non_differentiable(counts, psum, lse2, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu, mid)
@@ -629,12 +666,13 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     """The down dgrad comes first (it yields the routing weights' gradient), then
     the router's backward, whose input gradient is added inside the dispatch
     backward, so the two input gradients are never summed by a separate pass."""
-    (x, rw, logits, top_i, top_w32, gate_up, down, offs, inv_pos, stok, sw, gu, mid) = ctx.saved_tensors
+    (x, rw, logits, top_i, top_w32, gate_up, down, offs, inv_pos, stok, sw, gu, mid, pieces) = ctx.saved_tensors
     T, K = ctx.dims
-    need = _needs(ctx, 9)  # x, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
+    # x, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master, router_pieces
+    need = _needs(ctx, 10)
     need_gu, need_dn = need[2] or need[7], need[3] or need[8]
     if g_out is None and g_logits is None:
-        return (None,) * 9
+        return (None,) * 10
     if g_logits is not None:
         g_logits = g_logits.float().contiguous()
     g_x = g_rw = g_gu_w = g_dn_w = None
@@ -649,7 +687,7 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     gx_router = None
     if need[0] or need[1]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(_router_x(x, rw), rw, logits, top_i, top_w32, g_tw, g_logits,
-                                                    ctx.norm_topk_prob)
+                                                    ctx.norm_topk_prob, pieces)
         gx_router = gx_router.to(x.dtype)  # fp32 when fp16 x met a non-fp16 weight
     if g_gu is not None and (need[0] or need_gu or need_dn):
         g_hidden, g_gu_w, g_dn_w = torch.ops.pmoe.expert_bwd(
@@ -661,7 +699,8 @@ def _sparse_backward(ctx, g_out, g_logits, *_rest):
     elif need[0]:
         g_x = gx_router
     return ((g_x if need[0] else None), (g_rw if need[1] else None), g_gu_w if need[2] else None,
-            g_dn_w if need[3] else None, None, None, None, g_gu_w if need[7] else None, g_dn_w if need[8] else None)
+            g_dn_w if need[3] else None, None, None, None, g_gu_w if need[7] else None, g_dn_w if need[8] else None,
+            None)
 
 
 _sparse_moe_fwd.register_autograd(_sparse_backward, setup_context=_sparse_setup)
@@ -691,8 +730,9 @@ def sparse_moe_block(hidden: torch.Tensor, router_weight: torch.Tensor, gate_up_
     gu, gu_master, dn, dn_master = _expert_weights(gate_up_proj, down_proj, dt, Hp, Ip)
     if logit_bias is not None:
         logit_bias = logit_bias.float().contiguous()
+    pieces = _router_pieces(dt, rw, router_weight)
     out, logits, counts, psum, lse2 = torch.ops.pmoe.sparse_moe_fwd(x, rw, gu, dn, int(top_k), bool(norm_topk_prob),
-                                                                     logit_bias, gu_master, dn_master)[:5]
+                                                                     logit_bias, gu_master, dn_master, pieces)[:5]
     return out[:, :H].to(hidden.dtype), logits, RouterStats(counts, psum, lse2, T)
 
 
@@ -737,24 +777,25 @@ def moe_expert_ffn(
 @torch.library.custom_op("pmoe::moe_sublayer_fwd", mutates_args=(),
                          schema="(Tensor x, Tensor norm_weight, float eps, Tensor router_weight, Tensor gate_up_proj, "
                                 "Tensor down_proj, int top_k, bool norm_topk_prob, Tensor? logit_bias, "
-                                "Tensor? gate_up_master=None, Tensor? down_master=None) -> (Tensor, "
-                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
-                                "Tensor, Tensor, Tensor, Tensor, Tensor)")
+                                "Tensor? gate_up_master=None, Tensor? down_master=None, Tensor? router_pieces=None) "
+                                "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+                                "Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
 def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob,
-                      logit_bias, gate_up_master=None, down_master=None):
+                      logit_bias, gate_up_master=None, down_master=None, router_pieces=None):
     """x + SparseMLP(RMSNorm(x)) with the norm and the residual add in the row kernels.
 
     The kernels compute in gate_up_proj's dtype; x is the residual stream (its
     own dtype). -> out, router_logits, counts, prob_sum, lse_sq_sum, then what
     the backward reads: normed, rstd, top_i, top_w32, top_w, offs, inv_pos,
     sorted_token, sorted_w, gu, mid. The masters, when given, are the
-    differentiable fp32 weights whose bf16 copies gate_up_proj / down_proj are.
+    differentiable fp32 weights whose bf16 copies gate_up_proj / down_proj are;
+    router_pieces, the router weight's bf16 pieces (``_router_pieces``) or None.
     """
     with _stage("rmsnorm"):
         normed, rstd = ops.rmsnorm_forward(x, norm_weight, eps, gate_up_proj.dtype)
     with _stage("router_fwd"):
         logits, top_w, top_i, top_w32, counts, psum, lse2 = ops.router_forward(
-            normed, router_weight, top_k, norm_topk_prob, logit_bias)
+            normed, router_weight, top_k, norm_topk_prob, logit_bias, pieces=router_pieces)
     with _stage("permute"):
         _, offs, _sorted_pair, inv_pos, stok, sw = ops.permute_rows(top_i, top_w, gate_up_proj.shape[0])
     with _stage("gate_up_fwd"):
@@ -768,7 +809,7 @@ def _moe_sublayer_fwd(x, norm_weight, eps, router_weight, gate_up_proj, down_pro
 
 @_moe_sublayer_fwd.register_fake
 def _(x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias,
-      gate_up_master=None, down_master=None):
+      gate_up_master=None, down_master=None, router_pieces=None):
     T, H = x.shape
     E, K, I = router_weight.shape[0], top_k, gate_up_proj.shape[1] // 2
     cdt = gate_up_proj.dtype
@@ -826,12 +867,12 @@ def _(g_gu, grad_out_c, normed, gate_up, down, offs, inv_pos, sorted_token, mid,
 
 def _sublayer_setup(ctx, inputs, output):
     (x, norm_weight, eps, router_weight, gate_up_proj, down_proj, top_k, norm_topk_prob, logit_bias, gu_master,
-     dn_master) = inputs
+     dn_master, router_pieces) = inputs
     ctx.f32_wgrads = _f32_wgrads(gu_master, dn_master)
     (out, logits, counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu,
      mid) = output
     ctx.save_for_backward(x, norm_weight, rstd, normed, router_weight, logits, top_i, top_w32, gate_up_proj,
-                          down_proj, offs, inv_pos, stok, sw, gu, mid)
+                          down_proj, offs, inv_pos, stok, sw, gu, mid, router_pieces)
     ctx.norm_topk_prob = bool(norm_topk_prob)
     ctx.top_k = int(top_k)
     ctx.mark_non_differentiable(counts, psum, lse2, normed, rstd, top_i, top_w32, top_w, offs, inv_pos, stok, sw, gu,
@@ -844,11 +885,12 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
     the residual term, the router's share and the K expert rows are all summed
     inside the one row pass of the dispatch backward."""
     (x, nw, rstd, normed, rw, logits, top_i, top_w32, gate_up, down, offs, inv_pos, stok, sw, gu,
-     mid) = ctx.saved_tensors
-    # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master
-    need = _needs(ctx, 11)
+     mid, pieces) = ctx.saved_tensors
+    # x, norm_weight, eps, router_weight, gate_up, down, top_k, norm, bias, gate_up_master, down_master,
+    # router_pieces
+    need = _needs(ctx, 12)
     need_gu, need_dn = need[4] or need[9], need[5] or need[10]
-    nones = (None,) * 11
+    nones = (None,) * 12
     if g_out is None and g_logits is None:
         return nones
     if g_logits is not None:
@@ -864,7 +906,7 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
     gx_router = g_rw = None
     if need[0] or need[1] or need[3]:
         gx_router, g_rw = torch.ops.pmoe.router_bwd(normed, rw, logits, top_i, top_w32, g_tw, g_logits,
-                                                    ctx.norm_topk_prob)
+                                                    ctx.norm_topk_prob, pieces)
     needs = [bool(need[0]), bool(need[1]), bool(need_gu) and g_gu is not None, bool(need_dn) and g_gu is not None]
     g_x = g_nw = g_gu_w = g_dn_w = None
     if any(needs):
@@ -875,7 +917,7 @@ def _sublayer_backward(ctx, g_out, g_logits, *_rest):
         g_x, g_nw, g_gu_w, g_dn_w = (_none_if_empty(t) for t in (g_x, g_nw, g_gu_w, g_dn_w))
     return (g_x if need[0] else None, g_nw if need[1] else None, None, g_rw if need[3] else None,
             g_gu_w if need[4] else None, g_dn_w if need[5] else None, None, None, None, g_gu_w if need[9] else None,
-            g_dn_w if need[10] else None)
+            g_dn_w if need[10] else None, None)
 
 
 _moe_sublayer_fwd.register_autograd(_sublayer_backward, setup_context=_sublayer_setup)
@@ -918,8 +960,8 @@ def moe_sublayer(x: torch.Tensor, norm: torch.nn.RMSNorm, mlp) -> torch.Tensor:
     dn, dn_master = _compute_weight(mlp.experts.down_proj, cdt)
     bias = r.logit_bias.float().contiguous() if r.logit_bias is not None else None
     out, logits, counts, psum, lse2 = torch.ops.pmoe.moe_sublayer_fwd(
-        flat, nw.contiguous(), float(eps), rw.contiguous(), gu, dn, int(r.top_k), bool(r.norm_topk_prob), bias,
-        gu_master, dn_master)[:5]
+        flat, nw.contiguous(), float(eps), rw, gu, dn, int(r.top_k), bool(r.norm_topk_prob), bias,
+        gu_master, dn_master, _router_pieces(cdt, rw, r.weight))[:5]
     r.last_stats = RouterStats(counts, psum, lse2, flat.shape[0])
     mlp.last_router_logits = logits
     return out.reshape(B, S, H)

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import call, dtype_code, ptr, require_gpu, size, stream_of, workspace
+from ._lib import PMOE_BF16X3, call, dtype_code, ptr, require_gpu, size, stream_of, workspace
 
 
 def _dims(gate_up_proj: torch.Tensor):
@@ -17,9 +17,30 @@ def _dims(gate_up_proj: torch.Tensor):
     return E, H, two_i // 2
 
 
-def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bias=None, tw_dtype=None):
+def split_router_weight(weight):
+    """-> the bf16 pieces (4E, H) of an fp32 router weight (E, H), which
+    ``router_forward`` / ``router_backward`` take as ``pieces`` beside bf16 x."""
+    require_gpu(weight)
+    assert weight.dtype == torch.float32 and weight.dim() == 2 and weight.is_contiguous()
+    E, H = weight.shape
+    pieces = torch.empty(4 * E, H, dtype=torch.bfloat16, device=weight.device)
+    call("pmoe_router_split_weight", ptr(weight), E, H, ptr(pieces), stream_of(weight))
+    return pieces
+
+
+def _router_weight_arg(weight, pieces):
+    """(pointer, dtype code) of the router weight operand: the pieces of an
+    fp32 weight when given, else the weight itself."""
+    if pieces is not None:
+        assert weight.dtype == torch.float32 and pieces.shape == (4 * weight.shape[0], weight.shape[1])
+        return ptr(pieces), PMOE_BF16X3
+    return ptr(weight), dtype_code(weight.dtype)
+
+
+def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bias=None, tw_dtype=None,
+                   pieces=None):
     """-> logits, top_w (tw_dtype, default x.dtype), top_i (int64), top_w_f32, counts (int32), prob_sum,
-    lse_sq_sum."""
+    lse_sq_sum. ``pieces``: ``split_router_weight(weight)``, for bf16 x beside an fp32 weight."""
     require_gpu(x, weight, logit_bias)
     T, H = x.shape
     E = weight.shape[0]
@@ -33,22 +54,25 @@ def router_forward(x, weight, top_k: int, norm_topk_prob: bool = True, logit_bia
     psum = torch.empty(E, dtype=torch.float32, device=dev)
     lse2 = torch.empty(1, dtype=torch.float32, device=dev)
     ws = workspace(size("pmoe_router_forward_workspace_size", T, H, E), dev)
-    call("pmoe_router_forward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype), ptr(logit_bias),
+    w_ptr, w_code = _router_weight_arg(weight, pieces)
+    call("pmoe_router_forward", ptr(x), dtype_code(x.dtype), w_ptr, w_code, ptr(logit_bias),
          T, H, E, top_k, int(norm_topk_prob), ptr(logits), ptr(top_w), dtype_code(tw_dtype), ptr(top_i),
          ptr(top_w32), ptr(counts), ptr(psum), ptr(lse2), ptr(ws), ws.numel(), stream_of(x))
     return logits, top_w, top_i, top_w32, counts, psum, lse2
 
 
 def router_backward(x, weight, logits, top_i, top_w32, grad_top_w=None, grad_logits=None,
-                    norm_topk_prob: bool = True):
-    """-> grad_x (x.dtype), grad_weight (weight.dtype)."""
+                    norm_topk_prob: bool = True, pieces=None):
+    """-> grad_x (x.dtype), grad_weight (weight.dtype). ``pieces`` as in
+    ``router_forward`` (the forward's, so the weight is split once)."""
     T, H = x.shape
     E, K = weight.shape[0], top_i.shape[1]
     gx = torch.empty_like(x)
     gW = torch.empty_like(weight)
     gw_code = dtype_code(grad_top_w.dtype) if grad_top_w is not None else 0
     ws = workspace(size("pmoe_router_backward_workspace_size", T, H, E), x.device)
-    call("pmoe_router_backward", ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype), ptr(logits),
+    w_ptr, w_code = _router_weight_arg(weight, pieces)
+    call("pmoe_router_backward", ptr(x), dtype_code(x.dtype), w_ptr, w_code, ptr(logits),
          ptr(top_i), ptr(top_w32), ptr(grad_top_w), gw_code, ptr(grad_logits), T, H, E, K, int(norm_topk_prob),
          ptr(gx), ptr(gW), ptr(ws), ws.numel(), stream_of(x))
     return gx, gW

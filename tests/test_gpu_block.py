@@ -514,6 +514,69 @@ def test_fp32_masters_any_size_under_autocast():
     check_close("d down_proj (fp32)", mlp.experts.down_proj.grad, ref[5], 1e-2, frac)
 
 
+def test_router_weight_is_split_once_per_step_and_cached():
+    """bf16 activations beside an fp32 router weight: the forward splits the
+    weight into its bf16 pieces once and its backward reuses them (one split
+    per step); inside pluggy_amd.weight_cast_cache the pieces are kept across
+    steps until the weight changes in place. Outputs and gradients equal, bit
+    for bit, the path where the kernels split the weight inside every call."""
+    import pluggy_amd.moe as M
+
+    pa = _mod()
+    T, H, E, K, I = 512, 256, 16, 4, 128
+    say(f"router pieces T={T} H={H} E={E} K={K} I={I}")
+    g = gen(71)
+    x = torch.randn(T, H, generator=g).bfloat16().to(DEV)
+    gout = torch.randn(T, H, generator=g).bfloat16().to(DEV)
+    mlp = pa.Qwen3MoeSparseMLP(H, I, E, K).to(DEV)
+    with torch.no_grad():
+        for prm in mlp.parameters():
+            prm.copy_(torch.randn(prm.shape, generator=g) * 0.05)
+    mlp.experts.gate_up_proj.data = mlp.experts.gate_up_proj.data.bfloat16()
+    mlp.experts.down_proj.data = mlp.experts.down_proj.data.bfloat16()
+    assert mlp.router.weight.dtype == torch.float32
+
+    def step():
+        mlp.zero_grad(set_to_none=True)
+        xg = x.clone().reshape(1, T, H).requires_grad_(True)
+        out = mlp(xg)
+        out.reshape(T, H).backward(gout)
+        return [out.detach().clone(), xg.grad.clone()] + [p.grad.clone() for p in mlp.parameters()]
+
+    def unsplit_step():
+        orig = M._router_pieces
+        M._router_pieces = lambda *a, **k: None
+        try:
+            return step()
+        finally:
+            M._router_pieces = orig
+
+    real, n = M.ops.split_router_weight, [0]
+
+    def counting(w):
+        n[0] += 1
+        return real(w)
+
+    plain = unsplit_step()
+    M.ops.split_router_weight = counting
+    try:
+        first = step()
+        assert n[0] == 1, "one split per step, reused by the backward"
+        with pa.weight_cast_cache():
+            a, b = step(), step()
+            assert n[0] == 2, "the cached pieces were made again"
+            with torch.no_grad():
+                mlp.router.weight.mul_(0.5)
+            c = step()
+            assert n[0] == 3, "the pieces of the changed weight were not remade"
+    finally:
+        M.ops.split_router_weight = real
+    for u, v, w_, z in zip(plain, first, a, b):
+        assert torch.equal(u, v) and torch.equal(u, w_) and torch.equal(u, z)
+    for u, v in zip(c, unsplit_step()):
+        assert torch.equal(u, v)
+
+
 def test_weight_cast_cache_reuses_copies_until_the_master_changes():
     """Inside pluggy_amd.weight_cast_cache the bf16 copies of fp32 masters are
     made once and reused (outputs and fp32 weight gradients bitwise equal to

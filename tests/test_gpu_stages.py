@@ -472,7 +472,11 @@ def _router_weight(W, x_dtype):
 @pytest.mark.parametrize("T,H,E,K,norm", [(2048, 512, 8, 2, True), (1000, 2048, 128, 8, True),
                                           (300, 256, 60, 4, False), (64, 2048, 128, 8, True),
                                           # the largest expert count and top-k the kernels take
-                                          (256, 256, 1024, 64, True), (130, 264, 200, 13, False)])
+                                          (256, 256, 1024, 64, True), (130, 264, 200, 13, False),
+                                          # the four-rows-per-wave kernel (E <= 256): scalar loads
+                                          # (E not a multiple of 4), two experts per lane, K > 16
+                                          (2500, 256, 125, 7, True), (70, 512, 30, 3, False),
+                                          (2100, 256, 256, 40, True)])
 def test_router_forward(x_dtype, T, H, E, K, norm):
     say(f"router T={T} H={H} E={E} K={K} norm={norm} {x_dtype}")
     ops = _ops()
@@ -555,6 +559,47 @@ def test_router_backward(norm, x_dtype, T, H, E, K):
             assert miss < bound, (name, miss)
     else:
         check_close("dW", gW, ref_gW, 1e-5, 5e-5)
+
+
+def test_router_weight_pieces():
+    """pmoe_router_split_weight writes [lo; hi; mid; hi] with hi = bf16(W),
+    mid = bf16(W - hi), lo = bf16(W - hi - mid) (both residuals exact in fp32)
+    and hi + mid + lo = W to 2^-24; the router forward and backward given
+    these pieces (PMOE_BF16X3) equal, bit for bit, the calls that split the
+    fp32 weight themselves, and the backward refuses pieces for E not a
+    multiple of 8."""
+    ops = _ops()
+    T, H, E, K = 3000, 512, 64, 6
+    say(f"router weight pieces T={T} H={H} E={E} K={K}")
+    g = gen(8)
+    W = torch.randn(E, H, generator=g) * 0.05
+    # zeros, a tiny value and values that need all three pieces
+    W[0, :5] = torch.tensor([0.0, -0.0, 1e-30, 1.0 + 2.0 ** -8 + 2.0 ** -16 + 2.0 ** -23, -(1.0 + 2.0 ** -23)])
+    Wd = W.to(DEV)
+    pieces = ops.split_router_weight(Wd)
+    assert pieces.shape == (4 * E, H) and pieces.dtype == torch.bfloat16
+    lo, hi, mid, hi2 = pieces.view(4, E, H).cpu()
+    assert torch.equal(hi, hi2) and torch.equal(hi, W.bfloat16())
+    r1 = W - hi.float()
+    assert torch.equal(mid, r1.bfloat16()) and torch.equal(lo, (r1 - mid.float()).bfloat16())
+    err = (hi.double() + mid.double() + lo.double() - W.double()).abs()
+    assert bool((err <= W.double().abs() * 2.0 ** -24).all())
+    assert float(mid[0, 3]) != 0.0 and float(lo[0, 3]) != 0.0  # the special value uses every piece
+    x = torch.randn(T, H, generator=g).bfloat16().to(DEV)
+    a = ops.router_forward(x, Wd, K, True)
+    b = ops.router_forward(x, Wd, K, True, pieces=pieces)
+    assert all(torch.equal(u, v) for u, v in zip(a, b))
+    logits, tw, ti, tw32 = a[:4]
+    gw = torch.randn(T, K, generator=g).bfloat16().to(DEV)
+    gl = (torch.randn(T, E, generator=g) * 0.1).to(DEV)
+    gx0, gW0 = ops.router_backward(x, Wd, logits, ti, tw32, gw, gl, True)
+    gx1, gW1 = ops.router_backward(x, Wd, logits, ti, tw32, gw, gl, True, pieces=pieces)
+    assert gW1.dtype == torch.float32 and torch.equal(gx0, gx1) and torch.equal(gW0, gW1)
+    W60 = Wd[:60].contiguous()
+    p60 = ops.split_router_weight(W60)
+    lg, _, ti60, tw60 = ops.router_forward(x, W60, K, True, pieces=p60)[:4]
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        ops.router_backward(x, W60, lg, ti60, tw60, gw, None, True, pieces=p60)
 
 
 # ------------------------------------------------- fused C entry points
