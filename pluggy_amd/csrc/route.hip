@@ -707,31 +707,50 @@ struct RowTables {
   int K = 1;
 };
 
-__device__ __forceinline__ void write_row_tables(const RowTables& rt, int pos, int q) {
+// The routing weight of pair q for the row tables (0 when none are written).
+__device__ __forceinline__ float row_weight(const RowTables& rt, int q) {
+  if (rt.sorted_w == nullptr) return 0.0f;
+  return rt.w_code == 1   ? bf16_to_f32(static_cast<const bf16_t*>(rt.w)[q])
+         : rt.w_code == 2 ? (float)static_cast<const f16_t*>(rt.w)[q]
+                          : static_cast<const float*>(rt.w)[q];
+}
+
+__device__ __forceinline__ void write_row_tables(const RowTables& rt, int pos, int q, float wq) {
   if (rt.sorted_token != nullptr) {
     rt.sorted_token[pos] = q / rt.K;
-    if (rt.sorted_w != nullptr)
-      rt.sorted_w[pos] = rt.w_code == 1   ? bf16_to_f32(static_cast<const bf16_t*>(rt.w)[q])
-                         : rt.w_code == 2 ? (float)static_cast<const f16_t*>(rt.w)[q]
-                                          : static_cast<const float*>(rt.w)[q];
+    if (rt.sorted_w != nullptr) rt.sorted_w[pos] = wq;
   }
 }
 
-// Stable scatter of pairs q0 .. q1-1 by one block of 256 threads: s_base[e]
-// holds the position of expert e's first pair of the range, s_wcnt ([4][E])
-// is zero. Within a round of 256 pairs, a pair's rank among the lower lanes
-// of its wave with the same expert comes from ballots over the expert's bits,
-// and the lower waves' counts of that expert are added from LDS.
+// Stable scatter of pairs q0 .. q1-1 by one block of NT threads: s_base[e]
+// holds the position of expert e's first pair of the range, s_wcnt ([NT/64][E])
+// is zero. Within a round of NT pairs, a pair's rank among the lower lanes of
+// its wave with the same expert comes from ballots over the expert's bits, and
+// the lower waves' counts of that expert are added from LDS. The ids (and
+// routing weights) of the next round are loaded while this one is ranked.
+template <int NT>
 __device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict__ idx, int q0, int q1, int E,
                                                       int nbits, int* s_base, int* s_wcnt,
                                                       int32_t* __restrict__ sorted_pair,
                                                       int32_t* __restrict__ inv_pos, const RowTables& rt) {
+  constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int qb = q0; qb < q1; qb += 256) {
+  int e_nx = 0;
+  float w_nx = 0.0f;
+  if (q0 + tid < q1) {
+    e_nx = clamp_expert(idx[q0 + tid], E);
+    w_nx = row_weight(rt, q0 + tid);
+  }
+  for (int qb = q0; qb < q1; qb += NT) {
     const int q = qb + tid;
     const bool valid = q < q1;
-    const int e = valid ? clamp_expert(idx[q], E) : 0;
+    const int e = e_nx;
+    const float wq = w_nx;
+    if (q + NT < q1) {
+      e_nx = clamp_expert(idx[q + NT], E);
+      w_nx = row_weight(rt, q + NT);
+    }
     uint64_t mask = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1;
@@ -746,31 +765,38 @@ __device__ __forceinline__ void permute_scatter_range(const int64_t* __restrict_
       for (int w = 0; w < wave; ++w) pos += s_wcnt[w * E + e];
       sorted_pair[pos] = q;
       inv_pos[q] = pos;
-      write_row_tables(rt, pos, q);
+      write_row_tables(rt, pos, q, wq);
     }
     __syncthreads();
-    for (int x = tid; x < E; x += 256) {
-      s_base[x] += s_wcnt[x] + s_wcnt[E + x] + s_wcnt[2 * E + x] + s_wcnt[3 * E + x];
-      s_wcnt[x] = s_wcnt[E + x] = s_wcnt[2 * E + x] = s_wcnt[3 * E + x] = 0;
+    for (int x = tid; x < E; x += NT) {
+      int add = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        add += s_wcnt[w * E + x];
+        s_wcnt[w * E + x] = 0;
+      }
+      s_base[x] += add;
     }
     __syncthreads();
   }
 }
 
-__global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
-                                                              int chunk, const int32_t* __restrict__ chunk_base,
-                                                              int32_t* __restrict__ sorted_pair,
-                                                              int32_t* __restrict__ inv_pos, RowTables rt) {
+template <int NT>
+__global__ __launch_bounds__(NT) void permute_scatter_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
+                                                             int chunk, const int32_t* __restrict__ chunk_base,
+                                                             int32_t* __restrict__ sorted_pair,
+                                                             int32_t* __restrict__ inv_pos, RowTables rt) {
+  constexpr int NW = NT / 64;
   extern __shared__ int sm[];
   int* s_base = sm;       // [E]
-  int* s_wcnt = sm + E;   // [4][E]
-  for (int e = threadIdx.x; e < E; e += 256) {
+  int* s_wcnt = sm + E;   // [NW][E]
+  for (int e = threadIdx.x; e < E; e += NT) {
     s_base[e] = chunk_base[(int64_t)blockIdx.x * E + e];
-    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
+    for (int w = 0; w < NW; ++w) s_wcnt[w * E + e] = 0;
   }
   __syncthreads();
   const int q0 = blockIdx.x * chunk;
-  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
+  permute_scatter_range<NT>(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
 }
 
 // The scatter for at most kFusedScanChunks chunks, with the scan folded in:
@@ -784,25 +810,28 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
 // separate scan kernel.
 constexpr int kFusedScanChunks = 64;
 constexpr int kFusedScanEntries = 8192;
-__global__ __launch_bounds__(256) void permute_scatter_scan_kernel(const int64_t* __restrict__ idx, int P, int E,
-                                                                   int nbits, int chunk, int nchunks,
-                                                                   const int32_t* __restrict__ chunk_hist,
-                                                                   int32_t* __restrict__ counts,
-                                                                   int32_t* __restrict__ offs,
-                                                                   int32_t* __restrict__ sorted_pair,
-                                                                   int32_t* __restrict__ inv_pos, RowTables rt) {
+template <int NT>
+__global__ __launch_bounds__(NT) void permute_scatter_scan_kernel(const int64_t* __restrict__ idx, int P, int E,
+                                                                  int nbits, int chunk, int nchunks,
+                                                                  const int32_t* __restrict__ chunk_hist,
+                                                                  int32_t* __restrict__ counts,
+                                                                  int32_t* __restrict__ offs,
+                                                                  int32_t* __restrict__ sorted_pair,
+                                                                  int32_t* __restrict__ inv_pos, RowTables rt) {
+  constexpr int NW = NT / 64;
+  constexpr int PER = (1024 + NT - 1) / NT;  // experts per thread at E = 1024
   extern __shared__ int sm[];
   int* s_base = sm;       // [E]
-  int* s_wcnt = sm + E;   // [4][E]
-  __shared__ int s_wsum[4];
+  int* s_wcnt = sm + E;   // [NW][E]
+  __shared__ int s_wsum[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x;
-  // thread t takes experts t*per .. t*per+per-1 (E <= 1024, per <= 4): their
-  // totals over all chunks and their sums over the chunks before c
-  const int per = (E + 255) / 256;
-  int tot[4], pre[4], sum = 0;
+  // thread t takes experts t*per .. t*per+per-1 (per <= PER): their totals
+  // over all chunks and their sums over the chunks before c
+  const int per = (E + NT - 1) / NT;
+  int tot[PER], pre[PER], sum = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid * per + j;
     tot[j] = pre[j] = 0;
     if (j < per && e < E) {
@@ -823,7 +852,7 @@ __global__ __launch_bounds__(256) void permute_scatter_scan_kernel(const int64_t
   int excl = inc - sum;
   for (int w = 0; w < wave; ++w) excl += s_wsum[w];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid * per + j;
     if (j < per && e < E) {
       if (c == 0) {
@@ -834,36 +863,39 @@ __global__ __launch_bounds__(256) void permute_scatter_scan_kernel(const int64_t
       excl += tot[j];
     }
   }
-  for (int e = tid; e < 4 * E; e += 256) s_wcnt[e] = 0;
+  for (int e = tid; e < NW * E; e += NT) s_wcnt[e] = 0;
   __syncthreads();
   const int q0 = c * chunk;
-  permute_scatter_range(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
+  permute_scatter_range<NT>(idx, q0, min(P, q0 + chunk), E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
 }
 
 // The whole permutation of at most one chunk of pairs (decode) in one block:
 // histogram, exclusive scan over the experts, stable scatter. Same result as
 // the three-kernel path, in one launch instead of three.
-__global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
-                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offs,
-                                                            int32_t* __restrict__ sorted_pair,
-                                                            int32_t* __restrict__ inv_pos, RowTables rt) {
+template <int NT>
+__global__ __launch_bounds__(NT) void permute_small_kernel(const int64_t* __restrict__ idx, int P, int E, int nbits,
+                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offs,
+                                                           int32_t* __restrict__ sorted_pair,
+                                                           int32_t* __restrict__ inv_pos, RowTables rt) {
+  constexpr int NW = NT / 64;
+  constexpr int PER = (1024 + NT - 1) / NT;
   extern __shared__ int sm[];
   int* s_base = sm;       // [E]: counts, then exclusive bases
-  int* s_wcnt = sm + E;   // [4][E]
-  __shared__ int s_wsum[4];
+  int* s_wcnt = sm + E;   // [NW][E]
+  __shared__ int s_wsum[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += 256) {
+  for (int e = tid; e < E; e += NT) {
     s_base[e] = 0;
-    for (int w = 0; w < 4; ++w) s_wcnt[w * E + e] = 0;
+    for (int w = 0; w < NW; ++w) s_wcnt[w * E + e] = 0;
   }
   __syncthreads();
-  for (int q = tid; q < P; q += 256) atomicAdd(&s_base[clamp_expert(idx[q], E)], 1);
+  for (int q = tid; q < P; q += NT) atomicAdd(&s_base[clamp_expert(idx[q], E)], 1);
   __syncthreads();
-  // thread t scans experts t*per .. t*per+per-1 (E <= 1024, per <= 4)
-  const int per = (E + 255) / 256;
-  int c[4], sum = 0;
+  // thread t scans experts t*per .. t*per+per-1 (per <= PER)
+  const int per = (E + NT - 1) / NT;
+  int c[PER], sum = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid * per + j;
     c[j] = (j < per && e < E) ? s_base[e] : 0;
     sum += c[j];
@@ -874,7 +906,7 @@ __global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __res
   int excl = inc - sum;
   for (int w = 0; w < wave; ++w) excl += s_wsum[w];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid * per + j;
     if (j < per && e < E) {
       counts[e] = c[j];
@@ -884,7 +916,7 @@ __global__ __launch_bounds__(256) void permute_small_kernel(const int64_t* __res
     }
   }
   __syncthreads();
-  permute_scatter_range(idx, 0, P, E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
+  permute_scatter_range<NT>(idx, 0, P, E, nbits, s_base, s_wcnt, sorted_pair, inv_pos, rt);
 }
 
 // ---- row movers: one wave per token, 16-byte lanes. KC > 0 is the top-k
@@ -1189,22 +1221,31 @@ hipError_t permute_pairs(const int64_t* top_idx, int T, int K, int E, int32_t* c
   rt.w = w;
   rt.w_code = w_code;
   rt.K = K;
-  if (nchunks <= 1) {
-    hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits, counts,
-                       offs, sorted_pair, inv_pos, rt);
+  // The scatter ranks a round of one pair per thread at a time: blocks of 1024
+  // threads (a 2048-pair chunk in 2 rounds) while their LDS counts, one row of E
+  // per wave, stay small; 256 threads for E > 256.
+  auto launch = [&](auto ntc) {
+    constexpr int NT = decltype(ntc)::value;
+    const size_t shm = (size_t)(1 + NT / 64) * E * sizeof(int);
+    if (nchunks <= 1) {
+      hipLaunchKernelGGL((permute_small_kernel<NT>), dim3(1), dim3(NT), shm, s, top_idx, P, E, nbits, counts, offs,
+                         sorted_pair, inv_pos, rt);
+      return hipGetLastError();
+    }
+    hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
+                       chunk_hist);
+    if (nchunks <= kFusedScanChunks && nchunks * E <= kFusedScanEntries) {
+      hipLaunchKernelGGL((permute_scatter_scan_kernel<NT>), dim3(nchunks), dim3(NT), shm, s, top_idx, P, E, nbits,
+                         chunk, nchunks, chunk_hist, counts, offs, sorted_pair, inv_pos, rt);
+      return hipGetLastError();
+    }
+    hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_hist, nchunks, E, counts, offs);
+    hipLaunchKernelGGL((permute_scatter_kernel<NT>), dim3(nchunks), dim3(NT), shm, s, top_idx, P, E, nbits, chunk,
+                       chunk_hist, sorted_pair, inv_pos, rt);
     return hipGetLastError();
-  }
-  hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(256), E * sizeof(int), s, top_idx, P, E, chunk,
-                     chunk_hist);
-  if (nchunks <= kFusedScanChunks && nchunks * E <= kFusedScanEntries) {
-    hipLaunchKernelGGL(permute_scatter_scan_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E,
-                       nbits, chunk, nchunks, chunk_hist, counts, offs, sorted_pair, inv_pos, rt);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_hist, nchunks, E, counts, offs);
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(256), 5 * E * sizeof(int), s, top_idx, P, E, nbits,
-                     chunk, chunk_hist, sorted_pair, inv_pos, rt);
-  return hipGetLastError();
+  };
+  if (E <= 256) return launch(std::integral_constant<int, 1024>());
+  return launch(std::integral_constant<int, 256>());
 }
 
 // Ids outside [0, E): one block of 1024 threads strides over all n ids and
