@@ -65,12 +65,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Load/store 8 consecutive elements of type T as fp32.
+// Load/store 8 consecutive elements of type T as fp32. load_nt: a
+// non-temporal load, for rows read once (gathered rows of the row movers).
 template <typename T> struct Vec8;
 
 template <> struct Vec8<bf16_t> {
   __device__ static __forceinline__ void load(const bf16_t* p, float* v) {
     u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = bf16lo(w[i]); v[2 * i + 1] = bf16hi(w[i]); }
+  }
+  __device__ static __forceinline__ void load_nt(const bf16_t* p, float* v) {
+    const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[2 * i] = bf16lo(w[i]); v[2 * i + 1] = bf16hi(w[i]); }
   }
@@ -86,6 +92,12 @@ template <> struct Vec8<float> {
   __device__ static __forceinline__ void load(const float* p, float* v) {
     f32x4 a = *reinterpret_cast<const f32x4*>(p);
     f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+  }
+  __device__ static __forceinline__ void load_nt(const float* p, float* v) {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
   }
@@ -117,6 +129,11 @@ __device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
 template <> struct Vec8<f16_t> {
   __device__ static __forceinline__ void load(const f16_t* p, float* v) {
     u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = f16lo(w[i]); v[2 * i + 1] = f16hi(w[i]); }
+  }
+  __device__ static __forceinline__ void load_nt(const f16_t* p, float* v) {
+    const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[2 * i] = f16lo(w[i]); v[2 * i + 1] = f16hi(w[i]); }
   }

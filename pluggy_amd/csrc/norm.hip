@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void dispatch_rmsnorm_bwd_kernel(
           if (c < H) {
             float v[KC][8];
 #pragma unroll
-            for (int k = 0; k < KC; ++k) Vec8<T>::load(gxp + row[k] + c, v[k]);
+            for (int k = 0; k < KC; ++k) Vec8<T>::load_nt(gxp + row[k] + c, v[k]);  // read once
 #pragma unroll
             for (int k = 0; k < KC; ++k)
 #pragma unroll
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void dispatch_rmsnorm_bwd_kernel(
             const int c = lane * 8 + 512 * i;
             if (c < H) {
               float v[8];
-              Vec8<T>::load(gxp + rk + c, v);
+              Vec8<T>::load_nt(gxp + rk + c, v);
 #pragma unroll
               for (int e = 0; e < 8; ++e) g[i][e] += v[e];
             }
