@@ -47,7 +47,9 @@ typedef DmaCfg<256, 256, 128, 64, 3, 32, 1> DmaRouterDx;
 // of four 32x32 wave tiles, 128-deep k stages (256-byte weight-row pieces, which
 // stream from HBM ≈15 % faster than the 64-byte pieces of 32-deep stages), a
 // three-stage ring (120 KiB). Used when the experts average at most 32 rows.
-typedef DmaCfg<32, 128, 32, 32, 3, 128, 1> DmaDecode;
+// Each weight block is read by one tile only, so the weights stream in with
+// non-temporal loads.
+typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, bf16_t, true> DmaDecode;
 constexpr int kDecodeRowsPerExpert = 32;
 
 // The same tile shapes for each 16-bit operand format (fp16 runs the same
@@ -55,7 +57,7 @@ constexpr int kDecodeRowsPerExpert = 32;
 template <typename T16> struct PersistCfgs {
   typedef DmaCfg<256, 256, 128, 64, 4, 32, 1, T16> Main;
   typedef DmaCfg<128, 256, 64, 64, 4, 32, 1, T16> Rows128;
-  typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, T16> Decode;
+  typedef DmaCfg<32, 128, 32, 32, 3, 128, 1, T16, true> Decode;
 };
 static_assert(std::is_same<PersistCfgs<bf16_t>::Main, DmaExpert>::value &&
                   std::is_same<PersistCfgs<bf16_t>::Rows128, DmaExpert128>::value &&

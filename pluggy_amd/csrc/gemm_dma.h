@@ -34,9 +34,12 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 // MINB: blocks per CU the register allocation must allow (launch bounds).
 // Tc: the 16-bit operand format (bf16_t or f16_t; the persistent engine
 // serves both, the kernel in this file bf16 only).
-template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1, typename Tc_ = bf16_t>
+// STREAM_B: B (k-contiguous) is loaded non-temporally (see dma16).
+template <int BM_, int BN_, int WM_, int WN_, int NS_, int BK_ = 64, int MINB_ = 1, typename Tc_ = bf16_t,
+          bool STREAM_B_ = false>
 struct DmaCfg {
   typedef Tc_ Tc;
+  static constexpr bool STREAM_B = STREAM_B_;
   static_assert(std::is_same<Tc_, bf16_t>::value || std::is_same<Tc_, f16_t>::value, "16-bit operand format");
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, BK = BK_, MINB = MINB_;
   static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
@@ -88,18 +91,32 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // lds + 16*l (lds is wave-uniform). Issued from inline asm so that the
 // compiler adds no waits of its own; every consumer waits explicitly with
 // wait_vmcnt<> and a barrier. m0 (the LDS destination) is saved and restored
-// inside the statement, so the compiler's view of m0 is untouched.
+// inside the statement, so the compiler's view of m0 is untouched. NTL: a
+// non-temporal (streaming) load, for data each tile reads once and no other
+// tile reuses (the weight stream of the decode tiles).
+template <bool NTL = false>
 __device__ __forceinline__ void dma16(const BufRsrc& rs, uint32_t lds, uint32_t voff) {
   int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(voff), "s"(rs)
-      : "memory");
+  if constexpr (NTL)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rs)
+        : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rs)
+        : "memory");
 }
 
 // Block barrier for the DMA pipeline: waits for this wave's LDS reads only
@@ -202,12 +219,12 @@ struct KcDma {
   // k0: first k of the stage relative to the descriptor; tail: the stage
   // reaches past k_hi (only then are lanes checked one by one).
   // instruction I of the stage at LDS byte address tile
-  template <int I>
+  template <int I, bool NTL = false>
   __device__ __forceinline__ void issue1(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, bool tail,
                                          int wave) const {
     uint32_t v = rowoff[I] + (uint32_t)(k0 * 2);
     if (tail && k0 + kc[I] >= k_hi) v = kOOB;
-    dma16(rs, tile + (wave + I * NW) * 1024, v);
+    dma16<NTL>(rs, tile + (wave + I * NW) * 1024, v);
   }
 };
 

@@ -768,7 +768,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       else T.la.template issue1<J>(T.rsA, st, k0, p.lda, wave);
     } else {
       constexpr int JB = J - Cfg::A_INSTR;
-      if constexpr (B_KC) T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
+      if constexpr (B_KC)
+        T.lb.template issue1<JB, Cfg::STREAM_B>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
       else if constexpr (GATH == GB_KROWS)
         T.lb.template issue1_rows<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, lane < 32 ? tok[JB][0] : tok[JB][1],
                                        p.ldb, wave);
