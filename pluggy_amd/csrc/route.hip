@@ -606,6 +606,30 @@ __global__ void reduce_partials_kernel(const float* __restrict__ partial, int sp
   }
 }
 
+// The same sums, four consecutive values per thread (n a multiple of 4): 16-byte
+// loads, four planes' loads issued before their adds; each value still sums
+// the planes in order, so the result is the scalar kernel's bit for bit.
+template <typename TO>
+__global__ void reduce_partials4_kernel(const float* __restrict__ partial, int splits, int64_t n,
+                                        TO* __restrict__ out) {
+  const int64_t n4 = n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(partial) + i;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    int g = 0;
+    for (; g + 4 <= splits; g += 4) {
+      f32x4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = src[(int64_t)(g + j) * n4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc += v[j];
+    }
+    for (; g < splits; ++g) acc += src[(int64_t)g * n4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_scalar<TO>(out + 4 * i + j, acc[j]);
+  }
+}
+
 // ---- permutation: stable counting sort of the P = T*K pairs by expert id
 
 __device__ __forceinline__ int clamp_expert(int64_t e, int E) {
@@ -1204,6 +1228,11 @@ hipError_t router_dlogits(const float* logits, const int64_t* top_idx, const flo
 template <typename TO>
 hipError_t reduce_partials(const float* partial, int splits, int64_t n, TO* out, hipStream_t s) {
   if (n == 0) return hipSuccess;
+  if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(partial) & 15) == 0) {
+    const unsigned grid4 = (unsigned)std::min<int64_t>((n / 4 + 255) / 256, 4096);
+    hipLaunchKernelGGL((reduce_partials4_kernel<TO>), dim3(grid4), dim3(256), 0, s, partial, splits, n, out);
+    return hipGetLastError();
+  }
   const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
   hipLaunchKernelGGL((reduce_partials_kernel<TO>), dim3(grid), dim3(256), 0, s, partial, splits, n, out);
   return hipGetLastError();
