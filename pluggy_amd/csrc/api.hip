@@ -289,7 +289,7 @@ PMOE_API int pmoe_router_backward(const void* x, int x_dtype, const void* weight
     return PMOE_OK;
   }
   if (x_dtype == PMOE_BF16) {
-    // bf16 x: dl is split into bf16 planes hi + lo; dx = [hi|lo|hi].[W_hi;W_hi;W_lo]
+    // bf16 x: dl is split into bf16 planes hi + lo; dx = [hi|hi|lo].[W_hi;W_mid;W_hi]
     // and dW = hi^T x + lo^T x, all products exact, fp32 accumulation.
     bf16_t* dl3 = cv.take<bf16_t>((size_t)T * 3 * ldl);
     bf16_t* w3t = cv.take<bf16_t>((size_t)3 * ldl * H);
