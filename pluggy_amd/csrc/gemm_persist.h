@@ -24,9 +24,6 @@
 
 namespace pmoe {
 
-constexpr bool kNtAllEpilogues = false;
-constexpr bool kFastStoreEpilogue = true;
-
 template <class Cfg>
 struct PersistLayout {
   static constexpr int EPI_LD = Cfg::WN + 4;  // floats per staged fp32 row
@@ -88,7 +85,7 @@ __device__ __forceinline__ void st_out8(float* p, const float* v) {
 // 64 GB/s per CU without stores, 29 with cached stores, 50 with
 // non-temporal ones).
 template <int GM>
-constexpr bool nt_epilogue() { return GM == GM_RED || kNtAllEpilogues; }
+constexpr bool nt_epilogue() { return GM == GM_RED; }
 
 // Epilogue of a plain-store tile (EPI_STORE) whose columns all lie inside N,
 // the common case. Each 8-row slab of a wave's 32-row block goes through the
@@ -248,14 +245,14 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   static_assert(!PACK || (sizeof(Tout) == 2 && EPI != EPI_SWIGLU_BWD), "packed staging of bf16 outputs");
   static_assert(EPI == EPI_STORE || sizeof(Tout) == 2, "fused epilogues write bf16");
   constexpr bool NT = nt_epilogue<GM>();
-  if constexpr (EPI == EPI_SWIGLU_BWD && GM == GM_ROWS && Cfg::WN == 64 && kFastStoreEpilogue) {
+  if constexpr (EPI == EPI_SWIGLU_BWD && GM == GM_ROWS && Cfg::WN == 64) {
     if (ti.n0 + Cfg::BN <= p.N && (int64_t)Cfg::WM * p.ldaux * 2 < ((int64_t)1 << 31) &&
         (int64_t)Cfg::WM * p.ldc * 2 < ((int64_t)1 << 31)) {
       store_tile_swiglu_bwd<Cfg, NT>(acc, stage, ti, p, wm, wn, lane);
       return;
     }
   }
-  if constexpr (EPI == EPI_STORE && Cfg::WN == 64 && kFastStoreEpilogue) {
+  if constexpr (EPI == EPI_STORE && Cfg::WN == 64) {
     if (ti.n0 + Cfg::BN <= p.N && (int64_t)Cfg::WM * p.ldc * (int64_t)sizeof(Tout) < ((int64_t)1 << 31)) {
       store_tile_full_cols<Cfg, Tout, GM, NT>(acc, stage, ti, p, wm, wn, lane);
       return;
