@@ -463,6 +463,81 @@ __device__ __forceinline__ int red_cost_tile(const int* s_cost, int groups, int 
   return lo * tpg + (int)min<int64_t>(k, tpg);
 }
 
+// Dealing of GM_RED tiles under skewed routing. The tiles are taken in order
+// of descending cost (s_order: groups sorted by the cost of one tile, each
+// group's tpg tiles consecutive) and dealt in rounds: round 0 gives tile p to
+// the block at position p; in each later round only the blocks whose load is
+// still below the mean share take part (all of them when none is), in
+// ascending position order on even rounds and descending order on odd ones,
+// each taking the next tile. Against the plain snake (every block in every
+// round) this keeps a block that drew a heavy tile from also drawing its share
+// of the small ones: on config 4's routing a simulation of the two deals puts
+// the heaviest block at 1.05x (down wgrad) and 1.01x (gate_up wgrad) the mean
+// share, against 1.37x and 1.06x. Every block runs the same integer simulation
+// (thread p simulates position p; a round is one ballot and one barrier) and
+// keeps the list indices of its own tiles. The costs are staged in `scratch`
+// (the ring's LDS, unused until the first DMA); s_cost (the inclusive scan of
+// red_cost_scan) is overwritten by this block's list, ended by -1 when it is
+// shorter than kMaxDealt. Returns whether the deal fits (at most kMaxDealt
+// tiles for every block, at most kMaxRounds rounds, no more blocks than
+// threads; the same outcome in every block): otherwise the caller falls back
+// to the snake, in every block alike.
+constexpr int kMaxDealt = 1024;
+constexpr int kMaxRounds = 4096;
+template <int NT>
+__device__ __forceinline__ bool deal_below_mean(const unsigned short* s_order, int* s_cost, int groups, int tpg,
+                                            int total, int64_t c_all, int nb, int spos, char* scratch,
+                                            int* s_result) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (nb > NT) return false;  // uniform: the grid is the same for every block
+  int* c_sorted = reinterpret_cast<int*>(scratch);                 // [groups]
+  uint64_t* s_mask = reinterpret_cast<uint64_t*>(scratch + 4096);  // [2][NW]
+  for (int r = tid; r < groups; r += NT) {
+    const int g = s_order[r];
+    c_sorted[r] = s_cost[g + 1] - s_cost[g];
+  }
+  if (tid == 0) s_result[1] = 0;
+  __syncthreads();  // the costs are staged; s_cost is free for the list
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int64_t load = 0;
+  int cnt = 0, j0 = 0, round = 0;
+  while (j0 < total && round < kMaxRounds) {
+    bool act = tid < nb && (round == 0 || load * nb < c_all);
+    const uint64_t m = __ballot(act);
+    if (lane == 0) s_mask[(round & 1) * NW + wave] = m;
+    __syncthreads();
+    int a = 0, below = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int c = __popcll(s_mask[(round & 1) * NW + w]);
+      a += c;
+      below += w < wave ? c : 0;
+    }
+    below += __popcll(m & lt_mask);
+    if (a == 0) {  // every block has reached the mean: all take part
+      act = tid < nb;
+      a = nb;
+      below = tid;
+    }
+    if (act) {
+      const int j = j0 + ((round & 1) ? a - 1 - below : below);
+      if (j < total) {
+        load += c_sorted[j / tpg];
+        if (tid == spos && cnt < kMaxDealt) s_cost[cnt] = j;
+        ++cnt;
+      }
+    }
+    j0 += a;
+    ++round;
+  }
+  // end this block's list; flag any block whose list does not fit (uniform outcome)
+  if (tid == spos && cnt < kMaxDealt) s_cost[cnt] = -1;
+  if (cnt > kMaxDealt) atomicOr(&s_result[1], 1);
+  __syncthreads();
+  return s_result[1] == 0 && j0 >= total;
+}
+
 // The block's tiles form one continuous stream of k-stages: stage g lives in
 // ring slot g % NS, and the DMAs issued during stage g fetch stream stage
 // g + NS - 1, which in a tile's last NS - 1 stages is one of the next tile's
@@ -521,6 +596,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   __shared__ int s_offs[1024];
   __shared__ unsigned short s_order[1024];  // GM_RED under skew: groups by tile cost, descending
   __shared__ int s_cmax;
+  __shared__ int s_deal[2];                  // GM_RED under skew: the deal's overflow flag
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -543,9 +619,11 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // Under skewed routing (GM_RED, one tile costing more than half a block's
   // mean share) the shares cannot balance: a heavy group's tiles crowd one
   // XCD's blocks. Then the tiles are taken in order of descending cost and
-  // dealt to the blocks in a snake (round k gives tile k*NB + p to the block
-  // at position p, or k*NB + NB-1-p for odd k), positions XCD-major so that a
-  // group's tiles still run side by side on one XCD.
+  // dealt in rounds to the blocks still below the mean share
+  // (deal_below_mean), positions XCD-major so that a group's tiles still run
+  // side by side on one XCD; when that deal does not fit its bounds, in a
+  // snake (round k gives tile k*NB + p to the block at position p, or
+  // k*NB + NB-1-p for odd k).
   const int xcd = blockIdx.x & 7;
   const int nb = ((int)gridDim.x - xcd + 7) >> 3;  // blocks on this XCD
   const int bi = blockIdx.x >> 3;                  // this block's position on its XCD
@@ -573,6 +651,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       __syncthreads();
       for (int x = 0; x < xcd; ++x) spos += ((int)gridDim.x - x + 7) >> 3;
       spos += bi;
+      // spos < 0 from here on: this block's tiles are the list in s_scan
+      if (deal_below_mean<Cfg::NT>(s_order, s_scan, groups, tpg, total, c_all, (int)gridDim.x, spos, smem, s_deal))
+        spos = -1;
     } else {
       const int b0 = red_cost_tile(s_scan, groups, tpg, c_all * xcd / 8);
       const int b1 = xcd == 7 ? total : red_cost_tile(s_scan, groups, tpg, c_all * (xcd + 1) / 8);
@@ -587,6 +668,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // The k-th tile of this block (k = 0, 1, ...) as a list index, or -1 past its last.
   auto tile_at = [&](int k) -> int {
     if (skew) {
+      if (spos < 0) {
+        const int j = k < kMaxDealt ? s_scan[k] : -1;  // this block's k-th tile in the cost order
+        return j < 0 ? -1 : s_order[j / tpg] * tpg + j % tpg;
+      }
       const int NB = (int)gridDim.x;
       const int j = k * NB + ((k & 1) ? NB - 1 - spos : spos);
       return j < total ? s_order[j / tpg] * tpg + j % tpg : -1;
