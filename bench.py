@@ -407,8 +407,9 @@ def vendor_gemm_leg(dev, launches: int = 20, warmup: int = 5):
     where the grouped product is a plain batched one. Ours: gate_up with the
     SwiGLU epilogue (it also writes the activation) and down, on the sorted rows;
     the library's: torch.bmm (hipBLASLt) on the same operands, the weights
-    pre-transposed to contiguous (E, K, N) copies. Back-to-back launches timed
-    with HIP events."""
+    pre-transposed to contiguous (E, K, N) copies. The two alternate launch by
+    launch, each timed with its own pair of HIP events, so that both see the
+    same clock as the chip warms; the medians are reported."""
     import torch
 
     from pluggy_amd import ops
@@ -422,25 +423,32 @@ def vendor_gemm_leg(dev, launches: int = 20, warmup: int = 5):
     wgu_t, wdn_t = wgu.transpose(1, 2).contiguous(), wdn.transpose(1, 2).contiguous()
     _, mid = ops.gate_up_swiglu(xp, wgu, offs)
 
-    def timed(fn):
+    def timed_pair(fa, fb):
+        """Median ms of fa and of fb, launched alternately."""
         for _ in range(warmup):
-            fn()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            fa()
+            fb()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * launches)]
         torch.cuda.synchronize()
-        start.record()
-        for _ in range(launches):
-            fn()
-        end.record()
+        for i in range(launches):
+            ev[3 * i].record()
+            fa()
+            ev[3 * i + 1].record()
+            fb()
+            ev[3 * i + 2].record()
         torch.cuda.synchronize()
-        return start.elapsed_time(end) / launches
+        ta = sorted(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(launches))
+        tb = sorted(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(launches))
+        return ta[launches // 2], tb[launches // 2]
 
     xp3, mid3 = xp.view(E, R, H), mid.view(E, R, I)
-    out = {"problem": f"{E} experts x {R} rows, H={H}, I={I}, bf16", "launches": launches}
+    out = {"problem": f"{E} experts x {R} rows, H={H}, I={I}, bf16", "launches": launches,
+           "timing": "alternating launches, median of each"}
     for name, ours, lib, flop in (
             ("gate_up", lambda: ops.gate_up_swiglu(xp, wgu, offs), lambda: torch.bmm(xp3, wgu_t),
              2.0 * E * R * H * 2 * I),
             ("down", lambda: ops.down_proj(mid, wdn, offs), lambda: torch.bmm(mid3, wdn_t), 2.0 * E * R * I * H)):
-        t_ours, t_lib = timed(ours), timed(lib)
+        t_ours, t_lib = timed_pair(ours, lib)
         out[name] = {"ours_us": round(t_ours * 1e3, 1), "ours_TFLOP/s": round(flop / (t_ours * 1e-3) / 1e12, 1),
                      "hipblaslt_bmm_us": round(t_lib * 1e3, 1),
                      "hipblaslt_TFLOP/s": round(flop / (t_lib * 1e-3) / 1e12, 1),
