@@ -90,32 +90,26 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // One wave-wide 16-byte-per-lane DMA: lane l's chunk goes to LDS byte address
 // lds + 16*l (lds is wave-uniform). Issued from inline asm so that the
 // compiler adds no waits of its own; every consumer waits explicitly with
-// wait_vmcnt<> and a barrier. m0 (the LDS destination) is saved and restored
-// inside the statement, so the compiler's view of m0 is untouched. NTL: a
-// non-temporal (streaming) load, for data each tile reads once and no other
-// tile reuses (the weight stream of the decode tiles).
+// wait_vmcnt<> and a barrier. m0 (the LDS destination) is an input operand
+// of the statement, so the compiler sets it (often computing the address
+// straight into m0) and knows what it holds. NTL: a non-temporal (streaming)
+// load, for data each tile reads once and no other tile reuses (the weight
+// stream of the decode tiles).
 template <bool NTL = false>
 __device__ __forceinline__ void dma16(const BufRsrc& rs, uint32_t lds, uint32_t voff) {
-  int saved;
   if constexpr (NTL)
     asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(rs)
+        "buffer_load_dwordx4 %0, %1, 0 offen nt lds"
+        :
+        : "v"(voff), "s"(rs), "{m0}"(lds)
         : "memory");
   else
     asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(rs)
+        "buffer_load_dwordx4 %0, %1, 0 offen lds"
+        :
+        : "v"(voff), "s"(rs), "{m0}"(lds)
         : "memory");
 }
 
@@ -267,12 +261,16 @@ struct TDma {
   __device__ __forceinline__ void issue1(const BufRsrc& rs, uint32_t tile, int k0, int64_t ld, int wave) const {
     dma16(rs, tile + (wave + I * NW) * 1024, (uint32_t)((int64_t)(k0 + kk[I]) * ld * 2) + coloff[I]);
   }
-  // k-row gather: this lane's k-row of instruction I is storage row tok (the
-  // caller's token of that k-row); k-rows at or past k_hi read zero.
+  // k-row gather: the k-row of instruction I is storage row tok0 for lanes
+  // 0-31 and tok1 for lanes 32-63 (the caller's wave-uniform tokens of its two
+  // k-rows); k-rows at or past k_hi read zero. ld2: bytes per storage row. The
+  // offset is a 32-bit buffer offset, so the row's byte offset is formed in 32
+  // bits (the same value the instruction takes from 64-bit arithmetic).
   template <int I>
-  __device__ __forceinline__ void issue1_rows(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, int tok,
-                                              int64_t ld, int wave) const {
-    const uint32_t v = k0 + kk[I] < k_hi ? (uint32_t)((int64_t)tok * ld * 2) + coloff[I] : kOOB;
+  __device__ __forceinline__ void issue1_rows(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, int tok0,
+                                              int tok1, uint32_t ld2, int wave, int lane) const {
+    const uint32_t r0 = (uint32_t)tok0 * ld2, r1 = (uint32_t)tok1 * ld2;
+    const uint32_t v = k0 + kk[I] < k_hi ? (lane < 32 ? r0 : r1) + coloff[I] : kOOB;
     dma16(rs, tile + (wave + I * NW) * 1024, v);
   }
 };

@@ -690,6 +690,11 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even number of substeps");
   constexpr bool kInterleaveFrags = true;
+  // A tile's stages run as two loops (DMAs into this tile, then into the
+  // next) in the input-gradient GEMMs ([k][n] weights): gate_up dgrad -2.5 %
+  // measured; the forward GEMMs and the weight gradients measured 1-3 % slower
+  // that way and select the DMA source stage by stage.
+  constexpr bool kSplitStages = GM == GM_ROWS && !B_KC;
   // DMAs of stage g + NS - 1 ride on the MFMAs of the first SPREAD substeps
   // of stage g. Spread over all KS substeps, the last of which runs after the
   // stage's barrier: the gate_up forward (measured: -3 % on three slots, and
@@ -820,23 +825,26 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
   // covers two k-rows, tok[i][0] for lanes 0-31 and tok[i][1] for 32-63. They
   // are read through the scalar cache and stay wave-uniform (the per-lane
   // pick happens at the DMA), so a read issued a stage ahead is not waited
-  // for until that stage.
+  // for until that stage. Index arithmetic in 32 unsigned bits: the table
+  // holds at most 2^31 - 1 entries and q stays a few stages past its end.
   auto tokens = [&](const LoadTile& T, int ls, int (&tok)[GI][2]) {
     if constexpr (KGATH) {
       typedef const __attribute__((address_space(4))) int32_t cint;
       cint* ci = (cint*)gidx;
-      const int64_t last = p.n_index - 1;
+      const uint32_t last = (uint32_t)(p.n_index - 1);
+      const uint32_t q0 = (uint32_t)T.klo + (uint32_t)(ls * BK) + (uint32_t)(wave * 2);
 #pragma unroll
       for (int i = 0; i < GI; ++i) {
-        const int64_t q = (int64_t)T.klo + ls * BK + (wave + i * NW) * 2;
-        tok[i][0] = ci[min<int64_t>(q, last)];
-        tok[i][1] = ci[min<int64_t>(q + 1, last)];
+        const uint32_t q = q0 + (uint32_t)(i * NW * 2);
+        tok[i][0] = ci[min(q, last)];
+        tok[i][1] = ci[min(q + 1u, last)];
       }
     }
   };
+  const uint32_t lda2 = (uint32_t)(p.lda * 2), ldb2 = (uint32_t)(p.ldb * 2);  // gathered rows' bytes
 
   int gs = 0;  // stream stage of the current tile's stage 0
-  auto slot_of = [&](int g) { return (uint32_t)((g % NS) * SLOT); };
+  auto slot_of = [&](int g) { return ((uint32_t)g % NS) * SLOT; };  // g >= 0
   // DMA J of stage ls of tile T, into the ring slot of stream stage g; tok:
   // the gathered k-rows' tokens of that stage.
   auto dma_one = [&](const LoadTile& T, int ls, int g, const int (&tok)[GI][2], auto jc) {
@@ -846,15 +854,15 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     if constexpr (J < Cfg::A_INSTR) {
       if constexpr (A_KC) T.la.template issue1<J>(T.rsA, st, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
       else if constexpr (GATH == GA_KROWS)
-        T.la.template issue1_rows<J>(T.rsA, st, k0, T.kd_hi, lane < 32 ? tok[J][0] : tok[J][1], p.lda, wave);
+        T.la.template issue1_rows<J>(T.rsA, st, k0, T.kd_hi, tok[J][0], tok[J][1], lda2, wave, lane);
       else T.la.template issue1<J>(T.rsA, st, k0, p.lda, wave);
     } else {
       constexpr int JB = J - Cfg::A_INSTR;
       if constexpr (B_KC)
         T.lb.template issue1<JB, Cfg::STREAM_B>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, k0 + BK > T.kd_hi, wave);
       else if constexpr (GATH == GB_KROWS)
-        T.lb.template issue1_rows<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, lane < 32 ? tok[JB][0] : tok[JB][1],
-                                       p.ldb, wave);
+        T.lb.template issue1_rows<JB>(T.rsB, st + Cfg::A_BYTES, k0, T.kd_hi, tok[JB][0], tok[JB][1], ldb2, wave,
+                                       lane);
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
@@ -939,23 +947,12 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
     const int nk = cur.nk;
     // tokens of stage 0's DMAs (stream stage gs + NS - 1: this tile's stage NS - 1, or the next tile's)
     if constexpr (KGATH) tokens(NS - 1 >= nk ? nxt : cur, NS - 1 >= nk ? NS - 1 - nk : NS - 1, tok);
-    for (int kt = 0; kt < nk; ++kt) {
+    // One stage; its DMAs fetch stream stage g + NS - 1 (stage ls of tile T),
+    // which lies in the next tile in a tile's last NS - 1 stages.
+    auto run_stage = [&](int kt, const LoadTile& T, int ls) {
       const int g = gs + kt;
       const char* sa = smem + slot_of(g);
-      // the DMAs of this stage: stream stage g + NS - 1
       const int s = kt + NS - 1;
-      const bool in_next = s >= nk;
-      LoadTile T;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {  // uniform: the descriptors stay in SGPRs
-        T.rsA[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsA[w] : cur.rsA[w]);
-        T.rsB[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsB[w] : cur.rsB[w]);
-      }
-      T.la.select(in_next, nxt.la, cur.la);
-      T.lb.select(in_next, nxt.lb, cur.lb);
-      T.kd0 = in_next ? nxt.kd0 : cur.kd0;
-      T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
-      const int ls = in_next ? s - nk : s;
       if constexpr (KGATH) {
         // The token reads of the k-row gathers are scalar loads, which return
         // out of order: while one is outstanding the compiler can only wait
@@ -998,6 +995,30 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
           tok[i][0] = tok_next[i][0];
           tok[i][1] = tok_next[i][1];
         }
+      }
+    };
+    if constexpr (kSplitStages) {
+      // two loops, so that neither selects between the tiles' descriptors
+      // and DMA offsets stage by stage
+      const int kt_next = nk - (NS - 1);  // >= 0: nk >= NS - 1
+#pragma unroll 1
+      for (int kt = 0; kt < kt_next; ++kt) run_stage(kt, cur, kt + NS - 1);
+#pragma unroll 1
+      for (int kt = kt_next; kt < nk; ++kt) run_stage(kt, nxt, kt + NS - 1 - nk);
+    } else {
+      for (int kt = 0; kt < nk; ++kt) {
+        const bool in_next = kt + NS - 1 >= nk;
+        LoadTile T;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {  // uniform: the descriptors stay in SGPRs
+          T.rsA[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsA[w] : cur.rsA[w]);
+          T.rsB[w] = __builtin_amdgcn_readfirstlane(in_next ? nxt.rsB[w] : cur.rsB[w]);
+        }
+        T.la.select(in_next, nxt.la, cur.la);
+        T.lb.select(in_next, nxt.lb, cur.lb);
+        T.kd0 = in_next ? nxt.kd0 : cur.kd0;
+        T.kd_hi = in_next ? nxt.kd_hi : cur.kd_hi;
+        run_stage(kt, T, in_next ? kt + NS - 1 - nk : kt + NS - 1);
       }
     }
     // The next tile's first NS - 1 stages were issued during this tile's last
