@@ -294,6 +294,26 @@ __device__ __forceinline__ bf16x8 t_frag(const char* tile, int r_base, int kbase
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// The same fragment from a lane offset computed once: the swizzle depends on
+// k only through k & 3, which a k base of 16 ks and the +4 of the second read
+// leave unchanged, so the fragment at k base 16 ks lies at the lane's offset
+// for k base 0 (t_lane_off) plus 16 ks k-rows, a constant the reads take as
+// their immediate offset.
+template <int R>
+__device__ __forceinline__ uint32_t t_lane_off(int r_base, int lane) {
+  const int g = lane >> 4, q = lane & 15;
+  return t_addr<R>(8 * (g >> 1) + (q >> 2), r_base + 16 * (g & 1) + 4 * (q & 3));
+}
+template <int R>
+__device__ __forceinline__ bf16x8 t_frag_at(const char* tile, uint32_t lane_off, int ks) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const char* p = tile + lane_off + ks * 16 * R * 2;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * R * 2));
+  const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 // 8 consecutive outputs from fp32: bf16 through the native converter, or fp32.
 template <typename Tout> struct Out8;
 template <> struct Out8<bf16_t> {

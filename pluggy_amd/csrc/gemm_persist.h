@@ -866,18 +866,26 @@ __global__ __launch_bounds__(Cfg::NT, 1) void grouped_gemm_persist_kernel(GemmPa
       else T.lb.template issue1<JB>(T.rsB, st + Cfg::A_BYTES, k0, p.ldb, wave);
     }
   };
+  // Lane offsets of the [k][r] operands' fragments within a slot, computed
+  // once (t_lane_off): a fragment read is then the slot base plus one of
+  // these plus an immediate.
+  uint32_t toff_a[MI], toff_b[NI];
+#pragma unroll
+  for (int f = 0; f < MI; ++f) toff_a[f] = A_KC ? 0u : t_lane_off<BM>(a_row0 + f * 32, lane);
+#pragma unroll
+  for (int j = 0; j < NI; ++j) toff_b[j] = B_KC ? 0u : t_lane_off<BN>(b_row0 + j * 32, lane);
   // Fragment F of substep ks from the slot at sa: F < MI the A rows of block
   // F, then the B rows of block F - MI.
   auto load_frag = [&](const char* sa, int ks, auto fc, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
     constexpr int F = decltype(fc)::value;
     if constexpr (F < MI) {
       if constexpr (A_KC) af[F] = kc_frag<BK>(sa, a_row0 + F * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else af[F] = t_frag<BM>(sa, a_row0 + F * 32, ks * 16, lane);
+      else af[F] = t_frag_at<BM>(sa, toff_a[F], ks);
     } else {
       const char* sb = sa + Cfg::A_BYTES;
       constexpr int J = F - MI;
       if constexpr (B_KC) bfr[J] = kc_frag<BK>(sb, b_row0 + J * 32 + (lane & 31), ks * 2 + (lane >> 5));
-      else bfr[J] = t_frag<BN>(sb, b_row0 + J * 32, ks * 16, lane);
+      else bfr[J] = t_frag_at<BN>(sb, toff_b[J], ks);
     }
   };
   auto load_frags = [&](const char* sa, int ks, bf16x8 (&af)[MI], bf16x8 (&bfr)[NI]) {
