@@ -262,6 +262,22 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
   const int half = lane >> 5, col_l = lane & 31;
   uint32_t* st32 = reinterpret_cast<uint32_t*>(stage);
+  // SwiGLU forward: the routing weights of every row this lane writes, loaded
+  // before the first slab rather than one global load (and its latency) per slab
+  constexpr int SW_CPR = WN / 2 / 8, SW_NE = (SLAB * SW_CPR + 63) / 64;
+  float wsp[MI][NSL][SW_NE];
+  if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int hs = 0; hs < NSL; ++hs)
+#pragma unroll
+        for (int ei = 0; ei < SW_NE; ++ei) {
+          const int e = lane + 64 * ei;
+          const int row = ti.m0 + wm * Cfg::WM + i * 32 + SLAB * hs + e / SW_CPR;
+          wsp[i][hs][ei] = (p.row_w != nullptr && e < SLAB * SW_CPR && row < ti.m_end) ? p.row_w[row] : 1.0f;
+        }
+  }
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
 #pragma unroll
@@ -297,7 +313,9 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
         constexpr int H2 = WN / 2, CPR = H2 / 8;
         Tout* MID = reinterpret_cast<Tout*>(p.C2);
 #pragma unroll
-        for (int e = lane; e < SLAB * CPR; e += 64) {
+        for (int ei = 0; ei < SW_NE; ++ei) {
+          const int e = lane + 64 * ei;
+          if (e >= SLAB * CPR) break;
           const int r = e / CPR, c = (e % CPR) * 8;
           const int row = row_base + r, col = ti.n0 + wn * H2 + c;
           if (row < ti.m_end && col < p.inter) {
@@ -309,7 +327,7 @@ __device__ __forceinline__ void store_slabs(const f32x16 (&acc)[Cfg::MI][Cfg::NI
             st16<NT>(C + (int64_t)row * p.ldc + p.inter + col, uw);
             unpack8<Tout>(gw, g);  // the activation uses the stored (rounded) pre-activations
             unpack8<Tout>(uw, u);
-            const float ws = p.row_w != nullptr ? p.row_w[row] : 1.0f;  // the routing weight
+            const float ws = wsp[i][hs][ei];  // the routing weight
 #pragma unroll
             for (int t = 0; t < 8; ++t) m[t] = g[t] * fast_sigmoid(g[t]) * u[t] * ws;
             st_out8<NT>(MID + (int64_t)row * p.ldc2 + col, m);
