@@ -98,13 +98,30 @@ constexpr bool nt_epilogue() { return GM == GM_RED; }
 // LDS operations run in order, so each slab's reads follow its writes, and the
 // next slab's writes follow those reads, without a wait between them.
 // Per lane per slab: 4 write2, 2 ds_read_b128, 4 conversions, 1-2 stores.
+// 8-row fp32 staging of one MFMA row group in 64-float rows: lanes 0-31 write
+// a row and lanes 32-63 the row four below, then 8 lanes read each row as two
+// 16-byte halves. Columns are XORed with 4 on odd rows and with 32 on rows 4-7,
+// so both the writes and the 16-lane groups of the reads hit distinct banks
+// (a padded row of 68 floats left the writes 2-way conflicted).
+__device__ __forceinline__ int stage_swz(int row) { return ((row & 1) << 2) | ((row & 4) << 3); }
+__device__ __forceinline__ void stage_put(float* stage, int row, int col, float v) {
+  stage[row * 64 + (col ^ stage_swz(row))] = v;
+}
+__device__ __forceinline__ void stage_get8(const float* stage, int row, int c, float (&v)[8]) {
+  const int sw = stage_swz(row);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(stage + row * 64 + (c ^ sw));
+  const f32x4 b = *reinterpret_cast<const f32x4*>(stage + row * 64 + ((c + 4) ^ sw));
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+}
+
 template <class Cfg, typename Tout, int GM, bool NT>
 __device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI][Cfg::NI], float* stage,
                                                      const TileInfo& ti, const GemmParams& p, int wm, int wn,
                                                      int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI, WM = Cfg::WM, WN = Cfg::WN;
-  constexpr int LD = PersistLayout<Cfg>::EPI_LD;  // floats per staged row
-  constexpr int CPR = WN / 8;                     // 8-output chunks per row
+  constexpr int CPR = WN / 8;  // 8-output chunks per row
+  static_assert(PersistLayout<Cfg>::EPI_LD >= 64, "the staged rows hold 64 floats");
   static_assert(8 * CPR == kWave, "one chunk per lane per 8-row slab (64-column wave tiles)");
   Tout* C = reinterpret_cast<Tout*>(p.C);
   if constexpr (GM == GM_RED) C += (int64_t)ti.group * p.strideC;
@@ -126,9 +143,9 @@ __device__ __forceinline__ void store_tile_full_cols(const f32x16 (&acc)[Cfg::MI
 #pragma unroll
       for (int j = 0; j < NI; ++j)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) stage[(4 * half + rr) * LD + j * 32 + col_l] = acc[i][j][4 * q + rr];
+        for (int rr = 0; rr < 4; ++rr) stage_put(stage, 4 * half + rr, j * 32 + col_l, acc[i][j][4 * q + rr]);
       float v[8];
-      Vec8<float>::load(stage + r * LD + c, v);
+      stage_get8(stage, r, c, v);
       const int off = (i * 32 + 8 * q + r) * ld_bytes + c * (int)sizeof(Tout);
       if constexpr (sizeof(Tout) == 2) {
         __builtin_amdgcn_raw_buffer_store_b128(Out8<Tout>::pack(v), rs, off, 0, AUX);
@@ -160,7 +177,6 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
                                                       const TileInfo& ti, const GemmParams& p, int wm, int wn,
                                                       int lane) {
   constexpr int MI = Cfg::MI, NI = Cfg::NI, WM = Cfg::WM, WN = Cfg::WN;
-  constexpr int LD = PersistLayout<Cfg>::EPI_LD;
   constexpr int CPR = WN / 8;
   typedef typename Cfg::Tc T16;
   static_assert(WN == 64 && 8 * CPR == kWave, "one 8-column chunk per lane per 8-row slab, 64-column partials");
@@ -203,9 +219,9 @@ __device__ __forceinline__ void store_tile_swiglu_bwd(const f32x16 (&acc)[Cfg::M
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) stage[(4 * half + rr) * LD + j * 32 + col_l] = acc[i][j][4 * q + rr];
+      for (int rr = 0; rr < 4; ++rr) stage_put(stage, 4 * half + rr, j * 32 + col_l, acc[i][j][4 * q + rr]);
     float v[8], g[8], u[8], dg[8], du[8];
-    Vec8<float>::load(stage + r * LD + c, v);
+    stage_get8(stage, r, c, v);
     unpack8<T16>(pg[S % PF], g);
     unpack8<T16>(pu[S % PF], u);
     const float ws = pw[S % PF];
