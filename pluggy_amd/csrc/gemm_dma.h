@@ -265,12 +265,18 @@ struct TDma {
   // 0-31 and tok1 for lanes 32-63 (the caller's wave-uniform tokens of its two
   // k-rows); k-rows at or past k_hi read zero. ld2: bytes per storage row. The
   // offset is a 32-bit buffer offset, so the row's byte offset is formed in 32
-  // bits (the same value the instruction takes from 64-bit arithmetic).
+  // bits (the same value the instruction takes from 64-bit arithmetic). Both
+  // k-rows' offsets and range checks are wave-uniform scalar work; a lane then
+  // picks its half's offset and adds its column with a saturating add, so an
+  // out-of-range row or column (kOOB) stays past every bound.
   template <int I>
   __device__ __forceinline__ void issue1_rows(const BufRsrc& rs, uint32_t tile, int k0, int k_hi, int tok0,
                                               int tok1, uint32_t ld2, int wave, int lane) const {
-    const uint32_t r0 = (uint32_t)tok0 * ld2, r1 = (uint32_t)tok1 * ld2;
-    const uint32_t v = k0 + kk[I] < k_hi ? (lane < 32 ? r0 : r1) + coloff[I] : kOOB;
+    static_assert(KPI == 2 && CPR == 32, "one k-row per half-wave");
+    const int kr = k0 + (wave + I * NW) * KPI;  // the half-waves' k-rows: kr, kr + 1
+    const uint32_t r0 = kr < k_hi ? (uint32_t)tok0 * ld2 : kOOB;
+    const uint32_t r1 = kr + 1 < k_hi ? (uint32_t)tok1 * ld2 : kOOB;
+    const uint32_t v = __builtin_elementwise_add_sat(lane < 32 ? r0 : r1, coloff[I]);
     dma16(rs, tile + (wave + I * NW) * 1024, v);
   }
 };
